@@ -1,0 +1,279 @@
+/*
+ * kessie_mi355x.h -- C ABI of libkessie_mi355x.so, the MI355X (gfx950) build of
+ * KeSSie's long-context attention hot path: fog attention (paged decode and
+ * chunked prefill), RoPE position remap of recalled K, and paged-KV
+ * insert / evict / compact / gather.
+ *
+ * Conventions (all entry points):
+ *   - Every pointer argument is a DEVICE pointer unless stated otherwise; the
+ *     caller owns all memory.  Nothing here allocates device memory.
+ *   - `stream` is a hipStream_t passed as void* (0 = the null stream).  Calls
+ *     are asynchronous on that stream; none of them synchronises the device.
+ *   - The `kessie_*` entry points return an int status (KESSIE_OK == 0) and
+ *     never print.  On failure, kessie_get_last_error() returns the message
+ *     (thread-local).  Argument errors are detected on the host before any
+ *     launch, so a failed call has launched nothing.
+ *   - The five `launch_kessie_*` entry points keep the reference's exact
+ *     signatures and `void` return; they record errors through the same
+ *     thread-local message instead of printing to stderr.
+ *   - Page layout ("native"): pool[num_pages][page_size][2 (K,V)][Hkv][D];
+ *     other layouts (e.g. vLLM's [2][blocks][P][Hkv][D]) are described by the
+ *     element strides page_stride / tok_stride / kv_stride / head_stride, with
+ *     the innermost (D) dimension contiguous.
+ */
+#ifndef KESSIE_MI355X_H
+#define KESSIE_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* The library is built with hidden visibility; these entry points are its
+ * only exports. */
+#if defined(__GNUC__) || defined(__clang__)
+#pragma GCC visibility push(default)
+#endif
+
+/* Element type codes. */
+#define KESSIE_DTYPE_F32 0
+#define KESSIE_DTYPE_BF16 1
+#define KESSIE_DTYPE_F16 2
+
+/* Status codes. */
+#define KESSIE_OK 0
+#define KESSIE_ERR_INVALID 1     /* bad argument (null pointer, size, stride) */
+#define KESSIE_ERR_UNSUPPORTED 2 /* valid but not implemented (dtype, shape)  */
+#define KESSIE_ERR_WORKSPACE 3   /* workspace missing or too small            */
+#define KESSIE_ERR_HIP 4         /* the HIP runtime reported an error         */
+
+/* Copies the calling thread's last error message (NUL-terminated, truncated
+ * to `cap` bytes) into host buffer `buf`; returns the last status code. */
+int kessie_get_last_error(char* buf, size_t cap);
+
+/* Library version as major*10000 + minor*100 + patch. */
+int kessie_version(void);
+
+/* =========================================================================
+ * Legacy entry points -- identical signatures to the reference launchers.
+ * ========================================================================= */
+
+/* Dense windowed attention, fp16 [B,H,N,D] Q/K/V/O, D in {64,128}.
+ * Semantics of the reference's torch math (kessie_hip_kernels.py:577-589):
+ * causal mask j<=i, window keeps 0<=i-j<W (W=0: full).
+ * Replaces kessie_kernels_v2.hip:716-751 (launch_kessie_windowed_attn). */
+void launch_kessie_windowed_attn(const void* Q, const void* K, const void* V,
+                                 void* O, float sm_scale, int batch_size,
+                                 int num_heads, int seq_len, int head_dim,
+                                 int window_size, int is_causal, void* stream);
+
+/* Dense attention with fog weights scaling V rows: O = softmax(QK^T s) (w.V),
+ * fog_weights fp32 [N] (kessie_hip_kernels.py:592-593).
+ * Replaces kessie_kernels_v2.hip:788-825 (launch_kessie_fused_fog_attn). */
+void launch_kessie_fused_fog_attn(const void* Q, const void* K, const void* V,
+                                  void* O, const void* fog_weights,
+                                  float sm_scale, int batch_size, int num_heads,
+                                  int seq_len, int head_dim, int window_size,
+                                  int is_causal, void* stream);
+
+/* Threshold eviction: valid[p]==1 && positions[p] < thr  ->  valid[p]=0 and
+ * *evict_count += 1 (caller zeroes the counter).  int8 valid, int32 positions.
+ * Replaces kessie_kernels_v2.hip:753-764 (launch_kessie_page_evict). */
+void launch_kessie_page_evict(void* page_valid, const void* page_positions,
+                              void* evict_count, int evict_before_pos,
+                              int num_pages, void* stream);
+
+/* Scatter new fp16 K/V [T,H,D] into the native fp16 pool at target pages
+ * (token t -> page target_page_ids[t/P], slot t%P); sets valid=1 and
+ * positions = conv_pos + t for each page's slot-0 token; page ids outside
+ * [0,max_pages) are skipped.
+ * Replaces kessie_kernels_v2.hip:766-782 (launch_kessie_page_insert). */
+void launch_kessie_page_insert(void* kv_cache, const void* new_keys,
+                               const void* new_values,
+                               const void* target_page_ids, void* page_valid,
+                               void* page_positions, int conv_pos,
+                               int num_tokens, int num_heads, int head_dim,
+                               int page_size, int max_pages, void* stream);
+
+/* In-place RoPE remap of fp16 K [T,H,2*half_dim] from orig to target
+ * positions (rotate-half pairs (d, d+half)).
+ * Replaces kessie_kernels_v2.hip:827-842 (launch_kessie_rope_remap). */
+void launch_kessie_rope_remap(void* k_data, const void* orig_positions,
+                              const void* target_positions, float rope_theta,
+                              int num_tokens, int num_heads, int half_dim,
+                              void* stream);
+
+/* =========================================================================
+ * Paged fog attention
+ * ========================================================================= */
+
+/* Bytes of workspace kessie_fog_decode_paged needs for these sizes (host
+ * call, no device work).  max_ctx is the largest ctx_lens[b]. */
+size_t kessie_fog_decode_workspace_bytes(int batch, int num_q_heads,
+                                         int num_kv_heads, int head_dim,
+                                         int max_ctx, int page_size, int dtype);
+
+/* Decode (one query token per sequence) over paged KV, GQA
+ * (q head h uses kv head h / (Hq/Hkv)).  Sequence b holds ctx_lens[b] tokens
+ * at positions 0..ctx-1; token t lives in page page_table[b*table_stride +
+ * t/page_size], slot t%page_size.  The query sits at position ctx-1.
+ *   scores  s_j = (q . k_j) * sm_scale [+ fog_bias[b*fog_bias_bstride + j]]
+ *   mask    j < ctx and (window == 0 or (ctx-1) - j < window)
+ *   output  o = sum_j softmax(s)_j * w_j * v_j,  w_j = fog_vscale[b*bstride+j]
+ *           (w == 1 when fog_vscale is NULL; the sum is not renormalised).
+ * q/out: [B][Hq][D] contiguous in `dtype`; pool elements in `dtype`;
+ * accumulation in fp32.  Page ids outside [0,num_pages) mask their tokens.
+ * A sequence with no visible key yields a zero output row.  The fog semantics follow kessie_hip_kernels.py:
+ * 577-593 (V mode) and kessie_attention.py:114-139 (bias mode).  The
+ * reference has no paged/GQA decode kernel; the GPU launcher it stands in
+ * for is kessie_kernels_v2.hip:788-825. */
+int kessie_fog_decode_paged(
+    const void* q, const void* kv_pool, int num_pages, int64_t page_stride,
+    int64_t tok_stride,
+    int64_t kv_stride, int64_t head_stride, const int32_t* page_table,
+    int64_t table_stride, const int32_t* ctx_lens, const float* fog_vscale,
+    int64_t fog_vscale_bstride, const float* fog_bias, int64_t fog_bias_bstride,
+    void* out, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+    int page_size, int max_ctx, int window, float sm_scale, int dtype,
+    void* workspace, size_t workspace_bytes, void* stream);
+
+/* Bytes of workspace kessie_fog_prefill_paged needs (host call). */
+size_t kessie_fog_prefill_workspace_bytes(int batch, int num_q_tokens,
+                                          int num_q_heads, int num_kv_heads,
+                                          int head_dim, int max_ctx,
+                                          int page_size, int dtype);
+
+/* Chunked prefill: C query tokens per sequence appended after L prior tokens
+ * (ctx_lens[b] = L + C counts them all; the chunk's K/V are already in the
+ * pool).  Query i (0<=i<C) sits at position q_pos = ctx-C+i and attends keys
+ * j <= q_pos (causal) with (window == 0 or q_pos - j < window), fog as in
+ * decode, fog index = key position.  q/out: [B][C][Hq][D] contiguous.  This
+ * equals the last C rows of the reference's dense math over ctx tokens
+ * (kessie_hip_kernels.py:577-593). */
+int kessie_fog_prefill_paged(
+    const void* q, const void* kv_pool, int num_pages, int64_t page_stride,
+    int64_t tok_stride,
+    int64_t kv_stride, int64_t head_stride, const int32_t* page_table,
+    int64_t table_stride, const int32_t* ctx_lens, const float* fog_vscale,
+    int64_t fog_vscale_bstride, const float* fog_bias, int64_t fog_bias_bstride,
+    void* out, int batch, int num_q_tokens, int num_q_heads, int num_kv_heads,
+    int head_dim, int page_size, int max_ctx, int window, float sm_scale,
+    int causal, int dtype, void* workspace, size_t workspace_bytes,
+    void* stream);
+
+/* =========================================================================
+ * RoPE position remap
+ * ========================================================================= */
+
+/* In-place remap of K from orig_pos[t] to tgt_pos[t] for T tokens.  Token t's
+ * K row is at  kv_pool + page*page_stride + (t%page_size)*tok_stride  with
+ * page = page_list[t/page_size]; page_list == NULL means dense rows
+ * (row t at t*tok_stride).  Heads at head_stride, D contiguous, D even.
+ * inv_freq: fp32 [D/2] device table (the caller builds it exactly as
+ * 1/(theta ** (arange(D/2)/(D/2))), kessie_hip_kernels.py:600).
+ * Angle = float(tgt-orig) * inv_freq[j] (one fp32 multiply); the rotation
+ * of pair (j, j+D/2) is computed in fp32 without fused multiply-add and
+ * rounded to `dtype` (kessie_hip_kernels.py:596-606).  Tokens whose page id
+ * lies outside [0,num_pages) are left untouched. */
+int kessie_rope_remap_paged(void* kv_pool, int64_t page_stride,
+                            int64_t tok_stride, int64_t head_stride,
+                            const int32_t* page_list, int num_pages,
+                            const int32_t* orig_pos, const int32_t* tgt_pos,
+                            const float* inv_freq, int num_tokens,
+                            int num_heads, int head_dim, int page_size,
+                            int dtype, void* stream);
+
+/* =========================================================================
+ * Paged-KV management
+ * ========================================================================= */
+
+/* Insert T recalled tokens' K/V ([T][H][D] each, contiguous, `dtype`) into
+ * the pool at target_pages (token t -> page target_pages[t/P], slot t%P);
+ * page ids outside [0,num_pages) are skipped; for every inserted page the
+ * slot-0 token sets page_valid=1, page_positions=conv_pos+t
+ * (kessie_kernels_v2.hip:414-456 addressing).  When orig_pos/tgt_pos/inv_freq
+ * are all non-NULL, K is RoPE-remapped on the way in (same arithmetic as
+ * kessie_rope_remap_paged); otherwise it is copied unchanged. */
+int kessie_page_insert_paged(void* kv_pool, int64_t page_stride,
+                             int64_t tok_stride, int64_t kv_stride,
+                             int64_t head_stride, const void* new_k,
+                             const void* new_v, const int32_t* target_pages,
+                             int8_t* page_valid, int32_t* page_positions,
+                             int conv_pos, const int32_t* orig_pos,
+                             const int32_t* tgt_pos, const float* inv_freq,
+                             int num_tokens, int num_heads, int head_dim,
+                             int page_size, int num_pages, int dtype,
+                             void* stream);
+
+/* Threshold eviction that also reports WHICH pages were freed, in ascending
+ * physical id order (the order KeSSiePagedKVCache.evict_before appends them to
+ * its free list, kessie_hip_kernels.py:526-540).  A page is freed when
+ * page_valid==1 && positions < thr, or, when `allocated` is non-NULL, when it
+ * is allocated (allocated[p]!=0) but not valid; freed pages get
+ * page_valid=0 and allocated=0.  Writes the ids to freed_list[0..n) and n to
+ * *freed_count.  Workspace: kessie_page_workspace_bytes(num_pages). */
+int kessie_page_evict_list(int8_t* page_valid, const int32_t* page_positions,
+                           int8_t* allocated, int evict_before_pos,
+                           int num_pages, int32_t* freed_list,
+                           int32_t* freed_count, void* workspace,
+                           size_t workspace_bytes, void* stream);
+
+/* Bytes of workspace the page-management calls need for num_pages (host). */
+size_t kessie_page_workspace_bytes(int num_pages);
+
+/* Score eviction: among pages with page_valid==1, evict the k with the
+ * smallest keys (score[p], p) under the total order score ascending, then
+ * page id ascending (scores compared as IEEE floats, -0 == +0, NaN not
+ * allowed).  k = k_evict when k_evict >= 0 (clamped to the valid count),
+ * else floor(evict_fraction * n_valid) computed in double.  Evicted pages get
+ * page_valid=0; their ids go to evict_list ascending; k to *evict_count.
+ * Deterministic: no order depends on atomics.  (The reference only has the
+ * threshold predicate, kessie_kernels_v2.hip:393-407; this applies it with an
+ * exact k-th-order-statistic threshold.) */
+int kessie_page_select_evict(const float* scores, int8_t* page_valid,
+                             int num_pages, int k_evict, float evict_fraction,
+                             int32_t* evict_list, int32_t* evict_count,
+                             void* workspace, size_t workspace_bytes,
+                             void* stream);
+
+/* Compaction of S page tables [S][table_stride] with lens[s] used entries:
+ * survivors (page_valid[id]==1) keep their logical order; new_tables[s][0..n)
+ * holds them, entries [n, table_stride) are set to -1, new_lens[s]=n.
+ * gather_idx receives all survivors in (sequence, logical) order and
+ * *gather_count their number.  Entries outside [0,num_pages) count as not
+ * surviving.  Workspace: kessie_page_workspace_bytes(S*table_stride). */
+int kessie_page_compact(const int32_t* tables, const int32_t* lens,
+                        const int8_t* page_valid, int32_t* new_tables,
+                        int32_t* new_lens, int32_t* gather_idx,
+                        int32_t* gather_count, int num_seqs, int table_stride,
+                        int num_pages, void* workspace, size_t workspace_bytes,
+                        void* stream);
+
+/* Ids of valid pages in ascending physical order (the order of the
+ * reference's get_layer_kv, kessie_hip_kernels.py:558-564) into out_idx,
+ * their number into *out_count. */
+int kessie_page_valid_list(const int8_t* page_valid, int num_pages,
+                           int32_t* out_idx, int32_t* out_count,
+                           void* workspace, size_t workspace_bytes,
+                           void* stream);
+
+/* Byte copy of whole pages: dst[i] = src_pool[idx[i]] for i < n, each page
+ * `page_bytes` long (multiple of 16, 16-byte aligned pointers).  When
+ * count_dev is non-NULL the number of pages copied is min(n, *count_dev)
+ * read on the device (n is then the capacity of dst and idx).  Pages whose
+ * id lies outside [0,num_pages) are skipped (dst[i] is left untouched). */
+int kessie_page_gather(const void* src_pool, int64_t page_bytes,
+                       const int32_t* idx, const int32_t* count_dev, int n,
+                       int num_pages, void* dst, void* stream);
+
+#if defined(__GNUC__) || defined(__clang__)
+#pragma GCC visibility pop
+#endif
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KESSIE_MI355X_H */

@@ -1,0 +1,756 @@
+// Paged-KV management for gfx950: insert (optionally RoPE-remapping K),
+// threshold eviction, score eviction, page-table compaction, valid-page lists
+// and the page gather.
+//
+// Reference semantics:
+//   threshold evict  valid==1 && pos < thr -> valid=0     (kessie_kernels_v2.hip:393-407)
+//   insert           page = target[t/P], slot t%P; ids outside [0,pages)
+//                    skipped; slot-0 token sets valid/position
+//                                                          (kessie_kernels_v2.hip:414-456)
+//   free-list order  evicted ids appended ascending        (kessie_hip_kernels.py:534-538)
+//   gather order     valid ids ascending                   (kessie_hip_kernels.py:558-564)
+// Every list this file produces is ordered by a prefix sum, never by atomics:
+// count per block -> exclusive scan of the block counts -> each block writes
+// its survivors at its offset in element order.  Atomics appear only in
+// counters whose value does not depend on order (histograms, the legacy
+// evict count).
+#include <climits>
+
+#include "common.h"
+
+namespace kessie {
+namespace pages {
+
+constexpr int kThreads = 256;
+constexpr int kItems = 8;                      // consecutive elements per thread
+constexpr int kChunk = kThreads * kItems;      // elements per block in compaction
+constexpr int kWaves = kThreads / 64;
+
+// Exclusive scan of one int per thread across a 256-thread block.  `sm` needs
+// kWaves + 1 ints.  Returns the thread's exclusive prefix; *total = block sum.
+__device__ __forceinline__ int block_exclusive_scan(int v, int* total, int* sm) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) sm[wave] = x;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int s = 0;
+    for (int w = 0; w < kWaves; ++w) {
+      const int t = sm[w];
+      sm[w] = s;
+      s += t;
+    }
+    sm[kWaves] = s;
+  }
+  __syncthreads();
+  const int res = x - v + sm[wave];
+  *total = sm[kWaves];
+  __syncthreads();
+  return res;
+}
+
+// ---------------------------------------------------------------------------
+// Predicates for ordered compaction over page ids
+// ---------------------------------------------------------------------------
+enum PredKind : int {
+  kPredValid = 0,      // valid[i] == 1
+  kPredFreed = 1,      // (valid==1 && pos<thr) || (allocated && allocated[i] && valid!=1)
+  kPredScoreEvict = 2  // valid==1 && key(i) <= threshold key (threshold in workspace)
+};
+
+struct PredArgs {
+  int kind;
+  const int8_t* valid;
+  const int32_t* positions;
+  const int8_t* allocated;
+  int thr;
+  const float* scores;
+  const unsigned long long* key_thr;  // device, for kPredScoreEvict
+  const int* k_dev;                   // device: number to evict (0 -> none)
+};
+
+__device__ __forceinline__ unsigned long long score_key(float s, int id) {
+  if (s == 0.0f) s = 0.0f;  // -0 == +0
+  const uint32_t bits = __float_as_uint(s);
+  const uint32_t ord = (bits & 0x80000000u) ? ~bits : (bits | 0x80000000u);
+  return ((unsigned long long)ord << 32) | (uint32_t)id;
+}
+
+__device__ __forceinline__ bool pred_eval(const PredArgs& a, int i) {
+  switch (a.kind) {
+    case kPredValid:
+      return a.valid[i] == 1;
+    case kPredFreed: {
+      const bool v = a.valid[i] == 1;
+      if (v && a.positions[i] < a.thr) return true;
+      return a.allocated != nullptr && a.allocated[i] != 0 && !v;
+    }
+    case kPredScoreEvict:
+      return a.valid[i] == 1 && *a.k_dev > 0 && score_key(a.scores[i], i) <= *a.key_thr;
+  }
+  return false;
+}
+
+__global__ __launch_bounds__(kThreads) void compact_count_kernel(PredArgs a, int n, int* block_counts) {
+  __shared__ int sm[kWaves + 1];
+  const int base = blockIdx.x * kChunk + threadIdx.x * kItems;
+  int c = 0;
+#pragma unroll
+  for (int e = 0; e < kItems; ++e) {
+    const int i = base + e;
+    if (i < n && pred_eval(a, i)) ++c;
+  }
+  int total;
+  block_exclusive_scan(c, &total, sm);
+  if (threadIdx.x == 0) block_counts[blockIdx.x] = total;
+}
+
+// Exclusive scan of `n` ints by one 256-thread block (any n), total to *total.
+__global__ __launch_bounds__(kThreads) void scan_counts_kernel(const int* counts, int n, int* offsets, int* total) {
+  __shared__ int sm[kWaves + 1];
+  int carry = 0;
+  for (int base = 0; base < n; base += kThreads) {
+    const int i = base + threadIdx.x;
+    const int v = i < n ? counts[i] : 0;
+    int tot;
+    const int ex = block_exclusive_scan(v, &tot, sm);
+    if (i < n) offsets[i] = carry + ex;
+    carry += tot;
+  }
+  if (threadIdx.x == 0 && total) *total = carry;
+}
+
+__global__ __launch_bounds__(kThreads) void compact_write_kernel(PredArgs a, int n, const int* block_offsets,
+                                                                 int32_t* out) {
+  __shared__ int sm[kWaves + 1];
+  const int base = blockIdx.x * kChunk + threadIdx.x * kItems;
+  unsigned flags = 0;
+  int c = 0;
+#pragma unroll
+  for (int e = 0; e < kItems; ++e) {
+    const int i = base + e;
+    if (i < n && pred_eval(a, i)) {
+      flags |= 1u << e;
+      ++c;
+    }
+  }
+  int total;
+  int pos = block_exclusive_scan(c, &total, sm) + block_offsets[blockIdx.x];
+#pragma unroll
+  for (int e = 0; e < kItems; ++e)
+    if (flags & (1u << e)) out[pos++] = base + e;
+}
+
+// Marks the listed pages: valid=0 (and allocated=0 when given).
+__global__ __launch_bounds__(kThreads) void mark_evicted_kernel(const int32_t* list, const int32_t* count,
+                                                                int8_t* valid, int8_t* allocated, int num_pages) {
+  const int n = *count;
+  for (int i = blockIdx.x * kThreads + threadIdx.x; i < n; i += gridDim.x * kThreads) {
+    const int id = list[i];
+    if (id < 0 || id >= num_pages) continue;
+    valid[id] = 0;
+    if (allocated) allocated[id] = 0;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Radix select (one workgroup): the key of rank k-1 among valid pages.
+// ---------------------------------------------------------------------------
+constexpr int kSelThreads = 1024;
+constexpr int kSelWaves = kSelThreads / 64;
+
+struct SelectOut {
+  unsigned long long key_thr;  // largest evicted key
+  int k;                       // number evicted
+  int n_valid;
+};
+
+__global__ __launch_bounds__(kSelThreads) void radix_select_kernel(const float* scores, const int8_t* valid,
+                                                                   int n, int k_evict, float evict_fraction,
+                                                                   SelectOut* out) {
+  __shared__ int hist[kSelWaves][256];
+  __shared__ int tot[256];
+  __shared__ int s_digit, s_rank;
+  __shared__ int s_nvalid;
+  const int tid = threadIdx.x, wave = tid >> 6;
+
+  // Count valid pages.
+  if (tid == 0) s_nvalid = 0;
+  __syncthreads();
+  int c = 0;
+  for (int i = tid; i < n; i += kSelThreads) c += valid[i] == 1;
+  for (int o = 32; o >= 1; o >>= 1) c += __shfl_xor(c, o, 64);
+  if ((tid & 63) == 0) atomicAdd(&s_nvalid, c);
+  __syncthreads();
+  const int n_valid = s_nvalid;
+  long long k;
+  if (k_evict >= 0) {
+    k = min(k_evict, n_valid);
+  } else {
+    k = (long long)floor((double)evict_fraction * (double)n_valid);
+    if (k < 0) k = 0;
+    if (k > n_valid) k = n_valid;
+  }
+  if (k == 0) {
+    if (tid == 0) {
+      out->key_thr = 0;
+      out->k = 0;
+      out->n_valid = n_valid;
+    }
+    return;
+  }
+  unsigned long long prefix = 0;  // digits resolved so far (high bits)
+  int rank = (int)k - 1;          // rank of the wanted key among candidates
+  for (int pass = 0; pass < 8; ++pass) {
+    const int shift = 56 - 8 * pass;
+    for (int e = tid; e < kSelWaves * 256; e += kSelThreads) (&hist[0][0])[e] = 0;
+    __syncthreads();
+    for (int i = tid; i < n; i += kSelThreads) {
+      if (valid[i] != 1) continue;
+      const unsigned long long key = score_key(scores[i], i);
+      const bool match = (pass == 0) || ((key >> (shift + 8)) == prefix);
+      if (match) atomicAdd(&hist[wave][(key >> shift) & 255], 1);
+    }
+    __syncthreads();
+    if (tid < 256) {
+      int s = 0;
+      for (int w = 0; w < kSelWaves; ++w) s += hist[w][tid];
+      tot[tid] = s;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      int cum = 0, d = 0;
+      for (; d < 256; ++d) {
+        if (cum + tot[d] > rank) break;
+        cum += tot[d];
+      }
+      s_digit = d;
+      s_rank = rank - cum;
+    }
+    __syncthreads();
+    prefix = (prefix << 8) | (unsigned long long)s_digit;
+    rank = s_rank;
+    __syncthreads();
+  }
+  if (tid == 0) {
+    out->key_thr = prefix;
+    out->k = (int)k;
+    out->n_valid = n_valid;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Table compaction
+// ---------------------------------------------------------------------------
+// One block per table row: survivors keep logical order; the rest of the row
+// is filled with -1; new_lens[row] = survivors.
+__global__ __launch_bounds__(kThreads) void compact_rows_kernel(const int32_t* tables, const int32_t* lens,
+                                                                const int8_t* valid, int32_t* new_tables,
+                                                                int32_t* new_lens, int table_stride, int num_pages) {
+  __shared__ int sm[kWaves + 1];
+  const int row = blockIdx.x;
+  const int32_t* in = tables + (int64_t)row * table_stride;
+  int32_t* outr = new_tables + (int64_t)row * table_stride;
+  const int len = min(max(lens[row], 0), table_stride);
+  int carry = 0;
+  for (int base = 0; base < table_stride; base += kChunk) {
+    const int first = base + threadIdx.x * kItems;
+    unsigned flags = 0;
+    int ids[kItems];
+    int c = 0;
+#pragma unroll
+    for (int e = 0; e < kItems; ++e) {
+      const int j = first + e;
+      ids[e] = -1;
+      if (j < len) {
+        const int id = in[j];
+        ids[e] = id;
+        if (id >= 0 && id < num_pages && valid[id] == 1) {
+          flags |= 1u << e;
+          ++c;
+        }
+      }
+    }
+    int total;
+    int pos = carry + block_exclusive_scan(c, &total, sm);
+#pragma unroll
+    for (int e = 0; e < kItems; ++e)
+      if (flags & (1u << e)) outr[pos++] = ids[e];
+    carry += total;
+  }
+  __syncthreads();
+  for (int j = carry + threadIdx.x; j < table_stride; j += kThreads) outr[j] = -1;
+  if (threadIdx.x == 0) new_lens[row] = carry;
+}
+
+// gather_idx[row_off[row] + j] = new_tables[row][j], j < new_lens[row].
+__global__ __launch_bounds__(kThreads) void flatten_rows_kernel(const int32_t* new_tables, const int32_t* new_lens,
+                                                                const int* row_off, int table_stride,
+                                                                int32_t* gather_idx) {
+  const int row = blockIdx.x;
+  const int n = new_lens[row];
+  const int off = row_off[row];
+  for (int j = threadIdx.x; j < n; j += kThreads) gather_idx[off + j] = new_tables[(int64_t)row * table_stride + j];
+}
+
+// ---------------------------------------------------------------------------
+// Threshold evict (reference launcher semantics)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void threshold_evict_kernel(int8_t* valid, const int32_t* positions,
+                                                                   int32_t* count, int thr, int n) {
+  const int i = blockIdx.x * kThreads + threadIdx.x;
+  int hit = 0;
+  if (i < n && valid[i] == 1 && positions[i] < thr) {
+    valid[i] = 0;
+    hit = 1;
+  }
+  // One atomic per wave; the count does not depend on order.
+  for (int o = 32; o >= 1; o >>= 1) hit += __shfl_xor(hit, o, 64);
+  if ((threadIdx.x & 63) == 0 && hit) atomicAdd(count, hit);
+}
+
+// ---------------------------------------------------------------------------
+// Gather: whole-page byte copies, 16 bytes per lane.
+// ---------------------------------------------------------------------------
+constexpr int kGatherThreads = 256;
+constexpr int kGatherUnroll = 4;
+
+__global__ __launch_bounds__(kGatherThreads) void gather_kernel(const u32x4* __restrict__ src, int64_t page_vecs,
+                                                                const int32_t* __restrict__ idx,
+                                                                const int32_t* __restrict__ count_dev, int n,
+                                                                int num_pages, u32x4* __restrict__ dst) {
+  const int cnt = count_dev ? min(n, *count_dev) : n;
+  const int64_t step = (int64_t)kGatherThreads * kGatherUnroll;
+  for (int i = blockIdx.x; i < cnt; i += gridDim.x) {
+    const int pid = idx[i];
+    if (pid < 0 || pid >= num_pages) continue;
+    const u32x4* s = src + (int64_t)pid * page_vecs;
+    u32x4* d = dst + (int64_t)i * page_vecs;
+    for (int64_t v0 = threadIdx.x; v0 < page_vecs; v0 += step) {
+      u32x4 r[kGatherUnroll];
+#pragma unroll
+      for (int u = 0; u < kGatherUnroll; ++u) {
+        const int64_t v = v0 + (int64_t)u * kGatherThreads;
+        if (v < page_vecs) r[u] = __builtin_nontemporal_load(s + v);
+      }
+#pragma unroll
+      for (int u = 0; u < kGatherUnroll; ++u) {
+        const int64_t v = v0 + (int64_t)u * kGatherThreads;
+        if (v < page_vecs) __builtin_nontemporal_store(r[u], d + v);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Insert (optionally remapping K)
+// ---------------------------------------------------------------------------
+constexpr int kInsTile = 16;  // tokens per workgroup
+constexpr int kInsMaxHalf = 128;
+
+template <typename T>
+struct Vec16;
+template <>
+struct Vec16<bf16_t> {
+  static constexpr int N = 8;
+  typedef bf16x8 type;
+};
+template <>
+struct Vec16<f16_t> {
+  static constexpr int N = 8;
+  typedef f16x8 type;
+};
+template <>
+struct Vec16<float> {
+  static constexpr int N = 4;
+  typedef f32x4 type;
+};
+
+struct InsertArgs {
+  void* pool;
+  int64_t page_stride, tok_stride, kv_stride, head_stride;
+  const void* new_k;
+  const void* new_v;
+  const int32_t* target_pages;
+  int8_t* valid;
+  int32_t* positions;
+  int conv_pos;
+  const int32_t* orig_pos;
+  const int32_t* tgt_pos;
+  const float* inv_freq;
+  int T, H, D, page_size, num_pages;
+};
+
+// Element-wise insert, any layout/alignment: one thread per (token, head, d)
+// for V and for K pairs.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void insert_scalar_kernel(InsertArgs a) {
+#pragma clang fp contract(off)
+  const int half = a.D / 2;
+  const bool remap = a.inv_freq != nullptr;
+  const int64_t gid = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  const int64_t total = (int64_t)a.T * a.H * a.D;
+  if (gid >= total) return;
+  const int d = (int)(gid % a.D);
+  const int64_t rem = gid / a.D;
+  const int h = (int)(rem % a.H);
+  const int t = (int)(rem / a.H);
+  const int phys = a.target_pages[t / a.page_size];
+  if (phys < 0 || phys >= a.num_pages) return;
+  T* pool = static_cast<T*>(a.pool);
+  const T* nk = static_cast<const T*>(a.new_k);
+  const T* nv = static_cast<const T*>(a.new_v);
+  const int64_t dst = (int64_t)phys * a.page_stride + (int64_t)(t % a.page_size) * a.tok_stride +
+                      (int64_t)h * a.head_stride;
+  const int64_t src = ((int64_t)t * a.H + h) * a.D;
+  pool[dst + a.kv_stride + d] = nv[src + d];
+  if (!remap) {
+    pool[dst + d] = nk[src + d];
+  } else if (d < half) {
+    const float delta = (float)(a.tgt_pos[t] - a.orig_pos[t]);
+    const float ang = delta * a.inv_freq[d];
+    float s, c;
+    sincosf(ang, &s, &c);
+    const float x1 = to_f32(nk[src + d]);
+    const float x2 = to_f32(nk[src + d + half]);
+    const float u1 = x1 * c;
+    const float u2 = x2 * s;
+    const float w1 = x1 * s;
+    const float w2 = x2 * c;
+    pool[dst + d] = from_f32<T>(u1 - u2);
+    pool[dst + d + half] = from_f32<T>(w1 + w2);
+  }
+  if (t % a.page_size == 0 && h == 0 && d == 0) {
+    a.valid[phys] = 1;
+    a.positions[phys] = a.conv_pos + t;
+  }
+}
+
+// Vectorised insert: 16-byte chunks; per tile of tokens, cos/sin in LDS.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void insert_vec_kernel(InsertArgs a) {
+#pragma clang fp contract(off)
+  typedef typename Vec16<T>::type V;
+  constexpr int N = Vec16<T>::N;
+  __shared__ float2 cs[kInsTile * kInsMaxHalf];
+  const int half = a.D / 2;
+  const bool remap = a.inv_freq != nullptr;
+  const int t0 = blockIdx.x * kInsTile;
+  const int ntok = min(kInsTile, a.T - t0);
+  if (remap) {
+    for (int i = threadIdx.x; i < ntok * half; i += kThreads) {
+      const int tt = i / half, j = i - tt * half;
+      const int t = t0 + tt;
+      const float delta = (float)(a.tgt_pos[t] - a.orig_pos[t]);
+      const float ang = delta * a.inv_freq[j];
+      float s, c;
+      sincosf(ang, &s, &c);
+      cs[i] = make_float2(c, s);
+    }
+    __syncthreads();
+  }
+  T* pool = static_cast<T*>(a.pool);
+  const T* nk = static_cast<const T*>(a.new_k);
+  const T* nv = static_cast<const T*>(a.new_v);
+  const int chunks = half / N;             // chunk pairs per head
+  const int per_tok = a.H * chunks;
+  for (int i = threadIdx.x; i < ntok * per_tok; i += kThreads) {
+    const int tt = i / per_tok;
+    const int r = i - tt * per_tok;
+    const int h = r / chunks, c = r - h * chunks;
+    const int t = t0 + tt;
+    const int phys = a.target_pages[t / a.page_size];
+    if (phys < 0 || phys >= a.num_pages) continue;
+    const int64_t dst = (int64_t)phys * a.page_stride + (int64_t)(t % a.page_size) * a.tok_stride +
+                        (int64_t)h * a.head_stride + c * N;
+    const int64_t src = ((int64_t)t * a.H + h) * a.D + c * N;
+    const V k1 = *reinterpret_cast<const V*>(nk + src);
+    const V k2 = *reinterpret_cast<const V*>(nk + src + half);
+    const V v1 = *reinterpret_cast<const V*>(nv + src);
+    const V v2 = *reinterpret_cast<const V*>(nv + src + half);
+    V y1 = k1, y2 = k2;
+    if (remap) {
+      const float2* csr = cs + tt * half + c * N;
+#pragma unroll
+      for (int e = 0; e < N; ++e) {
+        const float2 q = csr[e];
+        const float x1 = to_f32(k1[e]);
+        const float x2 = to_f32(k2[e]);
+        const float u1 = x1 * q.x;
+        const float u2 = x2 * q.y;
+        const float w1 = x1 * q.y;
+        const float w2 = x2 * q.x;
+        y1[e] = from_f32<T>(u1 - u2);
+        y2[e] = from_f32<T>(w1 + w2);
+      }
+    }
+    *reinterpret_cast<V*>(pool + dst) = y1;
+    *reinterpret_cast<V*>(pool + dst + half) = y2;
+    *reinterpret_cast<V*>(pool + dst + a.kv_stride) = v1;
+    *reinterpret_cast<V*>(pool + dst + a.kv_stride + half) = v2;
+    if (t % a.page_size == 0 && h == 0 && c == 0) {
+      a.valid[phys] = 1;
+      a.positions[phys] = a.conv_pos + t;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host helpers
+// ---------------------------------------------------------------------------
+int num_blocks(int n) { return div_up(max(n, 1), kChunk); }
+
+struct Workspace {
+  SelectOut* sel;
+  int* counts;
+  int* offsets;
+  int* rows;  // per-row offsets (table compaction)
+};
+
+size_t workspace_bytes(int n) {
+  const size_t nb = (size_t)num_blocks(n);
+  size_t b = 256;                                   // SelectOut + misc
+  b += (nb * sizeof(int) + 255) / 256 * 256;        // counts
+  b += (nb * sizeof(int) + 255) / 256 * 256;        // offsets
+  b += (((size_t)n + 1) * sizeof(int) + 255) / 256 * 256;  // row offsets
+  return b;
+}
+
+Workspace carve(void* ws, int n) {
+  Workspace w;
+  char* c = static_cast<char*>(ws);
+  const size_t nb = (size_t)num_blocks(n);
+  w.sel = reinterpret_cast<SelectOut*>(c);
+  c += 256;
+  w.counts = reinterpret_cast<int*>(c);
+  c += (nb * sizeof(int) + 255) / 256 * 256;
+  w.offsets = reinterpret_cast<int*>(c);
+  c += (nb * sizeof(int) + 255) / 256 * 256;
+  w.rows = reinterpret_cast<int*>(c);
+  return w;
+}
+
+// Ordered compaction of page ids satisfying `a` into out[], count to *count.
+int ordered_compact(const PredArgs& a, int n, int32_t* out, int32_t* count, Workspace& w, hipStream_t s) {
+  const int nb = num_blocks(n);
+  hipLaunchKernelGGL(compact_count_kernel, dim3(nb), dim3(kThreads), 0, s, a, n, w.counts);
+  hipLaunchKernelGGL(scan_counts_kernel, dim3(1), dim3(kThreads), 0, s, w.counts, nb, w.offsets, count);
+  hipLaunchKernelGGL(compact_write_kernel, dim3(nb), dim3(kThreads), 0, s, a, n, w.offsets, out);
+  return check_launch("ordered compaction");
+}
+
+int check_ws(void* ws, size_t bytes, int n, const char* what) {
+  const size_t need = workspace_bytes(n);
+  KESSIE_REQUIRE(ws != nullptr && bytes >= need, KESSIE_ERR_WORKSPACE, "%s: workspace of %zu bytes needed, got %zu",
+                 what, need, bytes);
+  KESSIE_REQUIRE(aligned16(ws), KESSIE_ERR_INVALID, "%s: workspace not 16-byte aligned", what);
+  return KESSIE_OK;
+}
+
+template <typename T>
+int launch_insert(InsertArgs& a, hipStream_t s) {
+  constexpr int N = Vec16<T>::N;
+  const int half = a.D / 2;
+  const bool vec_ok = (a.D % 2 == 0) && (half % N == 0) && (half <= kInsMaxHalf) && aligned16(a.pool) &&
+                      aligned16(a.new_k) && aligned16(a.new_v) && a.page_stride % N == 0 &&
+                      a.tok_stride % N == 0 && a.head_stride % N == 0 && a.kv_stride % N == 0;
+  if (vec_ok) {
+    hipLaunchKernelGGL(insert_vec_kernel<T>, dim3(div_up(a.T, kInsTile)), dim3(kThreads), 0, s, a);
+  } else {
+    const int64_t total = (int64_t)a.T * a.H * a.D;
+    const int64_t grid = (total + kThreads - 1) / kThreads;
+    KESSIE_REQUIRE(grid <= 0x7fffffff, KESSIE_ERR_UNSUPPORTED, "page insert: %lld elements exceed one launch",
+                   (long long)total);
+    hipLaunchKernelGGL(insert_scalar_kernel<T>, dim3((unsigned)grid), dim3(kThreads), 0, s, a);
+  }
+  return check_launch("page insert");
+}
+
+int insert_dispatch(InsertArgs& a, int dtype, hipStream_t s) {
+  KESSIE_REQUIRE(a.T >= 0 && a.H > 0 && a.D > 0 && a.page_size > 0 && a.num_pages >= 0, KESSIE_ERR_INVALID,
+                 "page insert: bad sizes T=%d H=%d D=%d P=%d pages=%d", a.T, a.H, a.D, a.page_size, a.num_pages);
+  if (a.T == 0 || a.num_pages == 0) return KESSIE_OK;
+  KESSIE_REQUIRE(a.pool && a.new_k && a.new_v && a.target_pages && a.valid && a.positions, KESSIE_ERR_INVALID,
+                 "page insert: null pointer");
+  const bool any = a.orig_pos || a.tgt_pos || a.inv_freq;
+  const bool all = a.orig_pos && a.tgt_pos && a.inv_freq;
+  KESSIE_REQUIRE(!any || all, KESSIE_ERR_INVALID, "page insert: orig_pos, tgt_pos and inv_freq go together");
+  KESSIE_REQUIRE(!all || a.D % 2 == 0, KESSIE_ERR_INVALID, "page insert: remap needs an even head_dim");
+  KESSIE_REQUIRE(a.head_stride >= a.D && a.tok_stride >= (int64_t)a.H * a.head_stride, KESSIE_ERR_INVALID,
+                 "page insert: strides overlap");
+  switch (dtype) {
+    case KESSIE_DTYPE_BF16: return launch_insert<bf16_t>(a, s);
+    case KESSIE_DTYPE_F16: return launch_insert<f16_t>(a, s);
+    case KESSIE_DTYPE_F32: return launch_insert<float>(a, s);
+  }
+  set_error(KESSIE_ERR_UNSUPPORTED, "page insert: dtype %d", dtype);
+  return KESSIE_ERR_UNSUPPORTED;
+}
+
+}  // namespace pages
+}  // namespace kessie
+
+using namespace kessie;
+using namespace kessie::pages;
+
+extern "C" size_t kessie_page_workspace_bytes(int num_pages) { return pages::workspace_bytes(max(num_pages, 0)); }
+
+extern "C" int kessie_page_insert_paged(void* kv_pool, int64_t page_stride, int64_t tok_stride, int64_t kv_stride,
+                                        int64_t head_stride, const void* new_k, const void* new_v,
+                                        const int32_t* target_pages, int8_t* page_valid, int32_t* page_positions,
+                                        int conv_pos, const int32_t* orig_pos, const int32_t* tgt_pos,
+                                        const float* inv_freq, int num_tokens, int num_heads, int head_dim,
+                                        int page_size, int num_pages, int dtype, void* stream) {
+  clear_error();
+  InsertArgs a{kv_pool,  page_stride,    tok_stride, kv_stride, head_stride, new_k,     new_v,
+               target_pages, page_valid, page_positions, conv_pos, orig_pos, tgt_pos, inv_freq,
+               num_tokens, num_heads,     head_dim,   page_size, num_pages};
+  return insert_dispatch(a, dtype, as_stream(stream));
+}
+
+extern "C" int kessie_page_evict_list(int8_t* page_valid, const int32_t* page_positions, int8_t* allocated,
+                                      int evict_before_pos, int num_pages, int32_t* freed_list, int32_t* freed_count,
+                                      void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  KESSIE_REQUIRE(num_pages >= 0, KESSIE_ERR_INVALID, "page evict: num_pages %d", num_pages);
+  KESSIE_REQUIRE(page_valid && page_positions && freed_list && freed_count, KESSIE_ERR_INVALID,
+                 "page evict: null pointer");
+  int st = check_ws(workspace, workspace_bytes, num_pages, "page evict");
+  if (st) return st;
+  hipStream_t s = as_stream(stream);
+  Workspace w = carve(workspace, num_pages);
+  PredArgs a{kPredFreed, page_valid, page_positions, allocated, evict_before_pos, nullptr, nullptr, nullptr};
+  st = ordered_compact(a, num_pages, freed_list, freed_count, w, s);
+  if (st) return st;
+  hipLaunchKernelGGL(mark_evicted_kernel, dim3(max(1, min(1024, div_up(num_pages, kThreads)))), dim3(kThreads), 0,
+                     s, freed_list, freed_count, page_valid, allocated, num_pages);
+  return check_launch("page evict (mark)");
+}
+
+extern "C" int kessie_page_select_evict(const float* scores, int8_t* page_valid, int num_pages, int k_evict,
+                                        float evict_fraction, int32_t* evict_list, int32_t* evict_count,
+                                        void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  KESSIE_REQUIRE(num_pages >= 0, KESSIE_ERR_INVALID, "select evict: num_pages %d", num_pages);
+  KESSIE_REQUIRE(scores && page_valid && evict_list && evict_count, KESSIE_ERR_INVALID, "select evict: null pointer");
+  KESSIE_REQUIRE(k_evict >= 0 || (evict_fraction >= 0.0f && evict_fraction <= 1.0f), KESSIE_ERR_INVALID,
+                 "select evict: evict_fraction %g outside [0,1]", (double)evict_fraction);
+  int st = check_ws(workspace, workspace_bytes, num_pages, "select evict");
+  if (st) return st;
+  hipStream_t s = as_stream(stream);
+  Workspace w = carve(workspace, num_pages);
+  hipLaunchKernelGGL(radix_select_kernel, dim3(1), dim3(kSelThreads), 0, s, scores, page_valid, num_pages, k_evict,
+                     evict_fraction, w.sel);
+  st = check_launch("select evict (radix select)");
+  if (st) return st;
+  PredArgs a{kPredScoreEvict, page_valid, nullptr, nullptr, 0, scores, &w.sel->key_thr, &w.sel->k};
+  st = ordered_compact(a, num_pages, evict_list, evict_count, w, s);
+  if (st) return st;
+  hipLaunchKernelGGL(mark_evicted_kernel, dim3(max(1, min(1024, div_up(num_pages, kThreads)))), dim3(kThreads), 0,
+                     s, evict_list, evict_count, page_valid, static_cast<int8_t*>(nullptr), num_pages);
+  return check_launch("select evict (mark)");
+}
+
+extern "C" int kessie_page_compact(const int32_t* tables, const int32_t* lens, const int8_t* page_valid,
+                                   int32_t* new_tables, int32_t* new_lens, int32_t* gather_idx, int32_t* gather_count,
+                                   int num_seqs, int table_stride, int num_pages, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
+  clear_error();
+  KESSIE_REQUIRE(num_seqs >= 0 && table_stride >= 0 && num_pages >= 0, KESSIE_ERR_INVALID,
+                 "page compact: bad sizes S=%d W=%d pages=%d", num_seqs, table_stride, num_pages);
+  KESSIE_REQUIRE((int64_t)num_seqs * table_stride <= INT_MAX, KESSIE_ERR_UNSUPPORTED, "page compact: table too big");
+  if (num_seqs == 0) return KESSIE_OK;
+  KESSIE_REQUIRE(tables && lens && page_valid && new_tables && new_lens && gather_idx && gather_count,
+                 KESSIE_ERR_INVALID, "page compact: null pointer");
+  KESSIE_REQUIRE(tables != new_tables, KESSIE_ERR_INVALID, "page compact: tables and new_tables must differ");
+  const int n = num_seqs * table_stride;
+  int st = check_ws(workspace, workspace_bytes, max(n, num_seqs), "page compact");
+  if (st) return st;
+  hipStream_t s = as_stream(stream);
+  Workspace w = carve(workspace, max(n, num_seqs));
+  hipLaunchKernelGGL(compact_rows_kernel, dim3(num_seqs), dim3(kThreads), 0, s, tables, lens, page_valid, new_tables,
+                     new_lens, table_stride, num_pages);
+  hipLaunchKernelGGL(scan_counts_kernel, dim3(1), dim3(kThreads), 0, s, new_lens, num_seqs, w.rows, gather_count);
+  hipLaunchKernelGGL(flatten_rows_kernel, dim3(num_seqs), dim3(kThreads), 0, s, new_tables, new_lens, w.rows,
+                     table_stride, gather_idx);
+  return check_launch("page compact");
+}
+
+extern "C" int kessie_page_valid_list(const int8_t* page_valid, int num_pages, int32_t* out_idx, int32_t* out_count,
+                                      void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  KESSIE_REQUIRE(num_pages >= 0, KESSIE_ERR_INVALID, "valid list: num_pages %d", num_pages);
+  KESSIE_REQUIRE(page_valid && out_idx && out_count, KESSIE_ERR_INVALID, "valid list: null pointer");
+  int st = check_ws(workspace, workspace_bytes, num_pages, "valid list");
+  if (st) return st;
+  Workspace w = carve(workspace, num_pages);
+  PredArgs a{kPredValid, page_valid, nullptr, nullptr, 0, nullptr, nullptr, nullptr};
+  return ordered_compact(a, num_pages, out_idx, out_count, w, as_stream(stream));
+}
+
+extern "C" int kessie_page_gather(const void* src_pool, int64_t page_bytes, const int32_t* idx,
+                                  const int32_t* count_dev, int n, int num_pages, void* dst, void* stream) {
+  clear_error();
+  KESSIE_REQUIRE(n >= 0 && num_pages >= 0 && page_bytes > 0, KESSIE_ERR_INVALID,
+                 "page gather: n=%d pages=%d page_bytes=%lld", n, num_pages, (long long)page_bytes);
+  if (n == 0) return KESSIE_OK;
+  KESSIE_REQUIRE(src_pool && idx && dst, KESSIE_ERR_INVALID, "page gather: null pointer");
+  KESSIE_REQUIRE(page_bytes % 16 == 0 && aligned16(src_pool) && aligned16(dst), KESSIE_ERR_UNSUPPORTED,
+                 "page gather: page_bytes and pointers must be 16-byte multiples/aligned");
+  const int grid = min(n, 4096);
+  hipLaunchKernelGGL(gather_kernel, dim3(grid), dim3(kGatherThreads), 0, as_stream(stream),
+                     static_cast<const u32x4*>(src_pool), page_bytes / 16, idx, count_dev, n, num_pages,
+                     static_cast<u32x4*>(dst));
+  return check_launch("page gather");
+}
+
+// Reference launchers (kessie_kernels_v2.hip:753-782).
+extern "C" void launch_kessie_page_evict(void* page_valid, const void* page_positions, void* evict_count,
+                                         int evict_before_pos, int num_pages, void* stream) {
+  clear_error();
+  if (num_pages <= 0) return;
+  if (!page_valid || !page_positions || !evict_count) {
+    set_error(KESSIE_ERR_INVALID, "page evict: null pointer");
+    return;
+  }
+  hipLaunchKernelGGL(threshold_evict_kernel, dim3(div_up(num_pages, kThreads)), dim3(kThreads), 0, as_stream(stream),
+                     static_cast<int8_t*>(page_valid), static_cast<const int32_t*>(page_positions),
+                     static_cast<int32_t*>(evict_count), evict_before_pos, num_pages);
+  check_launch("page evict");
+}
+
+extern "C" void launch_kessie_page_insert(void* kv_cache, const void* new_keys, const void* new_values,
+                                          const void* target_page_ids, void* page_valid, void* page_positions,
+                                          int conv_pos, int num_tokens, int num_heads, int head_dim, int page_size,
+                                          int max_pages, void* stream) {
+  clear_error();
+  const int64_t hs = head_dim;
+  const int64_t kvs = (int64_t)num_heads * head_dim;
+  const int64_t ts = 2 * kvs;
+  const int64_t ps = (int64_t)page_size * ts;
+  InsertArgs a{kv_cache,
+               ps,
+               ts,
+               kvs,
+               hs,
+               new_keys,
+               new_values,
+               static_cast<const int32_t*>(target_page_ids),
+               static_cast<int8_t*>(page_valid),
+               static_cast<int32_t*>(page_positions),
+               conv_pos,
+               nullptr,
+               nullptr,
+               nullptr,
+               num_tokens,
+               num_heads,
+               head_dim,
+               page_size,
+               max_pages};
+  insert_dispatch(a, KESSIE_DTYPE_F16, as_stream(stream));
+}

@@ -1,0 +1,243 @@
+// RoPE position remap of recalled K, in place, for gfx950.
+//
+// Semantics (kessie_hip_kernels.py:596-606, _rope_remap_ref):
+//   inv[j]  = host table 1/(theta ** (j/half))          (fp32, j < half)
+//   ang     = float(tgt[t] - orig[t]) * inv[j]          (one fp32 multiply)
+//   x1 = K[t,h,j], x2 = K[t,h,j+half]  (upcast to fp32)
+//   K[t,h,j]      = round(x1*cos(ang) - x2*sin(ang))
+//   K[t,h,j+half] = round(x1*sin(ang) + x2*cos(ang))
+// Every product and sum is rounded separately (no FMA contraction), exactly
+// as the reference's sequence of torch ops does, so that given the same
+// cos/sin values the stored element is bit-identical.
+//
+// Design: HBM-bound (2 bytes read + 2 written per element, 4 flops).  A
+// workgroup owns a tile of tokens.  Phase 1 evaluates cos/sin once per
+// (token, frequency) into LDS, shared by all heads.  Phase 2 streams the K rows
+// with 16-byte loads: each lane owns one chunk pair (8 elements of the first
+// half of a head and the matching 8 of the second half), so a wave's loads
+// cover whole 128-byte segments of a token's K row.
+#include "common.h"
+
+namespace kessie {
+namespace {
+
+constexpr int kRemapThreads = 256;
+constexpr int kRemapTile = 16;    // tokens per workgroup
+constexpr int kVecMaxHalf = 128;  // vectorised kernel: head_dim <= 256
+
+// Byte-free addressing helper: element offset of token t's K row, or -1 when
+// the token's page id is out of range.
+__device__ __forceinline__ int64_t token_row(int t, const int32_t* __restrict__ page_list, int num_pages,
+                                             int page_size, int64_t page_stride, int64_t tok_stride) {
+  if (page_list == nullptr) return (int64_t)t * tok_stride;
+  const int page = page_list[t / page_size];
+  if (page < 0 || page >= num_pages) return -1;
+  return (int64_t)page * page_stride + (int64_t)(t % page_size) * tok_stride;
+}
+
+__device__ __forceinline__ float inv_freq_at(const float* __restrict__ inv_freq, float theta, int j, int half) {
+  if (inv_freq != nullptr) return inv_freq[j];
+  // Legacy entry point: no host table was supplied.
+  return 1.0f / powf(theta, (float)j / (float)half);
+}
+
+template <typename T>
+struct Vec16;  // 16 bytes of T
+template <>
+struct Vec16<bf16_t> {
+  static constexpr int N = 8;
+  typedef bf16x8 type;
+};
+template <>
+struct Vec16<f16_t> {
+  static constexpr int N = 8;
+  typedef f16x8 type;
+};
+template <>
+struct Vec16<float> {
+  static constexpr int N = 4;
+  typedef f32x4 type;
+};
+
+// Vectorised kernel: 16-byte chunks.  Requires half % N == 0, 16-byte aligned
+// rows and head starts.
+template <typename T>
+__global__ __launch_bounds__(kRemapThreads) void rope_remap_vec(
+    T* __restrict__ pool, int64_t page_stride, int64_t tok_stride, int64_t head_stride,
+    const int32_t* __restrict__ page_list, int num_pages, const int32_t* __restrict__ orig_pos,
+    const int32_t* __restrict__ tgt_pos, const float* __restrict__ inv_freq, float theta, int num_tokens,
+    int num_heads, int half, int page_size) {
+#pragma clang fp contract(off)
+  typedef typename Vec16<T>::type V;
+  constexpr int N = Vec16<T>::N;
+  __shared__ float2 cs[kRemapTile * kVecMaxHalf];  // [token][j] = (cos, sin)
+
+  const int t0 = blockIdx.x * kRemapTile;
+  const int ntok = min(kRemapTile, num_tokens - t0);
+  const int n_ang = ntok * half;
+  for (int i = threadIdx.x; i < n_ang; i += kRemapThreads) {
+    const int tt = i / half;
+    const int j = i - tt * half;
+    const int t = t0 + tt;
+    const float delta = (float)(tgt_pos[t] - orig_pos[t]);
+    const float ang = delta * inv_freq_at(inv_freq, theta, j, half);
+    float s, c;
+    sincosf(ang, &s, &c);
+    cs[i] = make_float2(c, s);
+  }
+  __syncthreads();
+
+  const int chunks = half / N;  // chunk pairs per head
+  const int per_tok = num_heads * chunks;
+  const int n_work = ntok * per_tok;
+  for (int i = threadIdx.x; i < n_work; i += kRemapThreads) {
+    const int tt = i / per_tok;
+    const int r = i - tt * per_tok;
+    const int h = r / chunks;
+    const int c = r - h * chunks;
+    const int64_t row = token_row(t0 + tt, page_list, num_pages, page_size, page_stride, tok_stride);
+    if (row < 0) continue;
+    T* p1 = pool + row + (int64_t)h * head_stride + c * N;
+    T* p2 = p1 + half;
+    const V a = *reinterpret_cast<const V*>(p1);
+    const V b = *reinterpret_cast<const V*>(p2);
+    const float2* csr = cs + tt * half + c * N;
+    V y1, y2;
+#pragma unroll
+    for (int e = 0; e < N; ++e) {
+      const float2 q = csr[e];
+      const float x1 = to_f32(a[e]);
+      const float x2 = to_f32(b[e]);
+      const float u1 = x1 * q.x;
+      const float u2 = x2 * q.y;
+      const float w1 = x1 * q.y;
+      const float w2 = x2 * q.x;
+      y1[e] = from_f32<T>(u1 - u2);
+      y2[e] = from_f32<T>(w1 + w2);
+    }
+    *reinterpret_cast<V*>(p1) = y1;
+    *reinterpret_cast<V*>(p2) = y2;
+  }
+}
+
+// Scalar kernel for any even head_dim / alignment: one thread per
+// (token, head, pair).
+template <typename T>
+__global__ __launch_bounds__(kRemapThreads) void rope_remap_scalar(
+    T* __restrict__ pool, int64_t page_stride, int64_t tok_stride, int64_t head_stride,
+    const int32_t* __restrict__ page_list, int num_pages, const int32_t* __restrict__ orig_pos,
+    const int32_t* __restrict__ tgt_pos, const float* __restrict__ inv_freq, float theta, int num_tokens,
+    int num_heads, int half, int page_size) {
+#pragma clang fp contract(off)
+  const int64_t gid = (int64_t)blockIdx.x * kRemapThreads + threadIdx.x;
+  const int64_t total = (int64_t)num_tokens * num_heads * half;
+  if (gid >= total) return;
+  const int j = (int)(gid % half);
+  const int64_t rem = gid / half;
+  const int h = (int)(rem % num_heads);
+  const int t = (int)(rem / num_heads);
+  const int64_t row = token_row(t, page_list, num_pages, page_size, page_stride, tok_stride);
+  if (row < 0) return;
+  const float delta = (float)(tgt_pos[t] - orig_pos[t]);
+  const float ang = delta * inv_freq_at(inv_freq, theta, j, half);
+  float s, c;
+  sincosf(ang, &s, &c);
+  T* p1 = pool + row + (int64_t)h * head_stride + j;
+  T* p2 = p1 + half;
+  const float x1 = to_f32(*p1);
+  const float x2 = to_f32(*p2);
+  const float u1 = x1 * c;
+  const float u2 = x2 * s;
+  const float w1 = x1 * s;
+  const float w2 = x2 * c;
+  *p1 = from_f32<T>(u1 - u2);
+  *p2 = from_f32<T>(w1 + w2);
+}
+
+template <typename T>
+int launch_remap(void* pool, int64_t page_stride, int64_t tok_stride, int64_t head_stride,
+                 const int32_t* page_list, int num_pages, const int32_t* orig_pos, const int32_t* tgt_pos,
+                 const float* inv_freq, float theta, int num_tokens, int num_heads, int head_dim,
+                 int page_size, hipStream_t stream) {
+  const int half = head_dim / 2;
+  constexpr int N = Vec16<T>::N;
+  const bool vec_ok = (half % N == 0) && (half <= kVecMaxHalf) && aligned16(pool) &&
+                      (page_list == nullptr || page_stride % N == 0) && tok_stride % N == 0 &&
+                      head_stride % N == 0;
+  T* p = static_cast<T*>(pool);
+  if (vec_ok) {
+    const int grid = div_up(num_tokens, kRemapTile);
+    hipLaunchKernelGGL(rope_remap_vec<T>, dim3(grid), dim3(kRemapThreads), 0, stream, p, page_stride,
+                       tok_stride, head_stride, page_list, num_pages, orig_pos, tgt_pos, inv_freq, theta,
+                       num_tokens, num_heads, half, page_size);
+  } else {
+    const int64_t total = (int64_t)num_tokens * num_heads * half;
+    const int64_t grid = (total + kRemapThreads - 1) / kRemapThreads;
+    if (grid > 0x7fffffff) {
+      set_error(KESSIE_ERR_UNSUPPORTED, "rope_remap: %lld elements exceed one launch", (long long)total);
+      return KESSIE_ERR_UNSUPPORTED;
+    }
+    hipLaunchKernelGGL(rope_remap_scalar<T>, dim3((unsigned)grid), dim3(kRemapThreads), 0, stream, p,
+                       page_stride, tok_stride, head_stride, page_list, num_pages, orig_pos, tgt_pos, inv_freq,
+                       theta, num_tokens, num_heads, half, page_size);
+  }
+  return check_launch("rope_remap");
+}
+
+int remap_dispatch(void* pool, int64_t page_stride, int64_t tok_stride, int64_t head_stride,
+                   const int32_t* page_list, int num_pages, const int32_t* orig_pos, const int32_t* tgt_pos,
+                   const float* inv_freq, float theta, int num_tokens, int num_heads, int head_dim, int page_size,
+                   int dtype, hipStream_t stream) {
+  KESSIE_REQUIRE(num_tokens >= 0 && num_heads > 0 && head_dim > 0, KESSIE_ERR_INVALID,
+                 "rope_remap: bad sizes T=%d H=%d D=%d", num_tokens, num_heads, head_dim);
+  KESSIE_REQUIRE(head_dim % 2 == 0, KESSIE_ERR_INVALID, "rope_remap: head_dim %d must be even", head_dim);
+  if (num_tokens == 0) return KESSIE_OK;
+  KESSIE_REQUIRE(pool && orig_pos && tgt_pos, KESSIE_ERR_INVALID, "rope_remap: null pointer");
+  KESSIE_REQUIRE(page_list == nullptr || (page_size > 0 && num_pages > 0), KESSIE_ERR_INVALID,
+                 "rope_remap: page_size=%d num_pages=%d", page_size, num_pages);
+  KESSIE_REQUIRE(tok_stride >= (int64_t)num_heads * head_stride && head_stride >= head_dim, KESSIE_ERR_INVALID,
+                 "rope_remap: strides overlap (tok %lld head %lld)", (long long)tok_stride, (long long)head_stride);
+  switch (dtype) {
+    case KESSIE_DTYPE_BF16:
+      return launch_remap<bf16_t>(pool, page_stride, tok_stride, head_stride, page_list, num_pages, orig_pos,
+                                  tgt_pos, inv_freq, theta, num_tokens, num_heads, head_dim, page_size, stream);
+    case KESSIE_DTYPE_F16:
+      return launch_remap<f16_t>(pool, page_stride, tok_stride, head_stride, page_list, num_pages, orig_pos,
+                                 tgt_pos, inv_freq, theta, num_tokens, num_heads, head_dim, page_size, stream);
+    case KESSIE_DTYPE_F32:
+      return launch_remap<float>(pool, page_stride, tok_stride, head_stride, page_list, num_pages, orig_pos,
+                                 tgt_pos, inv_freq, theta, num_tokens, num_heads, head_dim, page_size, stream);
+    default:
+      set_error(KESSIE_ERR_UNSUPPORTED, "rope_remap: dtype %d", dtype);
+      return KESSIE_ERR_UNSUPPORTED;
+  }
+}
+
+}  // namespace
+}  // namespace kessie
+
+extern "C" int kessie_rope_remap_paged(void* kv_pool, int64_t page_stride, int64_t tok_stride,
+                                       int64_t head_stride, const int32_t* page_list, int num_pages,
+                                       const int32_t* orig_pos, const int32_t* tgt_pos, const float* inv_freq,
+                                       int num_tokens, int num_heads, int head_dim, int page_size, int dtype,
+                                       void* stream) {
+  kessie::clear_error();
+  KESSIE_REQUIRE(inv_freq != nullptr, KESSIE_ERR_INVALID, "rope_remap: inv_freq table is required");
+  return kessie::remap_dispatch(kv_pool, page_stride, tok_stride, head_stride, page_list, num_pages, orig_pos,
+                                tgt_pos, inv_freq, 0.0f, num_tokens, num_heads, head_dim, page_size, dtype,
+                                kessie::as_stream(stream));
+}
+
+// Reference launcher signature (kessie_kernels_v2.hip:827-842): fp16 dense
+// [T][H][2*half_dim]; the frequency table is evaluated on the device from
+// rope_theta because this signature carries no table.
+extern "C" void launch_kessie_rope_remap(void* k_data, const void* orig_positions, const void* target_positions,
+                                         float rope_theta, int num_tokens, int num_heads, int half_dim,
+                                         void* stream) {
+  kessie::clear_error();
+  const int head_dim = 2 * half_dim;
+  kessie::remap_dispatch(k_data, 0, (int64_t)num_heads * head_dim, head_dim, nullptr, 0,
+                         static_cast<const int32_t*>(orig_positions), static_cast<const int32_t*>(target_positions),
+                         nullptr, rope_theta, num_tokens, num_heads, head_dim, 0, KESSIE_DTYPE_F16,
+                         kessie::as_stream(stream));
+}

@@ -1,0 +1,141 @@
+"""GPU parity: paged fog decode vs the CPU oracle.
+
+Tolerances (north star): bf16/fp16 outputs with fp32 accumulation
+|gpu - ref| <= 2e-2 + 1e-2*|ref|; fp32 configs 1e-5 (atol and rtol).
+"""
+import math
+
+import pytest
+import torch
+
+from oracle.attention import paged_decode_blockwise, paged_decode_ref
+from oracle.fog import build_fog_weights, fog_bias
+from tests.inputs import decode_case, gen
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.bfloat16: (2e-2, 1e-2), torch.float16: (2e-2, 1e-2), torch.float32: (1e-5, 1e-5)}
+
+
+def _check(got, ref, dtype):
+    atol, rtol = TOL[dtype]
+    g = got.float().cpu()
+    diff = (g - ref).abs()
+    bad = diff > atol + rtol * ref.abs()
+    assert not bad.any(), f"{int(bad.sum())}/{bad.numel()} outside tol, max diff {diff.max().item():.3e}"
+
+
+def _run(dev, b, hq, hkv, ctx, dtype, fog="vscale", window=0, ctx_lens=None, layout="native", seed=0):
+    from kessie_amd import ops
+
+    d, p = 128, 16
+    q, pool, table, lens = decode_case(b, hq, hkv, d, ctx, p, dtype, dev, seed=seed, ctx_lens=ctx_lens)
+    vs = bias = None
+    if fog == "vscale":
+        vs = build_fog_weights(ctx, 0.5, 0.5).to(dev)
+    elif fog == "bias":
+        bias = fog_bias(ctx, 0.5, 0.5, {3, 17, ctx - 2}, 0.1).to(dev)
+    elif fog == "vscale_batched":
+        vs = torch.rand(b, ctx, generator=gen(dev, 77), device=dev)
+    pool_arg = pool
+    if layout == "kv_first":
+        pool_arg = pool.permute(2, 0, 1, 3, 4).contiguous()
+    elif layout == "block_kv":
+        pool_arg = pool.permute(0, 2, 1, 3, 4).contiguous()
+    out = ops.fog_decode(q, pool_arg, table, lens, max_ctx=ctx, fog_vscale=vs, fog_bias=bias, window=window,
+                         layout=layout)
+    torch.cuda.synchronize()
+    ref = paged_decode_ref(q.cpu(), pool.cpu(), table.cpu(), lens.cpu(),
+                           None if vs is None else vs.cpu(), None if bias is None else bias.cpu(), window)
+    return out, ref
+
+
+@pytest.mark.parametrize("hq,hkv", [(32, 8), (8, 8), (16, 8), (64, 8)])
+def test_decode_bf16_gqa(dev, hq, hkv):
+    out, ref = _run(dev, 2, hq, hkv, 1000, torch.bfloat16)
+    _check(out, ref, torch.bfloat16)
+
+
+def test_decode_fp16(dev):
+    out, ref = _run(dev, 2, 32, 8, 777, torch.float16)
+    _check(out, ref, torch.float16)
+
+
+def test_decode_fp32_cpu_path_shape(dev):
+    """Config: fp32, B=1, 32q/8kv, D=128, 4096-token context, V-fog defaults."""
+    out, ref = _run(dev, 1, 32, 8, 4096, torch.float32)
+    _check(out, ref, torch.float32)
+
+
+@pytest.mark.parametrize("fog", ["none", "bias", "vscale_batched"])
+def test_decode_fog_modes(dev, fog):
+    out, ref = _run(dev, 3, 32, 8, 530, torch.bfloat16, fog=fog)
+    _check(out, ref, torch.bfloat16)
+
+
+@pytest.mark.parametrize("window", [1, 15, 16, 100, 5000])
+def test_decode_window(dev, window):
+    out, ref = _run(dev, 2, 32, 8, 1200, torch.bfloat16, window=window)
+    _check(out, ref, torch.bfloat16)
+
+
+def test_decode_ragged_and_empty(dev):
+    lens = [0, 1, 15, 16, 17, 999]
+    out, ref = _run(dev, 6, 32, 8, 1000, torch.bfloat16, ctx_lens=lens)
+    _check(out, ref, torch.bfloat16)
+    assert torch.count_nonzero(out[0]) == 0
+
+
+@pytest.mark.parametrize("layout", ["kv_first", "block_kv"])
+def test_decode_vllm_layouts(dev, layout):
+    out, ref = _run(dev, 2, 32, 8, 640, torch.bfloat16, layout=layout)
+    _check(out, ref, torch.bfloat16)
+
+
+def test_decode_invalid_page_ids_are_masked(dev):
+    from kessie_amd import ops
+
+    q, pool, table, lens = decode_case(1, 32, 8, 128, 256, 16, torch.bfloat16, dev, seed=3)
+    table[0, 5] = -1
+    table[0, 9] = 1 << 20
+    out = ops.fog_decode(q, pool, table, lens, max_ctx=256)
+    torch.cuda.synchronize()
+    # Oracle: the same attention without the tokens of logical pages 5 and 9.
+    keep = [i for i in range(16) if i not in (5, 9)]
+    pool_c = pool.cpu()
+    t2 = table.cpu()[:, keep].contiguous()
+    ref = paged_decode_ref(q.cpu(), pool_c, t2, torch.tensor([len(keep) * 16]))
+    _check(out, ref, torch.bfloat16)
+
+
+def test_decode_generic_path_matches_mfma_path(dev, monkeypatch):
+    """The VALU fallback kernel (any shape) and the MFMA kernel agree."""
+    from kessie_amd import ops
+
+    q, pool, table, lens = decode_case(2, 32, 8, 128, 900, 16, torch.bfloat16, dev, seed=4)
+    vs = build_fog_weights(900).to(dev)
+    a = ops.fog_decode(q, pool, table, lens, 900, fog_vscale=vs)
+    monkeypatch.setenv("KESSIE_FORCE_GENERIC", "1")
+    b = ops.fog_decode(q, pool, table, lens, 900, fog_vscale=vs)
+    torch.cuda.synchronize()
+    assert (a.float() - b.float()).abs().max().item() < 2e-2
+
+
+def test_decode_llama8b_128k_sampled(dev):
+    """Config: bf16, B=16, 32q/8kv, D=128, 131,072-token context in 16-token pages,
+    V-fog defaults.  Full-size run; two sequences checked against the oracle."""
+    from kessie_amd import ops
+
+    b, ctx = 16, 131072
+    q, pool, table, lens = decode_case(b, 32, 8, 128, ctx, 16, torch.bfloat16, dev, seed=0)
+    vs = build_fog_weights(ctx).to(dev)
+    out = ops.fog_decode(q, pool, table, lens, ctx, fog_vscale=vs)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    for s in (0, 11):
+        # Gather the sequence's pages on the device first (8192 pages), then run
+        # the blockwise oracle on the CPU copy of just those pages.
+        sub_pool = pool[table[s].long()].cpu()
+        sub_table = torch.arange(table.shape[1], dtype=torch.int32).view(1, -1)
+        ref = paged_decode_blockwise(q[s:s + 1].cpu(), sub_pool, sub_table, lens[s:s + 1].cpu(), vs.cpu())
+        _check(out[s:s + 1], ref, torch.bfloat16)

@@ -1,0 +1,207 @@
+"""GPU parity: paged-KV management vs the CPU oracle (bit-exact: page tables,
+gather indices, eviction order, valid masks, gathered bytes)."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import pages as P
+from tests.inputs import gen, paged_pool, randperm
+
+pytestmark = pytest.mark.gpu
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+def test_legacy_page_evict_known_answer(dev):
+    """kessie_kernels_v2.hip:1008-1023: 128 valid pages at pos i*128, thr 8192 -> 64."""
+    from kessie_amd.kessie_hip_ctypes import KeSSieKernels
+
+    kk = KeSSieKernels()
+    valid = torch.zeros(256, dtype=torch.int8, device=dev)
+    valid[:128] = 1
+    pos = torch.zeros(256, dtype=torch.int32, device=dev)
+    pos[:128] = torch.arange(128, device=dev, dtype=torch.int32) * 128
+    ref_valid, ref_count = P.threshold_evict(_np(valid), _np(pos), 8192)
+    n = kk.page_evict(valid, pos, 8192)
+    assert n == 64 == ref_count
+    assert np.array_equal(_np(valid), ref_valid)
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_evict_list_matches_free_list_order(dev, seed):
+    from kessie_amd import ops
+
+    rng = np.random.default_rng(seed)
+    n = 5000
+    valid = rng.integers(0, 2, n).astype(np.int8)
+    allocated = np.where(valid == 1, 1, rng.integers(0, 2, n)).astype(np.int8)
+    pos = rng.integers(0, 100000, n).astype(np.int32)
+    ref_valid, ref_alloc, ref_freed = P.evict_list(valid, pos, allocated, 50000)
+    dv, dp, da = (torch.from_numpy(x).to(dev) for x in (valid, pos, allocated))
+    lst, cnt = ops.page_evict_list(dv, dp, 50000, da)
+    torch.cuda.synchronize()
+    c = int(cnt.item())
+    assert c == len(ref_freed)
+    assert np.array_equal(_np(lst[:c]), ref_freed)
+    assert np.array_equal(_np(dv), ref_valid)
+    assert np.array_equal(_np(da), ref_alloc)
+
+
+@pytest.mark.parametrize("n,frac,k", [(65536, 0.25, -1), (1000, 0.25, -1), (3000, 0.0, 17), (777, 0.5, -1),
+                                      (4096, 0.25, 100000)])
+def test_select_evict_bit_exact(dev, n, frac, k):
+    from kessie_amd import ops
+
+    g = torch.Generator().manual_seed(n)
+    scores = torch.rand(n, generator=g)
+    # Plant duplicates, -0/+0 and negative scores to exercise the tie order.
+    scores[: n // 10] = scores[n // 10: 2 * (n // 10)]
+    scores[5] = -0.0
+    scores[6] = 0.0
+    scores[7] = -1.5
+    valid = (torch.rand(n, generator=g) < 0.9).to(torch.int8)
+    ref_valid, ref_list = P.select_evict(scores.numpy(), valid.numpy(), k, frac)
+    dv = valid.to(dev)
+    lst, cnt = ops.page_select_evict(scores.to(dev), dv, k, frac)
+    torch.cuda.synchronize()
+    c = int(cnt.item())
+    assert c == len(ref_list)
+    assert np.array_equal(_np(lst[:c]), ref_list)
+    assert np.array_equal(_np(dv), ref_valid)
+
+
+def test_compact_and_gather_bit_exact(dev):
+    from kessie_amd import ops
+
+    num_pages, s, w = 4096, 8, 512
+    pool = paged_pool(num_pages, 16, 8, 128, torch.bfloat16, dev, 0)
+    tables = randperm(num_pages, dev, 1).view(s, w).contiguous()
+    lens = torch.tensor([512, 0, 1, 300, 511, 512, 17, 256], dtype=torch.int32, device=dev)
+    tables[2, 0] = -1  # out-of-range entries never survive
+    valid = (torch.rand(num_pages, generator=gen(dev, 2), device=dev) < 0.7).to(torch.int8)
+    nt, nl, gi, gc = ops.page_compact(tables, lens, valid)
+    out = ops.page_gather(pool, gi, gc, n=s * w)
+    torch.cuda.synchronize()
+    rt, rl, rg = P.compact(_np(tables), _np(lens), _np(valid))
+    assert np.array_equal(_np(nt), rt)
+    assert np.array_equal(_np(nl), rl)
+    c = int(gc.item())
+    assert c == len(rg)
+    assert np.array_equal(_np(gi[:c]), rg)
+    ref_bytes = P.gather_pages(_np(pool.view(num_pages, -1).view(torch.int16)), rg)
+    assert np.array_equal(_np(out[:c].reshape(c, -1).view(torch.int16)), ref_bytes)
+
+
+def test_valid_list_matches_get_layer_kv_order(dev):
+    from kessie_amd import ops
+
+    valid = (torch.rand(10000, generator=gen(dev, 3), device=dev) < 0.3).to(torch.int8)
+    idx, cnt = ops.page_valid_list(valid)
+    torch.cuda.synchronize()
+    ref = P.valid_list(_np(valid))
+    assert int(cnt.item()) == len(ref)
+    assert np.array_equal(_np(idx[: len(ref)]), ref)
+
+
+def test_score_evict_full_config(dev):
+    """Config: 65,536-page pool (1,048,576 tokens), 64 sequences x 1,024 pages,
+    scores ~ U(0,1), evict the lowest 25%, compact, gather survivors (3 GiB)."""
+    from kessie_amd import ops
+
+    num_pages, s, w = 65536, 64, 1024
+    pool = paged_pool(num_pages, 16, 8, 128, torch.bfloat16, dev, 0)
+    tables = randperm(num_pages, dev, 1).view(s, w).contiguous()
+    scores = torch.rand(num_pages, generator=gen(dev, 2), device=dev)
+    valid = torch.ones(num_pages, dtype=torch.int8, device=dev)
+    lens = torch.full((s,), w, dtype=torch.int32, device=dev)
+    lst, cnt = ops.page_select_evict(scores, valid, -1, 0.25)
+    nt, nl, gi, gc = ops.page_compact(tables, lens, valid)
+    out = ops.page_gather(pool, gi, gc, n=s * w)
+    torch.cuda.synchronize()
+    rv, rlist = P.select_evict(_np(scores), np.ones(num_pages, np.int8), -1, 0.25)
+    assert len(rlist) == 16384
+    assert int(cnt.item()) == 16384 and np.array_equal(_np(lst[:16384]), rlist)
+    assert np.array_equal(_np(valid), rv)
+    rt, rl, rg = P.compact(_np(tables), _np(lens), rv)
+    assert np.array_equal(_np(nt), rt) and np.array_equal(_np(nl), rl)
+    c = int(gc.item())
+    assert c == 49152 and np.array_equal(_np(gi[:c]), rg)
+    # Gathered bytes: checksum per page plus a full compare of 512 sampled pages.
+    sample = np.random.default_rng(0).choice(c, 512, replace=False)
+    got = out[torch.from_numpy(sample).to(dev)]
+    ref = pool[torch.from_numpy(rg[sample]).long().to(dev)]
+    assert torch.equal(got, ref)
+    sums_got = out[:c].view(c, -1).view(torch.int16).to(torch.int64).sum(1)
+    sums_ref = pool[gi[:c].long()].view(c, -1).view(torch.int16).to(torch.int64).sum(1)
+    assert torch.equal(sums_got, sums_ref)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_insert_matches_oracle(dev, dtype):
+    from kessie_amd import ops
+
+    num_pages, p, h, d = 64, 16, 8, 128
+    pool = paged_pool(num_pages, p, h, d, dtype, dev, 0)
+    t = 70
+    nk = torch.randn(t, h, d, generator=gen(dev, 1), device=dev).to(dtype)
+    nv = torch.randn(t, h, d, generator=gen(dev, 2), device=dev).to(dtype)
+    target = torch.tensor([5, -1, 63, 64, 9], dtype=torch.int32, device=dev)
+    valid = torch.zeros(num_pages, dtype=torch.int8, device=dev)
+    posn = torch.zeros(num_pages, dtype=torch.int32, device=dev)
+    ref_pool, ref_valid, ref_pos = (x.cpu().numpy().copy() for x in (pool.view(torch.int16) if dtype != torch.float32 else pool, valid, posn))
+    P.page_insert(ref_pool, (nk.view(torch.int16) if dtype != torch.float32 else nk).cpu().numpy(),
+                  (nv.view(torch.int16) if dtype != torch.float32 else nv).cpu().numpy(), target.cpu().numpy(),
+                  ref_valid, ref_pos, 1000)
+    ops.page_insert(pool, nk, nv, target, valid, posn, 1000)
+    torch.cuda.synchronize()
+    got = (pool.view(torch.int16) if dtype != torch.float32 else pool).cpu().numpy()
+    assert np.array_equal(got, ref_pool)
+    assert np.array_equal(_np(valid), ref_valid)
+    assert np.array_equal(_np(posn), ref_pos)
+
+
+def test_insert_with_remap_matches_insert_then_remap(dev):
+    from kessie_amd import ops
+
+    num_pages, p, h, d = 32, 16, 8, 128
+    pool_a = paged_pool(num_pages, p, h, d, torch.bfloat16, dev, 0)
+    pool_b = pool_a.clone()
+    t = 48
+    nk = torch.randn(t, h, d, generator=gen(dev, 1), device=dev).bfloat16()
+    nv = torch.randn(t, h, d, generator=gen(dev, 2), device=dev).bfloat16()
+    target = torch.tensor([3, 7, 11], dtype=torch.int32, device=dev)
+    orig = torch.randint(0, 1_000_000, (t,), generator=gen(dev, 3), device=dev, dtype=torch.int32)
+    tgt = (5000 + torch.arange(t, device=dev)).to(torch.int32)
+    va, pa = torch.zeros(num_pages, dtype=torch.int8, device=dev), torch.zeros(num_pages, dtype=torch.int32, device=dev)
+    vb, pb = va.clone(), pa.clone()
+    ops.page_insert(pool_a, nk, nv, target, va, pa, 0, orig_pos=orig, tgt_pos=tgt, rope_theta=500000.0)
+    ops.page_insert(pool_b, nk, nv, target, vb, pb, 0)
+    ops.rope_remap_paged(pool_b, orig, tgt, 500000.0, page_list=target)
+    torch.cuda.synchronize()
+    assert torch.equal(pool_a, pool_b)  # same kernels' arithmetic, same bits
+    assert torch.equal(va, vb) and torch.equal(pa, pb)
+
+
+def test_legacy_page_insert_fp16(dev):
+    from kessie_amd import _lib
+
+    num_pages, p, h, d = 16, 8, 4, 64
+    pool = torch.zeros(num_pages, p, 2, h, d, dtype=torch.float16, device=dev)
+    t = 20
+    nk = torch.randn(t, h, d, generator=gen(dev, 5), device=dev).half()
+    nv = torch.randn(t, h, d, generator=gen(dev, 6), device=dev).half()
+    target = torch.tensor([2, 40, 9], dtype=torch.int32, device=dev)
+    valid = torch.zeros(num_pages, dtype=torch.int8, device=dev)
+    posn = torch.zeros(num_pages, dtype=torch.int32, device=dev)
+    rp, rv, rpos = pool.cpu().numpy().copy(), valid.cpu().numpy().copy(), posn.cpu().numpy().copy()
+    P.page_insert(rp, nk.cpu().numpy(), nv.cpu().numpy(), target.cpu().numpy(), rv, rpos, 77)
+    ptr = lambda x: ctypes.c_void_p(x.data_ptr())
+    _lib.call_legacy("launch_kessie_page_insert", ptr(pool), ptr(nk), ptr(nv), ptr(target), ptr(valid), ptr(posn),
+                     77, t, h, d, p, num_pages, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    assert np.array_equal(pool.cpu().numpy(), rp)
+    assert np.array_equal(_np(valid), rv) and np.array_equal(_np(posn), rpos)
