@@ -1,0 +1,396 @@
+#!/usr/bin/env python3
+"""KeSSie hot path on one MI355X: fog-attention decode GB/s (primary) and RoPE
+remap Mtok/s, with the kernels' roofline and the CPU oracle timed beside them.
+
+Primary workload (the JSON ``value``): fog-attention decode, bf16, Llama-3-8B
+attention shape -- batch 16, 32 query / 8 KV heads, head_dim 128, 131,072-token
+context per sequence in 16-token pages (random page tables), V-fog weights
+alpha 0.5 / fog_start 0.5, window 0.  A step is one decode of the batch:
+the streaming partials kernel plus the split-combine kernel.  ``value`` =
+algorithmic bytes of one decode / step time.
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu] [--no-secondary]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "fog-attn decode GB/s (% HBM peak) @128K ctx; RoPE-remap Mtok/s"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2516.6
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def events(n):
+    import torch
+
+    return [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+
+
+def decode_bytes(b, ctx, hq, hkv, d, es, page_size, fog=True):
+    pages = (ctx + page_size - 1) // page_size
+    kv = b * ctx * hkv * d * 2 * es
+    return kv + 2 * b * hq * d * es + b * pages * 4 + (ctx * 4 if fog else 0)
+
+
+def read_traffic(kernel: str):
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE/WRITE_SIZE),
+    scaled by the copy-kernel calibration; from profiles/hbm_traffic.txt."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    for ln in open(path):
+        parts = ln.split()
+        if len(parts) >= 2 and parts[0] == kernel and not ln.startswith("#"):
+            try:
+                return float(parts[1])
+            except ValueError:
+                return None
+    return None
+
+
+# ---------------------------------------------------------------------------
+# Primary: bf16 decode @128K
+# ---------------------------------------------------------------------------
+def setup_decode(dev, b=16, hq=32, hkv=8, d=128, ctx=131072, page_size=16, dtype=None, seed=0):
+    import torch
+
+    from kessie_amd import ops
+
+    dtype = dtype or torch.bfloat16
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    q = torch.randn(b, hq, d, generator=g, device=dev, dtype=torch.float32).to(dtype)
+    pages = (ctx + page_size - 1) // page_size
+    n_pages = b * pages
+    pool = torch.empty(n_pages, page_size, 2, hkv, d, device=dev, dtype=dtype)
+    chunk = 4096
+    for p0 in range(0, n_pages, chunk):  # K and V ~ N(0,1), generated chunk by chunk
+        p1 = min(n_pages, p0 + chunk)
+        pool[p0:p1] = torch.randn(p1 - p0, page_size, 2, hkv, d, generator=g, device=dev).to(dtype)
+    g1 = torch.Generator(device=dev)
+    g1.manual_seed(seed + 1)
+    table = torch.randperm(n_pages, generator=g1, device=dev).to(torch.int32).view(b, pages).contiguous()
+    lens = torch.full((b,), ctx, dtype=torch.int32, device=dev)
+    # Fog weights: the reference's kessie_build_fog_weights(ctx, 0.5, 0.5), built on the device.
+    c = int(ctx * 0.5)
+    fog = torch.ones(ctx, dtype=torch.float32, device=dev)
+    fog[:c] = (torch.arange(c, dtype=torch.float32, device=dev) / max(c - 1, 1)).pow(0.5)
+    nbytes = ws_bytes = 0
+    from kessie_amd import _lib
+
+    ws_bytes = _lib.load().kessie_fog_decode_workspace_bytes(b, hq, hkv, d, ctx, page_size, ops.dtype_code(dtype))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    out = torch.empty_like(q)
+    nbytes = decode_bytes(b, ctx, hq, hkv, d, q.element_size(), page_size)
+    return dict(q=q, pool=pool, table=table, lens=lens, fog=fog, ws=ws, out=out, ctx=ctx, hkv=hkv,
+                page_size=page_size, bytes=nbytes, b=b, hq=hq, d=d)
+
+
+def run_decode_step(s):
+    from kessie_amd import ops
+
+    ops.fog_decode_partials(s["q"], s["pool"], s["table"], s["lens"], s["ctx"], s["ws"], fog_vscale=s["fog"])
+    ops.fog_decode_combine(s["ws"], s["out"], s["hkv"], s["ctx"], s["page_size"])
+
+
+def time_decode(s, steps, warmup):
+    import torch
+
+    from kessie_amd import ops
+
+    for _ in range(warmup):
+        run_decode_step(s)
+    torch.cuda.synchronize()
+    e0, e1 = events(steps), events(steps)
+    start, end = events(2)
+    start.record()
+    for i in range(steps):
+        e0[i].record()
+        ops.fog_decode_partials(s["q"], s["pool"], s["table"], s["lens"], s["ctx"], s["ws"], fog_vscale=s["fog"])
+        e1[i].record()
+        ops.fog_decode_combine(s["ws"], s["out"], s["hkv"], s["ctx"], s["page_size"])
+    end.record()
+    torch.cuda.synchronize()
+    total_ms = start.elapsed_time(end)
+    kern = [a.elapsed_time(b) for a, b in zip(e0, e1)]
+    return total_ms / steps, sum(kern) / len(kern)
+
+
+def cpu_decode_baseline(s, budget_s=12.0):
+    """The CPU oracle (oracle.attention.paged_decode_blockwise) on the GPU box's
+    host cores: whole sequences of the same workload until ~budget_s seconds."""
+    import torch
+
+    from oracle.attention import paged_decode_blockwise
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    fog = s["fog"].cpu()
+    q = s["q"].cpu()
+    table = s["table"]
+    per_seq_bytes = s["bytes"] / s["b"]
+
+    def seq_inputs(i):
+        sub_pool = s["pool"][table[i].long()].cpu()
+        sub_table = torch.arange(table.shape[1], dtype=torch.int32).view(1, -1)
+        return sub_pool, sub_table
+
+    p0, t0 = seq_inputs(0)
+    paged_decode_blockwise(q[0:1], p0, t0, s["lens"][0:1].cpu(), fog)  # warm-up
+    done, elapsed = 0, 0.0
+    for i in range(1, s["b"]):
+        pool_i, table_i = seq_inputs(i)
+        t = time.perf_counter()
+        paged_decode_blockwise(q[i:i + 1], pool_i, table_i, s["lens"][i:i + 1].cpu(), fog)
+        elapsed += time.perf_counter() - t
+        done += 1
+        if elapsed >= budget_s:
+            break
+    return {
+        "value": round(per_seq_bytes * done / elapsed / 1e9, 3),
+        "unit": "GB/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"{done} of {s['b']} sequences x {s['ctx']} tokens (bf16 pages upcast to fp32, blockwise "
+                  f"online softmax, torch {torch.__version__}, {platform.processor() or platform.machine()})",
+        "seconds": round(elapsed, 2),
+    }
+
+
+# ---------------------------------------------------------------------------
+# Secondary workloads
+# ---------------------------------------------------------------------------
+def bench_remap(dev, reps=20, sets=4, n_tok=65536, page_size=16, hkv=8, d=128, theta=500000.0):
+    """RoPE remap, bf16, 65,536 tokens in 16-token pages, 8 KV heads, D=128,
+    theta 5e5, only K rotated.  ``sets`` disjoint page sets rotate across reps
+    so the 256 MB MALL cannot serve the next rep."""
+    import torch
+
+    from kessie_amd import ops
+
+    pages = n_tok // page_size
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    pool = torch.randn(pages * sets, page_size, 2, hkv, d, generator=g, device=dev).bfloat16()
+    g1 = torch.Generator(device=dev)
+    g1.manual_seed(1)
+    perm = torch.randperm(pages * sets, generator=g1, device=dev).to(torch.int32)
+    lists = [perm[i * pages:(i + 1) * pages].contiguous() for i in range(sets)]
+    g2 = torch.Generator(device=dev)
+    g2.manual_seed(2)
+    orig = torch.randint(0, 1_000_000, (n_tok,), generator=g2, device=dev, dtype=torch.int32)
+    g3 = torch.Generator(device=dev)
+    g3.manual_seed(3)
+    base = int(torch.randint(0, 1_000_000, (1,), generator=g3, device=dev).item())
+    tgt = (base + torch.arange(n_tok, device=dev)).to(torch.int32)
+    for i in range(3):
+        ops.rope_remap_paged(pool, orig, tgt, theta, page_list=lists[i % sets])
+    torch.cuda.synchronize()
+    e0, e1 = events(reps), events(reps)
+    for i in range(reps):
+        e0[i].record()
+        ops.rope_remap_paged(pool, orig, tgt, theta, page_list=lists[i % sets])
+        e1[i].record()
+    torch.cuda.synchronize()
+    ts = sorted(a.elapsed_time(b) for a, b in zip(e0, e1))
+    mean_ms = sum(ts) / len(ts)
+    nbytes = 2 * n_tok * hkv * d * 2 + 2 * n_tok * 4 + pages * 4
+    achieved = nbytes / (mean_ms * 1e-3) / 1e9
+    return {
+        "workload": f"RoPE remap bf16, {n_tok} tokens in {page_size}-token pages, {hkv} KV heads, D={d}, "
+                    f"theta {theta:g}, K only, {sets} rotating page sets",
+        "mtok_s": round(n_tok / (mean_ms * 1e-3) / 1e6, 1),
+        "kernel_ms_mean": round(mean_ms, 5),
+        "kernel_ms_median": round(ts[len(ts) // 2], 5),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic("rope_remap_vec"),
+                     "algorithmic_bytes": nbytes},
+    }
+
+
+def bench_gather_evict(dev, reps=5):
+    """Paged-KV gather + eviction: 65,536-page pool (1,048,576 tokens, 16-token
+    pages, 8 KV heads x D=128 bf16), 64 sequences x 1,024 pages (random
+    tables), per-page scores ~ U(0,1); evict the lowest 25%, compact the
+    tables, gather the survivors' pages."""
+    import torch
+
+    from kessie_amd import ops
+
+    num_pages, s, w = 65536, 64, 1024
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    pool = torch.randn(num_pages, 16, 2, 8, 128, generator=g, device=dev).bfloat16()
+    g1 = torch.Generator(device=dev)
+    g1.manual_seed(1)
+    tables = torch.randperm(num_pages, generator=g1, device=dev).to(torch.int32).view(s, w).contiguous()
+    g2 = torch.Generator(device=dev)
+    g2.manual_seed(2)
+    scores = torch.rand(num_pages, generator=g2, device=dev)
+    lens = torch.full((s,), w, dtype=torch.int32, device=dev)
+    valid = torch.ones(num_pages, dtype=torch.int8, device=dev)
+    out = torch.empty(s * w, 16, 2, 8, 128, dtype=torch.bfloat16, device=dev)
+    ev_list = torch.empty(num_pages, dtype=torch.int32, device=dev)
+    ev_cnt = torch.zeros(1, dtype=torch.int32, device=dev)
+    nt = torch.empty_like(tables)
+    nl = torch.empty(s, dtype=torch.int32, device=dev)
+    gi = torch.empty(s * w, dtype=torch.int32, device=dev)
+    gc = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def pipeline(e_sel=None, e_gat=None):
+        ops.page_select_evict(scores, valid, -1, 0.25, ev_list, ev_cnt)
+        ops.page_compact(tables, lens, valid, nt, nl, gi, gc)
+        if e_sel is not None:
+            e_sel.record()
+        ops.page_gather(pool, gi, gc, out=out, n=s * w)
+        if e_gat is not None:
+            e_gat.record()
+
+    for _ in range(2):
+        valid.fill_(1)
+        pipeline()
+    torch.cuda.synchronize()
+    e0, e1, e2 = events(reps), events(reps), events(reps)
+    for i in range(reps):
+        valid.fill_(1)
+        e0[i].record()
+        pipeline(e1[i], e2[i])
+    torch.cuda.synchronize()
+    tot = sum(a.elapsed_time(c) for a, c in zip(e0, e2)) / reps
+    gat = sum(b.elapsed_time(c) for b, c in zip(e1, e2)) / reps
+    survivors = int(gc.item())
+    page_bytes = 16 * 2 * 8 * 128 * 2
+    gather_bytes = 2 * survivors * page_bytes
+    alg = gather_bytes + num_pages * 4 * 2 + s * w * 4 + survivors * 4 + int(ev_cnt.item()) * 4
+    ach = gather_bytes / (gat * 1e-3) / 1e9
+    return {
+        "workload": "score evict 25% of 65,536 pages + compact 64x1024 tables + gather survivors (bf16 pages)",
+        "pipeline_ms": round(tot, 4),
+        "gather_kernel_ms": round(gat, 4),
+        "select_compact_ms": round(tot - gat, 4),
+        "pipeline_gbs": round(alg / (tot * 1e-3) / 1e9, 1),
+        "survivor_pages": survivors,
+        "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": read_traffic("gather_kernel"),
+                     "algorithmic_bytes": gather_bytes},
+    }
+
+
+def bench_decode_fp32(dev, reps=20):
+    """Fog decode on the reference CPU path's shape, fp32: B=1, 32q/8kv, D=128,
+    4,096-token context in 16-token pages."""
+    import torch
+
+    s = setup_decode(dev, b=1, ctx=4096, dtype=torch.float32)
+    for _ in range(3):
+        run_decode_step(s)
+    torch.cuda.synchronize()
+    e0, e1 = events(reps), events(reps)
+    for i in range(reps):
+        e0[i].record()
+        run_decode_step(s)
+        e1[i].record()
+    torch.cuda.synchronize()
+    ms = sum(a.elapsed_time(b) for a, b in zip(e0, e1)) / reps
+    return {"workload": "fog decode fp32, B=1, 32q/8kv, D=128, 4096-token context",
+            "ms": round(ms, 5), "gbs": round(s["bytes"] / (ms * 1e-3) / 1e9, 1)}
+
+
+# ---------------------------------------------------------------------------
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-secondary", action="store_true", help="skip remap / gather / fp32 lines")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (the hot path is built and measured on a single MI355X); "
+              f"--gpus {args.gpus} is not supported", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from kessie_amd import _lib
+
+    _lib.load()
+    dev = torch.device("cuda:0")
+    props = torch.cuda.get_device_properties(dev)
+    log(f"device {props.name} CUs={props.multi_processor_count} lib={_lib.lib_path()}")
+
+    log("setting up decode: B=16, 131072-token context, bf16")
+    s = setup_decode(dev)
+    torch.cuda.synchronize()
+    log(f"timing decode: warmup {args.warmup}, steps {args.steps}")
+    ms_step, ms_kern = time_decode(s, args.steps, args.warmup)
+    value = s["bytes"] / (ms_step * 1e-3) / 1e9
+    achieved = s["bytes"] / (ms_kern * 1e-3) / 1e9
+    log(f"decode: {ms_step:.4f} ms/step, partials kernel {ms_kern:.4f} ms, {value:.1f} GB/s")
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: q, K, V ~ N(0,1) (seed 0), random page tables (seed 1)",
+        "config": {
+            "workload": "fog-attention decode, bf16, batch 16, 32 query / 8 KV heads, head_dim 128, "
+                        "131072-token context per sequence in 16-token pages, V-fog alpha 0.5 fog_start 0.5, "
+                        "window 0; step = partials kernel + split combine",
+            "batch": 16, "ctx": 131072, "q_heads": 32, "kv_heads": 8, "head_dim": 128, "page_size": 16,
+            "splits": _lib.load().kessie_fog_decode_num_splits(16, 8, 131072, 16),
+            "algorithmic_bytes": s["bytes"],
+        },
+        "pct_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
+        "roofline": {
+            "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic("decode_mfma_kernel"),
+            "kernel": "decode_mfma_kernel", "kernel_ms": round(ms_kern, 5),
+        },
+        "device": {"name": props.name, "cus": props.multi_processor_count},
+    }
+    if not args.no_cpu:
+        log("CPU baseline (oracle, host cores)")
+        result["cpu_baseline"] = cpu_decode_baseline(s)
+    else:
+        result["cpu_baseline"] = None
+    del s
+    torch.cuda.empty_cache()
+    if not args.no_secondary:
+        sec = {}
+        log("secondary: RoPE remap")
+        sec["rope_remap"] = bench_remap(dev)
+        result["rope_remap_mtok_s"] = sec["rope_remap"]["mtok_s"]
+        torch.cuda.empty_cache()
+        log("secondary: gather + evict")
+        sec["gather_evict"] = bench_gather_evict(dev)
+        torch.cuda.empty_cache()
+        log("secondary: fp32 decode 4K")
+        sec["decode_fp32_4k"] = bench_decode_fp32(dev)
+        result["secondary"] = sec
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -139,6 +139,36 @@ int kessie_fog_decode_paged(
     int page_size, int max_ctx, int window, float sm_scale, int dtype,
     void* workspace, size_t workspace_bytes, void* stream);
 
+/* Number of key splits S the decode uses for these sizes (host call). */
+int kessie_fog_decode_num_splits(int batch, int num_kv_heads, int max_ctx,
+                                 int page_size);
+
+/* First half of kessie_fog_decode_paged: the streaming kernel only.  Writes
+ * the per-split partials of every row r = b*Hq + h into the workspace:
+ *   o[r][s][D] fp32 (unnormalised sum of p*w*v), then, each starting on a
+ *   256-byte boundary, m[r][s] (running max, -inf when the split saw no key)
+ *   and l[r][s] (sum of p), with S = kessie_fog_decode_num_splits(...).
+ * Always writes partials, also when S == 1.  These are also the (m, l, o)
+ * triples a context-parallel split of one sequence across devices would
+ * exchange before kessie_fog_decode_combine.  (No reference counterpart: the
+ * reference has no split decode.) */
+int kessie_fog_decode_partials(
+    const void* q, const void* kv_pool, int num_pages, int64_t page_stride,
+    int64_t tok_stride, int64_t kv_stride, int64_t head_stride,
+    const int32_t* page_table, int64_t table_stride, const int32_t* ctx_lens,
+    const float* fog_vscale, int64_t fog_vscale_bstride, const float* fog_bias,
+    int64_t fog_bias_bstride, int batch, int num_q_heads, int num_kv_heads,
+    int head_dim, int page_size, int max_ctx, int window, float sm_scale,
+    int dtype, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Second half: merges the partials in `workspace` (laid out as above) into
+ * out [B][Hq][D] in `dtype`: o = sum_s e_s o_s / sum_s e_s l_s with
+ * e_s = exp(m_s - max_s m_s); rows with no key get zeros. */
+int kessie_fog_decode_combine(const void* workspace, size_t workspace_bytes,
+                              void* out, int batch, int num_q_heads,
+                              int num_kv_heads, int head_dim, int max_ctx,
+                              int page_size, int dtype, void* stream);
+
 /* Bytes of workspace kessie_fog_prefill_paged needs (host call). */
 size_t kessie_fog_prefill_workspace_bytes(int batch, int num_q_tokens,
                                           int num_q_heads, int num_kv_heads,

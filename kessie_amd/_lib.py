@@ -45,6 +45,12 @@ SIGNATURES = {
     "kessie_fog_decode_paged": (_I, [
         _P, _P, _I, _I64, _I64, _I64, _I64, _P, _I64, _P, _P, _I64, _P, _I64,
         _P, _I, _I, _I, _I, _I, _I, _I, _F, _I, _P, _SZ, _P]),
+    "kessie_fog_decode_num_splits": (_I, [_I, _I, _I, _I]),
+    # as kessie_fog_decode_paged without `out`
+    "kessie_fog_decode_partials": (_I, [
+        _P, _P, _I, _I64, _I64, _I64, _I64, _P, _I64, _P, _P, _I64, _P, _I64,
+        _I, _I, _I, _I, _I, _I, _I, _F, _I, _P, _SZ, _P]),
+    "kessie_fog_decode_combine": (_I, [_P, _SZ, _P, _I, _I, _I, _I, _I, _I, _I, _P]),
     "kessie_fog_prefill_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I, _I, _I, _I]),
     # ... out, B, C, Hq, Hkv, D, P, max_ctx, window, sm_scale, causal, dtype, ws, ws_bytes, stream
     "kessie_fog_prefill_paged": (_I, [

@@ -60,6 +60,8 @@ struct Params {
   int window, causal;
   float sm_scale;
   int num_splits;
+  int direct_out;      // 1: the main kernel writes the normalised output
+  int launch_combine;  // host side: follow the main kernel with the combine
   float* ws_o;  // [B*C*Hq][S][D]
   float* ws_m;  // [B*C*Hq][S]
   float* ws_l;  // [B*C*Hq][S]
@@ -285,7 +287,7 @@ __global__ __launch_bounds__(kGenThreads) void attn_generic_kernel(Params p) {
     const int fr = tile * kGenRT + r;
     if (fr >= n_rows) continue;
     const int i = fr / p.G, h = g * p.G + (fr - i * p.G);
-    if (p.num_splits == 1) {
+    if (p.direct_out) {
       const float l = l_s[r];
       store_out<T>(p, b, i, h, d, l > 0.0f ? acc[a] / l : 0.0f);
     } else {
@@ -531,7 +533,7 @@ __global__ __launch_bounds__(kDecThreads) void decode_mfma_kernel(Params p) {
 #pragma unroll
   for (int h = 0; h < G; ++h) {
     const int head = g * G + h;
-    if (S == 1) {
+    if (p.direct_out) {
       const float il = lh[h] > 0.0f ? 1.0f / lh[h] : 0.0f;
       vec8 ov;
 #pragma unroll
@@ -583,7 +585,6 @@ int prefill_splits(int B, int C, int Hkv, int G, int max_ctx, int page_size) {
 }
 
 size_t partial_bytes(int64_t rows, int S, int D) {
-  if (S <= 1) return 0;
   const size_t o = (size_t)rows * S * D * sizeof(float);
   const size_t ml = (size_t)rows * S * sizeof(float);
   return o + 2 * ((ml + 255) / 256 * 256);
@@ -612,7 +613,7 @@ int launch_generic(Params& p, hipStream_t stream) {
   dim3 grid(p.num_splits, tiles, p.B * p.Hkv);
   hipLaunchKernelGGL(attn_generic_kernel<T>, grid, dim3(kGenThreads), lds, stream, p);
   if (check_launch("fog attention (generic)") != KESSIE_OK) return KESSIE_ERR_HIP;
-  if (p.num_splits > 1) {
+  if (!p.direct_out && p.launch_combine) {
     const int64_t rows = (int64_t)p.B * p.C * p.Hq;
     hipLaunchKernelGGL(combine_kernel<T>, dim3((unsigned)rows), dim3(kCombineThreads), 0, stream, p);
     return check_launch("fog attention (combine)");
@@ -629,7 +630,7 @@ int launch_decode_mfma(Params& p, hipStream_t stream) {
   else
     hipLaunchKernelGGL((decode_mfma_kernel<T, G, 2>), grid, dim3(kDecThreads), 0, stream, p);
   if (check_launch("fog decode (mfma)") != KESSIE_OK) return KESSIE_ERR_HIP;
-  if (p.num_splits > 1) {
+  if (!p.direct_out && p.launch_combine) {
     const int64_t rows = (int64_t)p.B * p.Hq;
     hipLaunchKernelGGL(combine_kernel<T>, dim3((unsigned)rows), dim3(kCombineThreads), 0, stream, p);
     return check_launch("fog decode (combine)");
@@ -703,16 +704,17 @@ extern "C" size_t kessie_fog_decode_workspace_bytes(int batch, int num_q_heads, 
   return kessie::attn::partial_bytes((int64_t)batch * num_q_heads, S, head_dim);
 }
 
-extern "C" int kessie_fog_decode_paged(const void* q, const void* kv_pool, int num_pages, int64_t page_stride,
-                                       int64_t tok_stride, int64_t kv_stride, int64_t head_stride,
-                                       const int32_t* page_table, int64_t table_stride, const int32_t* ctx_lens,
-                                       const float* fog_vscale, int64_t fog_vscale_bstride, const float* fog_bias,
-                                       int64_t fog_bias_bstride, void* out, int batch, int num_q_heads,
-                                       int num_kv_heads, int head_dim, int page_size, int max_ctx, int window,
-                                       float sm_scale, int dtype, void* workspace, size_t workspace_bytes,
-                                       void* stream) {
-  using namespace kessie;
-  using namespace kessie::attn;
+namespace kessie {
+namespace attn {
+
+// Shared body of the decode entry points.  partials_only: write (m, l, o) per
+// split into the workspace and skip the combine.
+static int decode_entry(const void* q, const void* kv_pool, int num_pages, int64_t page_stride, int64_t tok_stride,
+                        int64_t kv_stride, int64_t head_stride, const int32_t* page_table, int64_t table_stride,
+                        const int32_t* ctx_lens, const float* fog_vscale, int64_t fog_vscale_bstride,
+                        const float* fog_bias, int64_t fog_bias_bstride, void* out, int batch, int num_q_heads,
+                        int num_kv_heads, int head_dim, int page_size, int max_ctx, int window, float sm_scale,
+                        int dtype, void* workspace, size_t workspace_bytes, void* stream, bool partials_only) {
   clear_error();
   Params p{};
   const int es = dtype_size(dtype);
@@ -720,7 +722,7 @@ extern "C" int kessie_fog_decode_paged(const void* q, const void* kv_pool, int n
   p.q_bs = (int64_t)num_q_heads * head_dim;
   p.q_is = 0;
   p.q_hs = head_dim;
-  p.out = out;
+  p.out = partials_only ? const_cast<void*>(q) : out;  // validated non-null; never written in that mode
   p.o_bs = p.q_bs;
   p.o_is = 0;
   p.o_hs = head_dim;
@@ -756,8 +758,10 @@ extern "C" int kessie_fog_decode_paged(const void* q, const void* kv_pool, int n
   KESSIE_REQUIRE(kv_stride >= 0, KESSIE_ERR_INVALID, "fog decode: kv_stride %lld", (long long)kv_stride);
   if (batch == 0) return KESSIE_OK;
   p.num_splits = decode_splits(batch, num_kv_heads, max_ctx, page_size);
-  const size_t need = partial_bytes((int64_t)batch * num_q_heads, p.num_splits, head_dim);
-  if (need > 0) {
+  p.direct_out = (!partials_only && p.num_splits == 1) ? 1 : 0;
+  p.launch_combine = partials_only ? 0 : 1;
+  if (!p.direct_out) {
+    const size_t need = partial_bytes((int64_t)batch * num_q_heads, p.num_splits, head_dim);
     KESSIE_REQUIRE(workspace != nullptr && workspace_bytes >= need, KESSIE_ERR_WORKSPACE,
                    "fog decode: workspace of %zu bytes needed, got %zu", need, workspace_bytes);
     KESSIE_REQUIRE(aligned16(workspace), KESSIE_ERR_INVALID, "fog decode: workspace not 16-byte aligned");
@@ -768,6 +772,85 @@ extern "C" int kessie_fog_decode_paged(const void* q, const void* kv_pool, int n
     return dtype == KESSIE_DTYPE_BF16 ? run_decode_mfma<bf16_t>(p, s) : run_decode_mfma<f16_t>(p, s);
   }
   return run_generic(dtype, p, s);
+}
+
+}  // namespace attn
+}  // namespace kessie
+
+extern "C" int kessie_fog_decode_paged(const void* q, const void* kv_pool, int num_pages, int64_t page_stride,
+                                       int64_t tok_stride, int64_t kv_stride, int64_t head_stride,
+                                       const int32_t* page_table, int64_t table_stride, const int32_t* ctx_lens,
+                                       const float* fog_vscale, int64_t fog_vscale_bstride, const float* fog_bias,
+                                       int64_t fog_bias_bstride, void* out, int batch, int num_q_heads,
+                                       int num_kv_heads, int head_dim, int page_size, int max_ctx, int window,
+                                       float sm_scale, int dtype, void* workspace, size_t workspace_bytes,
+                                       void* stream) {
+  return kessie::attn::decode_entry(q, kv_pool, num_pages, page_stride, tok_stride, kv_stride, head_stride,
+                                    page_table, table_stride, ctx_lens, fog_vscale, fog_vscale_bstride, fog_bias,
+                                    fog_bias_bstride, out, batch, num_q_heads, num_kv_heads, head_dim, page_size,
+                                    max_ctx, window, sm_scale, dtype, workspace, workspace_bytes, stream, false);
+}
+
+extern "C" int kessie_fog_decode_partials(const void* q, const void* kv_pool, int num_pages, int64_t page_stride,
+                                          int64_t tok_stride, int64_t kv_stride, int64_t head_stride,
+                                          const int32_t* page_table, int64_t table_stride, const int32_t* ctx_lens,
+                                          const float* fog_vscale, int64_t fog_vscale_bstride,
+                                          const float* fog_bias, int64_t fog_bias_bstride, int batch,
+                                          int num_q_heads, int num_kv_heads, int head_dim, int page_size,
+                                          int max_ctx, int window, float sm_scale, int dtype, void* workspace,
+                                          size_t workspace_bytes, void* stream) {
+  return kessie::attn::decode_entry(q, kv_pool, num_pages, page_stride, tok_stride, kv_stride, head_stride,
+                                    page_table, table_stride, ctx_lens, fog_vscale, fog_vscale_bstride, fog_bias,
+                                    fog_bias_bstride, nullptr, batch, num_q_heads, num_kv_heads, head_dim,
+                                    page_size, max_ctx, window, sm_scale, dtype, workspace, workspace_bytes, stream,
+                                    true);
+}
+
+extern "C" int kessie_fog_decode_num_splits(int batch, int num_kv_heads, int max_ctx, int page_size) {
+  if (batch <= 0 || num_kv_heads <= 0) return 0;
+  return kessie::attn::decode_splits(batch, num_kv_heads, max_ctx, page_size);
+}
+
+extern "C" int kessie_fog_decode_combine(const void* workspace, size_t workspace_bytes, void* out, int batch,
+                                         int num_q_heads, int num_kv_heads, int head_dim, int max_ctx,
+                                         int page_size, int dtype, void* stream) {
+  using namespace kessie;
+  using namespace kessie::attn;
+  clear_error();
+  KESSIE_REQUIRE(batch >= 0 && num_q_heads > 0 && num_kv_heads > 0 && head_dim > 0, KESSIE_ERR_INVALID,
+                 "fog decode combine: bad sizes");
+  KESSIE_REQUIRE(dtype_size(dtype) > 0, KESSIE_ERR_UNSUPPORTED, "fog decode combine: dtype %d", dtype);
+  if (batch == 0) return KESSIE_OK;
+  KESSIE_REQUIRE(out != nullptr, KESSIE_ERR_INVALID, "fog decode combine: null output");
+  Params p{};
+  p.out = out;
+  p.o_bs = (int64_t)num_q_heads * head_dim;
+  p.o_is = 0;
+  p.o_hs = head_dim;
+  p.B = batch;
+  p.C = 1;
+  p.Hq = num_q_heads;
+  p.Hkv = num_kv_heads;
+  p.D = head_dim;
+  p.num_splits = decode_splits(batch, num_kv_heads, max_ctx, page_size);
+  const int64_t rows = (int64_t)batch * num_q_heads;
+  const size_t need = partial_bytes(rows, p.num_splits, head_dim);
+  KESSIE_REQUIRE(workspace != nullptr && workspace_bytes >= need, KESSIE_ERR_WORKSPACE,
+                 "fog decode combine: workspace of %zu bytes needed, got %zu", need, workspace_bytes);
+  carve_workspace(p, const_cast<void*>(workspace), rows);
+  hipStream_t s = as_stream(stream);
+  switch (dtype) {
+    case KESSIE_DTYPE_F32:
+      hipLaunchKernelGGL(combine_kernel<float>, dim3((unsigned)rows), dim3(kCombineThreads), 0, s, p);
+      break;
+    case KESSIE_DTYPE_BF16:
+      hipLaunchKernelGGL(combine_kernel<bf16_t>, dim3((unsigned)rows), dim3(kCombineThreads), 0, s, p);
+      break;
+    default:
+      hipLaunchKernelGGL(combine_kernel<f16_t>, dim3((unsigned)rows), dim3(kCombineThreads), 0, s, p);
+      break;
+  }
+  return check_launch("fog decode combine");
 }
 
 extern "C" size_t kessie_fog_prefill_workspace_bytes(int batch, int num_q_tokens, int num_q_heads, int num_kv_heads,
@@ -833,9 +916,11 @@ extern "C" int kessie_fog_prefill_paged(const void* q, const void* kv_pool, int 
   KESSIE_REQUIRE(kv_stride >= 0, KESSIE_ERR_INVALID, "fog prefill: kv_stride %lld", (long long)kv_stride);
   if (batch == 0) return KESSIE_OK;
   p.num_splits = prefill_splits(batch, num_q_tokens, num_kv_heads, p.G, max_ctx, page_size);
+  p.direct_out = p.num_splits == 1 ? 1 : 0;
+  p.launch_combine = 1;
   const int64_t rows = (int64_t)batch * num_q_tokens * num_q_heads;
   const size_t need = partial_bytes(rows, p.num_splits, head_dim);
-  if (need > 0) {
+  if (!p.direct_out) {
     KESSIE_REQUIRE(workspace != nullptr && workspace_bytes >= need, KESSIE_ERR_WORKSPACE,
                    "fog prefill: workspace of %zu bytes needed, got %zu", need, workspace_bytes);
     KESSIE_REQUIRE(aligned16(workspace), KESSIE_ERR_INVALID, "fog prefill: workspace not 16-byte aligned");
@@ -883,6 +968,8 @@ static void dense_fp16(const void* Q, const void* K, const void* V, void* O, con
   p.causal = causal ? 1 : 0;
   p.sm_scale = sm_scale;
   p.num_splits = 1;
+  p.direct_out = 1;
+  p.launch_combine = 0;
   if (D != 64 && D != 128) {
     set_error(KESSIE_ERR_UNSUPPORTED, "dense attention: head_dim=%d unsupported (64 or 128)", D);
     return;

@@ -192,6 +192,53 @@ def fog_decode(q: torch.Tensor, pool: torch.Tensor, page_table: torch.Tensor, ct
     return out
 
 
+def decode_num_splits(batch: int, num_kv_heads: int, max_ctx: int, page_size: int) -> int:
+    return _lib.load().kessie_fog_decode_num_splits(batch, num_kv_heads, max_ctx, page_size)
+
+
+def fog_decode_partials(q: torch.Tensor, pool: torch.Tensor, page_table: torch.Tensor, ctx_lens: torch.Tensor,
+                        max_ctx: int, ws: torch.Tensor, fog_vscale: Optional[torch.Tensor] = None,
+                        fog_bias: Optional[torch.Tensor] = None, window: int = 0,
+                        sm_scale: Optional[float] = None, layout: str = "native", stream=None) -> torch.Tensor:
+    """The streaming half of fog_decode: per-split (m, l, o) partials into ``ws``
+    (layout in include/kessie_mi355x.h).  Returns ws."""
+    pv = pool_view(pool, layout)
+    q = _contig(q, "q")
+    b, hq, d = q.shape
+    if d != pv.head_dim or q.dtype != pool.dtype:
+        raise ValueError("q and pool disagree on head_dim or dtype")
+    if page_table.dtype != torch.int32 or ctx_lens.dtype != torch.int32:
+        raise TypeError("page_table and ctx_lens must be int32")
+    if page_table.dim() != 2 or page_table.shape[0] != b or page_table.stride(1) != 1:
+        raise ValueError("page_table must be [B, W] with contiguous rows")
+    if max_ctx > page_table.shape[1] * pv.page_size:
+        raise ValueError(f"max_ctx={max_ctx} exceeds the page table's {page_table.shape[1]} pages")
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(d)
+    vs, vs_bs = _fog_arg(fog_vscale, b, "fog_vscale", max_ctx)
+    bi, bi_bs = _fog_arg(fog_bias, b, "fog_bias", max_ctx)
+    lib = _lib.load()
+    _lib.check("kessie_fog_decode_partials", lib.kessie_fog_decode_partials(
+        _ptr(q), C.c_void_p(pv.k_ptr), pv.num_pages, pv.page_stride, pv.tok_stride, pv.kv_stride,
+        pv.head_stride, _ptr(page_table), page_table.stride(0), _ptr(ctx_lens), _ptr(vs), vs_bs,
+        _ptr(bi), bi_bs, b, hq, pv.num_kv_heads, d, pv.page_size, int(max_ctx), int(window),
+        float(sm_scale), dtype_code(q.dtype), _ptr(ws), ws.numel() * ws.element_size(),
+        _stream_ptr(stream, q.device)))
+    return ws
+
+
+def fog_decode_combine(ws: torch.Tensor, out: torch.Tensor, num_kv_heads: int, max_ctx: int, page_size: int,
+                       stream=None) -> torch.Tensor:
+    """Merge the partials of fog_decode_partials into out [B, Hq, D]."""
+    out = _contig(out, "out")
+    b, hq, d = out.shape
+    lib = _lib.load()
+    _lib.check("kessie_fog_decode_combine", lib.kessie_fog_decode_combine(
+        _ptr(ws), ws.numel() * ws.element_size(), _ptr(out), b, hq, num_kv_heads, d, int(max_ctx),
+        int(page_size), dtype_code(out.dtype), _stream_ptr(stream, out.device)))
+    return out
+
+
 def fog_prefill(q: torch.Tensor, pool: torch.Tensor, page_table: torch.Tensor, ctx_lens: torch.Tensor,
                 max_ctx: int, fog_vscale: Optional[torch.Tensor] = None,
                 fog_bias: Optional[torch.Tensor] = None, window: int = 0, causal: bool = True,
