@@ -15,9 +15,8 @@
 //                 one (sequence, split) x 8 kv heads, one wave per kv head; a
 //                 wave streams its kv head's 256-byte K and V rows of every
 //                 page in its split with 16-byte loads (register prefetch of
-//                 PREF pages), QK^T on MFMA 16x16x32 (A = 16 tokens of K,
-//                 B = the GQA query rows), online softmax with cross-lane
-//                 shuffles, PV on the VALU in fp32.
+//                 PREF pages); QK^T and PV both on MFMA (P in the input
+//                 dtype, accumulation in fp32), V transposed through LDS.
 //   attn_generic  any dtype / head_dim <= 256 / page size / GQA ratio: K and
 //                 V tiles staged in LDS as fp32, one workgroup per
 //                 (row tile, kv head, sequence, split).  Serves fp32 decode,
@@ -346,39 +345,82 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(Params p) {
 
 // ---------------------------------------------------------------------------
 // MFMA decode (bf16 / f16, head_dim 128, 16-token pages)
+//
+// One workgroup = (split of one sequence's pages) x 8 kv heads, one wave per
+// kv head, no workgroup barriers.  Per page a wave:
+//   * loads its kv head's K rows (16 tokens x 256 B) straight into the A
+//     operand layout of MFMA 16x16x32 (lane = token l%16, 16 bytes of d), and
+//     its V rows with 16-byte loads (lane group q = tokens 4q..4q+3, chunk
+//     l%16), PREF pages ahead in registers;
+//   * S^T = K Q^T on MFMA (B operand = the GQA group's query rows, head =
+//     column l%16).  The accumulator layout puts head l%16's scores for tokens
+//     4q..4q+3 in lane l, so the online softmax is lane-local plus two
+//     cross-row reductions, and p (times the fog weight) is already the B
+//     operand layout of MFMA 16x16x16 for PV -- no shuffles;
+//   * V goes through a per-wave LDS tile (row stride 272 B: the four token
+//     rows a read touches land on different banks) and is read back
+//     transposed as the A operand: O^T[d][h] += V^T[d][t] P^T[t][h];
+//   * the O^T accumulators are rescaled only when some head's running max
+//     moved on that page.
 // ---------------------------------------------------------------------------
-constexpr int kDecWaves = 8;  // kv heads per workgroup
-constexpr int kDecThreads = kDecWaves * 64;
+constexpr int kDecWaves = 8;     // kv heads (waves) per decode workgroup
+constexpr int kVRow = 128 + 8;  // LDS row stride of the V and Q tiles (elements)
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
 
 template <typename T>
 struct Mfma;
 template <>
 struct Mfma<bf16_t> {
   typedef bf16x8 vec8;
-  static __device__ __forceinline__ f32x4 mma(vec8 a, vec8 b, f32x4 c) {
+  typedef bf16x4 vec4;
+  static __device__ __forceinline__ f32x4 mma32(vec8 a, vec8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4 mma16(vec4 a, vec4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a), __builtin_bit_cast(s16x4, b), c,
+                                                     0, 0, 0);
   }
 };
 template <>
 struct Mfma<f16_t> {
   typedef f16x8 vec8;
-  static __device__ __forceinline__ f32x4 mma(vec8 a, vec8 b, f32x4 c) {
+  typedef f16x4 vec4;
+  static __device__ __forceinline__ f32x4 mma32(vec8 a, vec8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4 mma16(vec4 a, vec4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
   }
 };
 
-template <typename T, int G, int PREF>
-__global__ __launch_bounds__(kDecThreads) void decode_mfma_kernel(Params p) {
+// Orders this wave's LDS writes before its later LDS reads (and the reads of
+// one page before the writes of the next): wait for outstanding LDS traffic
+// and keep the compiler from moving LDS accesses across.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <typename T, int G, int PREF, int W>
+// Four waves per SIMD (128 VGPRs): two 8-wave workgroups share a CU.
+__global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4, 4))) void decode_mfma_kernel(Params p) {
   typedef typename Mfma<T>::vec8 vec8;
+  typedef typename Mfma<T>::vec4 vec4;
+  __shared__ __align__(16) T vtile_all[W][16 * kVRow];
+  __shared__ __align__(16) T qtile_all[W][16 * kVRow];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int g = blockIdx.z * kDecWaves + wave;
+  const int g = blockIdx.z * W + wave;
   if (g >= p.Hkv) return;  // no workgroup barriers below
+  T* vtile = vtile_all[wave];
+  T* qtile = qtile_all[wave];
   const int b = blockIdx.y;
   const int split = blockIdx.x;
   const int S = p.num_splits;
-  const int row = lane & 15;  // MFMA row/column index; chunk index in PV
-  const int grp = lane >> 4;  // lane group: k-block slot / token quad
+  const int row = lane & 15;  // MFMA row / column index: token (K rows), head (scores), d (O^T)
+  const int grp = lane >> 4;  // lane group: k-block slot, token quad
 
   const int ctx = seq_ctx(p, b);
   const int lo = p.window > 0 ? max(0, ctx - p.window) : 0;
@@ -392,28 +434,32 @@ __global__ __launch_bounds__(kDecThreads) void decode_mfma_kernel(Params p) {
   const T* vbase = static_cast<const T*>(p.v) + (int64_t)g * p.head_stride;
   const int32_t* table = p.page_table + (int64_t)b * p.table_stride;
   const int64_t ts = p.tok_stride;
+  const int64_t koff = (int64_t)row * ts + 8 * grp;        // + 32*kb
+  const int64_t voff = (int64_t)(4 * grp) * ts + 8 * row;  // + i*ts
 
-  // B operand: query rows of this kv head's GQA group (column = head).
-  vec8 qv[4];
+  // B operand of S^T = K Q^T: the GQA group's query rows (column = head),
+  // kept in this wave's LDS tile (zero rows past G) and read per page, which
+  // leaves the registers to the page prefetch.
   {
     const T* qrow = static_cast<const T*>(p.q) + (int64_t)b * p.q_bs + (int64_t)(g * G + row) * p.q_hs;
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
+      vec8 x;
       if (row < G) {
-        qv[kb] = *reinterpret_cast<const vec8*>(qrow + 32 * kb + 8 * grp);
+        x = *reinterpret_cast<const vec8*>(qrow + 32 * kb + 8 * grp);
       } else {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) qv[kb][e] = static_cast<T>(0.0f);
+        for (int e = 0; e < 8; ++e) x[e] = static_cast<T>(0.0f);
       }
+      *reinterpret_cast<vec8*>(qtile + row * kVRow + 32 * kb + 8 * grp) = x;
     }
+    wave_lds_sync();
   }
 
-  float o[G][8];
+  f32x4 oacc[8];  // O^T[d = 16*blk + 4*grp + i][head = row]
 #pragma unroll
-  for (int h = 0; h < G; ++h)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) o[h][e] = 0.0f;
-  float m_run = kNegInf, l_run = 0.0f;
+  for (int blk = 0; blk < 8; ++blk) oacc[blk] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  float m_run = kNegInf, l_run = 0.0f;  // softmax state of head `row`
 
   vec8 kreg[PREF][4], vreg[PREF][4];
   int pid_s[PREF];
@@ -425,9 +471,9 @@ __global__ __launch_bounds__(kDecThreads) void decode_mfma_kernel(Params p) {
       const T* kp = kbase + (int64_t)pid * p.page_stride;
       const T* vp = vbase + (int64_t)pid * p.page_stride;
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb) kreg[st][kb] = *reinterpret_cast<const vec8*>(kp + row * ts + 32 * kb + 8 * grp);
+      for (int kb = 0; kb < 4; ++kb) kreg[st][kb] = *reinterpret_cast<const vec8*>(kp + koff + 32 * kb);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) vreg[st][i] = *reinterpret_cast<const vec8*>(vp + (4 * grp + i) * ts + 8 * row);
+      for (int i = 0; i < 4; ++i) vreg[st][i] = *reinterpret_cast<const vec8*>(vp + voff + i * ts);
     }
   };
 
@@ -441,26 +487,27 @@ __global__ __launch_bounds__(kDecThreads) void decode_mfma_kernel(Params p) {
       const int lp = base + st;
       if (lp >= p1) break;
       const int pid = pid_s[st];
-      const bool page_ok = pid >= 0 && pid < p.num_pages;
+      if (pid < 0 || pid >= p.num_pages) {  // masked page: contributes nothing
+        if (lp + PREF < p1) issue(st, lp + PREF);
+        continue;
+      }
       const int t_page = lp << 4;
-      // Token (of this lane's score slots and V rows) = t_page + 4*grp + i.
-      const bool full = page_ok && t_page >= lo && t_page + 16 <= ctx;
+      const bool full = t_page >= lo && t_page + 16 <= ctx;
+      // Scores: lane (grp, row) holds head `row`, tokens t_page + 4*grp + i.
+      f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        const vec8 qv = *reinterpret_cast<const vec8*>(qtile + row * kVRow + 32 * kb + 8 * grp);
+        acc = Mfma<T>::mma32(kreg[st][kb], qv, acc);
+      }
       float sc[4];
-      if (page_ok) {
-        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) acc = Mfma<T>::mma(kreg[st][kb], qv[kb], acc);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int t = t_page + 4 * grp + i;
-          const bool ok = full || (t >= lo && t < ctx);
-          float s = acc[i] * p.sm_scale;
-          if (p.bias && ok) s += p.bias[(int64_t)b * p.bias_bs + t];
-          sc[i] = ok ? s : kNegInf;
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) sc[i] = kNegInf;
+      for (int i = 0; i < 4; ++i) {
+        const int t = t_page + 4 * grp + i;
+        const bool ok = full || (t >= lo && t < ctx);
+        float s = acc[i] * p.sm_scale;
+        if (p.bias && ok) s += p.bias[(int64_t)b * p.bias_bs + t];
+        sc[i] = ok ? s : kNegInf;
       }
       float mloc = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
       mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
@@ -485,70 +532,60 @@ __global__ __launch_bounds__(kDecThreads) void decode_mfma_kernel(Params p) {
           pr[i] = (pr[i] != 0.0f) ? pr[i] * p.vscale[(int64_t)b * p.vs_bs + t] : 0.0f;
         }
       }
-      // PV: lane (grp, chunk=row) accumulates tokens 4*grp+i, d = 8*row..+7.
-      const int src0 = lane & 48;
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
 #pragma unroll
-      for (int h = 0; h < G; ++h) {
-        const float ah = __shfl(alpha, src0 | h);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o[h][e] *= ah;
+        for (int blk = 0; blk < 8; ++blk) oacc[blk] *= alpha;
       }
-      if (page_ok) {
+      // V rows of this lane's token quad -> LDS tile (masked tokens as zeros).
+      if (!full) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          float vf[8];
           const int t = t_page + 4 * grp + i;
-          const bool ok = full || (t >= lo && t < ctx);
+          if (!(t >= lo && t < ctx)) {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) vf[e] = ok ? to_f32(vreg[st][i][e]) : 0.0f;
-#pragma unroll
-          for (int h = 0; h < G; ++h) {
-            const float ph = __shfl(pr[i], src0 | h);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) o[h][e] += ph * vf[e];
+            for (int e = 0; e < 8; ++e) vreg[st][i][e] = static_cast<T>(0.0f);
           }
         }
+      }
+      wave_lds_sync();  // the previous page's transposed reads are done
+#pragma unroll
+      for (int i = 0; i < 4; ++i) *reinterpret_cast<vec8*>(vtile + (4 * grp + i) * kVRow + 8 * row) = vreg[st][i];
+      wave_lds_sync();
+      vec4 pb;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) pb[i] = static_cast<T>(pr[i]);
+#pragma unroll
+      for (int blk = 0; blk < 8; ++blk) {
+        vec4 va;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) va[i] = vtile[(4 * grp + i) * kVRow + 16 * blk + row];
+        oacc[blk] = Mfma<T>::mma16(va, pb, oacc[blk]);
       }
       if (lp + PREF < p1) issue(st, lp + PREF);
     }
   }
 
-  // Reduce the four token quads.
+  // Lane (grp, row) holds head `row`, d = 16*blk + 4*grp + i.
+  if (row >= G) return;
+  const int head = g * G + row;
+  if (p.direct_out) {
+    const float il = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+    T* dst = static_cast<T*>(p.out) + (int64_t)b * p.o_bs + (int64_t)head * p.o_hs + 4 * grp;
 #pragma unroll
-  for (int h = 0; h < G; ++h)
+    for (int blk = 0; blk < 8; ++blk) {
+      vec4 ov;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float x = o[h][e];
-      x += __shfl_xor(x, 16);
-      x += __shfl_xor(x, 32);
-      o[h][e] = x;
+      for (int i = 0; i < 4; ++i) ov[i] = from_f32<T>(oacc[blk][i] * il);
+      *reinterpret_cast<vec4*>(dst + 16 * blk) = ov;
     }
-  float mh[G], lh[G];
+  } else {
+    const int64_t r = row_id(p, b, 0, head);
+    float* dst = p.ws_o + (r * S + split) * 128 + 4 * grp;
 #pragma unroll
-  for (int h = 0; h < G; ++h) {
-    mh[h] = __shfl(m_run, h);
-    lh[h] = __shfl(l_run, h);
-  }
-  if (grp != 0) return;
-#pragma unroll
-  for (int h = 0; h < G; ++h) {
-    const int head = g * G + h;
-    if (p.direct_out) {
-      const float il = lh[h] > 0.0f ? 1.0f / lh[h] : 0.0f;
-      vec8 ov;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) ov[e] = from_f32<T>(o[h][e] * il);
-      T* dst = static_cast<T*>(p.out) + (int64_t)b * p.o_bs + (int64_t)head * p.o_hs + 8 * row;
-      *reinterpret_cast<vec8*>(dst) = ov;
-    } else {
-      const int64_t r = row_id(p, b, 0, head);
-      float* dst = p.ws_o + (r * S + split) * 128 + 8 * row;
-      *reinterpret_cast<f32x4*>(dst) = f32x4{o[h][0], o[h][1], o[h][2], o[h][3]};
-      *reinterpret_cast<f32x4*>(dst + 4) = f32x4{o[h][4], o[h][5], o[h][6], o[h][7]};
-      if (row == 0) {
-        p.ws_m[r * S + split] = mh[h];
-        p.ws_l[r * S + split] = lh[h];
-      }
+    for (int blk = 0; blk < 8; ++blk) *reinterpret_cast<f32x4*>(dst + 16 * blk) = oacc[blk];
+    if (grp == 0) {
+      p.ws_m[r * S + split] = m_run;
+      p.ws_l[r * S + split] = l_run;
     }
   }
 }
@@ -623,12 +660,10 @@ int launch_generic(Params& p, hipStream_t stream) {
 
 template <typename T, int G>
 int launch_decode_mfma(Params& p, hipStream_t stream) {
+  // 8 kv heads per workgroup, two pages in flight per wave (deeper prefetch
+  // does not fit the 128 VGPRs that let two workgroups share a CU).
   dim3 grid(p.num_splits, p.B, div_up(p.Hkv, kDecWaves));
-  const int pref = env_int("KESSIE_DECODE_PREFETCH", 2);
-  if (pref >= 3)
-    hipLaunchKernelGGL((decode_mfma_kernel<T, G, 3>), grid, dim3(kDecThreads), 0, stream, p);
-  else
-    hipLaunchKernelGGL((decode_mfma_kernel<T, G, 2>), grid, dim3(kDecThreads), 0, stream, p);
+  hipLaunchKernelGGL((decode_mfma_kernel<T, G, 2, kDecWaves>), grid, dim3(kDecWaves * 64), 0, stream, p);
   if (check_launch("fog decode (mfma)") != KESSIE_OK) return KESSIE_ERR_HIP;
   if (!p.direct_out && p.launch_combine) {
     const int64_t rows = (int64_t)p.B * p.Hq;

@@ -15,6 +15,7 @@
 // counters whose value does not depend on order (histograms, the legacy
 // evict count).
 #include <climits>
+#include <cstdlib>
 
 #include "common.h"
 
@@ -160,9 +161,16 @@ __global__ __launch_bounds__(kThreads) void mark_evicted_kernel(const int32_t* l
 
 // ---------------------------------------------------------------------------
 // Radix select (one workgroup): the key of rank k-1 among valid pages.
+// Keys are 64-bit (ordered score << 32 | page id), so they are unique and the
+// k smallest form exactly the set the total order (score, id) puts first.
+// Passes 0-3 resolve the ordered score a byte at a time, passes 4-7 the page
+// id among keys whose score equals the resolved one, in 32-bit arithmetic.
+// Each pass streams scores/valid from L2 in batches of kSelBatch independent
+// loads per thread, so a pass costs a couple of round trips, not one per key.
 // ---------------------------------------------------------------------------
 constexpr int kSelThreads = 1024;
 constexpr int kSelWaves = kSelThreads / 64;
+constexpr int kSelBatch = 32;
 
 struct SelectOut {
   unsigned long long key_thr;  // largest evicted key
@@ -170,20 +178,65 @@ struct SelectOut {
   int n_valid;
 };
 
-__global__ __launch_bounds__(kSelThreads) void radix_select_kernel(const float* scores, const int8_t* valid,
-                                                                   int n, int k_evict, float evict_fraction,
+__device__ __forceinline__ uint32_t ordered_score(float s) {
+  if (s == 0.0f) s = 0.0f;  // -0 == +0
+  const uint32_t bits = __float_as_uint(s);
+  return (bits & 0x80000000u) ? ~bits : (bits | 0x80000000u);
+}
+
+// Wave 0: the digit whose cumulative count range holds `rank`; 4 bins a lane.
+__device__ __forceinline__ void pick_digit(const int* tot, int rank, int* s_digit, int* s_rank) {
+  const int lane = threadIdx.x;
+  const int c0 = tot[4 * lane], c1 = tot[4 * lane + 1], c2 = tot[4 * lane + 2], c3 = tot[4 * lane + 3];
+  const int sum = c0 + c1 + c2 + c3;
+  int incl = sum;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += y;
+  }
+  const int excl = incl - sum;
+  if (rank >= excl && rank < incl) {
+    int r = rank - excl, d = 4 * lane;
+    if (r >= c0) {
+      r -= c0;
+      ++d;
+      if (r >= c1) {
+        r -= c1;
+        ++d;
+        if (r >= c2) {
+          r -= c2;
+          ++d;
+        }
+      }
+    }
+    *s_digit = d;
+    *s_rank = r;
+  }
+}
+
+__global__ __launch_bounds__(kSelThreads) void radix_select_kernel(const float* __restrict__ scores,
+                                                                   const int8_t* __restrict__ valid, int n,
+                                                                   int k_evict, float evict_fraction,
                                                                    SelectOut* out) {
   __shared__ int hist[kSelWaves][256];
   __shared__ int tot[256];
-  __shared__ int s_digit, s_rank;
-  __shared__ int s_nvalid;
+  __shared__ int s_digit, s_rank, s_nvalid;
   const int tid = threadIdx.x, wave = tid >> 6;
 
-  // Count valid pages.
   if (tid == 0) s_nvalid = 0;
   __syncthreads();
   int c = 0;
-  for (int i = tid; i < n; i += kSelThreads) c += valid[i] == 1;
+  for (int b0 = 0; b0 < n; b0 += kSelBatch * kSelThreads) {
+    int8_t vv[kSelBatch];
+#pragma unroll
+    for (int j = 0; j < kSelBatch; ++j) {
+      const int i = b0 + j * kSelThreads + tid;
+      vv[j] = i < n ? valid[i] : (int8_t)0;
+    }
+#pragma unroll
+    for (int j = 0; j < kSelBatch; ++j) c += vv[j] == 1;
+  }
   for (int o = 32; o >= 1; o >>= 1) c += __shfl_xor(c, o, 64);
   if ((tid & 63) == 0) atomicAdd(&s_nvalid, c);
   __syncthreads();
@@ -204,41 +257,58 @@ __global__ __launch_bounds__(kSelThreads) void radix_select_kernel(const float* 
     }
     return;
   }
-  unsigned long long prefix = 0;  // digits resolved so far (high bits)
+  uint32_t pre_s = 0, pre_i = 0;  // resolved high bits of score / id
   int rank = (int)k - 1;          // rank of the wanted key among candidates
   for (int pass = 0; pass < 8; ++pass) {
-    const int shift = 56 - 8 * pass;
+    const bool id_pass = pass >= 4;
+    const int sh = 24 - 8 * (pass & 3);  // digit shift within the 32-bit half
     for (int e = tid; e < kSelWaves * 256; e += kSelThreads) (&hist[0][0])[e] = 0;
     __syncthreads();
-    for (int i = tid; i < n; i += kSelThreads) {
-      if (valid[i] != 1) continue;
-      const unsigned long long key = score_key(scores[i], i);
-      const bool match = (pass == 0) || ((key >> (shift + 8)) == prefix);
-      if (match) atomicAdd(&hist[wave][(key >> shift) & 255], 1);
+    for (int b0 = 0; b0 < n; b0 += kSelBatch * kSelThreads) {
+      float sc[kSelBatch];
+      int8_t vv[kSelBatch];
+#pragma unroll
+      for (int j = 0; j < kSelBatch; ++j) {
+        const int i = b0 + j * kSelThreads + tid;
+        vv[j] = i < n ? valid[i] : (int8_t)0;
+        sc[j] = i < n ? scores[i] : 0.0f;
+      }
+#pragma unroll
+      for (int j = 0; j < kSelBatch; ++j) {
+        if (vv[j] != 1) continue;
+        const uint32_t ks = ordered_score(sc[j]);
+        const uint32_t id = (uint32_t)(b0 + j * kSelThreads + tid);
+        bool match;
+        uint32_t digit;
+        if (!id_pass) {
+          match = (pass == 0) || ((ks >> (sh + 8)) == pre_s);
+          digit = (ks >> sh) & 255u;
+        } else {
+          match = (ks == pre_s) && (pass == 4 || (id >> (sh + 8)) == pre_i);
+          digit = (id >> sh) & 255u;
+        }
+        if (match) atomicAdd(&hist[wave][digit], 1);
+      }
     }
     __syncthreads();
     if (tid < 256) {
-      int s = 0;
-      for (int w = 0; w < kSelWaves; ++w) s += hist[w][tid];
-      tot[tid] = s;
+      int sum = 0;
+#pragma unroll
+      for (int w = 0; w < kSelWaves; ++w) sum += hist[w][tid];
+      tot[tid] = sum;
     }
     __syncthreads();
-    if (tid == 0) {
-      int cum = 0, d = 0;
-      for (; d < 256; ++d) {
-        if (cum + tot[d] > rank) break;
-        cum += tot[d];
-      }
-      s_digit = d;
-      s_rank = rank - cum;
-    }
+    if (wave == 0) pick_digit(tot, rank, &s_digit, &s_rank);
     __syncthreads();
-    prefix = (prefix << 8) | (unsigned long long)s_digit;
+    if (!id_pass)
+      pre_s = (pre_s << 8) | (uint32_t)s_digit;
+    else
+      pre_i = (pre_i << 8) | (uint32_t)s_digit;
     rank = s_rank;
     __syncthreads();
   }
   if (tid == 0) {
-    out->key_thr = prefix;
+    out->key_thr = ((unsigned long long)pre_s << 32) | pre_i;
     out->k = (int)k;
     out->n_valid = n_valid;
   }
@@ -318,30 +388,35 @@ __global__ __launch_bounds__(kThreads) void threshold_evict_kernel(int8_t* valid
 // Gather: whole-page byte copies, 16 bytes per lane.
 // ---------------------------------------------------------------------------
 constexpr int kGatherThreads = 256;
-constexpr int kGatherUnroll = 4;
 
+template <bool kNtLoad, bool kNtStore, int kUnroll>
 __global__ __launch_bounds__(kGatherThreads) void gather_kernel(const u32x4* __restrict__ src, int64_t page_vecs,
                                                                 const int32_t* __restrict__ idx,
                                                                 const int32_t* __restrict__ count_dev, int n,
                                                                 int num_pages, u32x4* __restrict__ dst) {
   const int cnt = count_dev ? min(n, *count_dev) : n;
-  const int64_t step = (int64_t)kGatherThreads * kGatherUnroll;
+  const int64_t step = (int64_t)kGatherThreads * kUnroll;
   for (int i = blockIdx.x; i < cnt; i += gridDim.x) {
     const int pid = idx[i];
     if (pid < 0 || pid >= num_pages) continue;
     const u32x4* s = src + (int64_t)pid * page_vecs;
     u32x4* d = dst + (int64_t)i * page_vecs;
     for (int64_t v0 = threadIdx.x; v0 < page_vecs; v0 += step) {
-      u32x4 r[kGatherUnroll];
+      u32x4 r[kUnroll];
 #pragma unroll
-      for (int u = 0; u < kGatherUnroll; ++u) {
+      for (int u = 0; u < kUnroll; ++u) {
         const int64_t v = v0 + (int64_t)u * kGatherThreads;
-        if (v < page_vecs) r[u] = __builtin_nontemporal_load(s + v);
+        if (v < page_vecs) r[u] = kNtLoad ? __builtin_nontemporal_load(s + v) : s[v];
       }
 #pragma unroll
-      for (int u = 0; u < kGatherUnroll; ++u) {
+      for (int u = 0; u < kUnroll; ++u) {
         const int64_t v = v0 + (int64_t)u * kGatherThreads;
-        if (v < page_vecs) __builtin_nontemporal_store(r[u], d + v);
+        if (v < page_vecs) {
+          if (kNtStore)
+            __builtin_nontemporal_store(r[u], d + v);
+          else
+            d[v] = r[u];
+        }
       }
     }
   }
@@ -702,10 +777,12 @@ extern "C" int kessie_page_gather(const void* src_pool, int64_t page_bytes, cons
   KESSIE_REQUIRE(src_pool && idx && dst, KESSIE_ERR_INVALID, "page gather: null pointer");
   KESSIE_REQUIRE(page_bytes % 16 == 0 && aligned16(src_pool) && aligned16(dst), KESSIE_ERR_UNSUPPORTED,
                  "page gather: page_bytes and pointers must be 16-byte multiples/aligned");
-  const int grid = min(n, 4096);
-  hipLaunchKernelGGL(gather_kernel, dim3(grid), dim3(kGatherThreads), 0, as_stream(stream),
-                     static_cast<const u32x4*>(src_pool), page_bytes / 16, idx, count_dev, n, num_pages,
-                     static_cast<u32x4*>(dst));
+  // One workgroup per page slot, non-temporal loads and stores (measured best
+  // among plain/non-temporal x unroll 4/8 x grid 1K..64K for 64 KiB pages).
+  const u32x4* s = static_cast<const u32x4*>(src_pool);
+  u32x4* d = static_cast<u32x4*>(dst);
+  hipLaunchKernelGGL((gather_kernel<true, true, 4>), dim3(n), dim3(kGatherThreads), 0, as_stream(stream), s,
+                     page_bytes / 16, idx, count_dev, n, num_pages, d);
   return check_launch("page gather");
 }
 

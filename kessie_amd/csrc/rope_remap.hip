@@ -60,7 +60,11 @@ struct Vec16<float> {
 };
 
 // Vectorised kernel: 16-byte chunks.  Requires half % N == 0, 16-byte aligned
-// rows and head starts.
+// rows and head starts.  The K chunks of a round are loaded into registers
+// before the cos/sin phase, so HBM latency overlaps the trigonometry; the
+// workgroup barrier that publishes cos/sin keeps those loads ahead of it.
+constexpr int kRemapItems = 4;  // chunk pairs per thread per round
+
 template <typename T>
 __global__ __launch_bounds__(kRemapThreads) void rope_remap_vec(
     T* __restrict__ pool, int64_t page_stride, int64_t tok_stride, int64_t head_stride,
@@ -74,49 +78,68 @@ __global__ __launch_bounds__(kRemapThreads) void rope_remap_vec(
 
   const int t0 = blockIdx.x * kRemapTile;
   const int ntok = min(kRemapTile, num_tokens - t0);
-  const int n_ang = ntok * half;
-  for (int i = threadIdx.x; i < n_ang; i += kRemapThreads) {
-    const int tt = i / half;
-    const int j = i - tt * half;
-    const int t = t0 + tt;
-    const float delta = (float)(tgt_pos[t] - orig_pos[t]);
-    const float ang = delta * inv_freq_at(inv_freq, theta, j, half);
-    float s, c;
-    sincosf(ang, &s, &c);
-    cs[i] = make_float2(c, s);
-  }
-  __syncthreads();
-
   const int chunks = half / N;  // chunk pairs per head
   const int per_tok = num_heads * chunks;
   const int n_work = ntok * per_tok;
-  for (int i = threadIdx.x; i < n_work; i += kRemapThreads) {
-    const int tt = i / per_tok;
-    const int r = i - tt * per_tok;
-    const int h = r / chunks;
-    const int c = r - h * chunks;
-    const int64_t row = token_row(t0 + tt, page_list, num_pages, page_size, page_stride, tok_stride);
-    if (row < 0) continue;
-    T* p1 = pool + row + (int64_t)h * head_stride + c * N;
-    T* p2 = p1 + half;
-    const V a = *reinterpret_cast<const V*>(p1);
-    const V b = *reinterpret_cast<const V*>(p2);
-    const float2* csr = cs + tt * half + c * N;
-    V y1, y2;
+
+  for (int round = 0; round * kRemapItems * kRemapThreads < n_work; ++round) {
+    const int base = round * kRemapItems * kRemapThreads;
+    V a[kRemapItems], b[kRemapItems];
+    T* p1[kRemapItems];
+    int csi[kRemapItems];
 #pragma unroll
-    for (int e = 0; e < N; ++e) {
-      const float2 q = csr[e];
-      const float x1 = to_f32(a[e]);
-      const float x2 = to_f32(b[e]);
-      const float u1 = x1 * q.x;
-      const float u2 = x2 * q.y;
-      const float w1 = x1 * q.y;
-      const float w2 = x2 * q.x;
-      y1[e] = from_f32<T>(u1 - u2);
-      y2[e] = from_f32<T>(w1 + w2);
+    for (int it = 0; it < kRemapItems; ++it) {
+      const int i = base + it * kRemapThreads + threadIdx.x;
+      p1[it] = nullptr;
+      csi[it] = 0;
+      if (i < n_work) {
+        const int tt = i / per_tok;
+        const int r = i - tt * per_tok;
+        const int h = r / chunks;
+        const int c = r - h * chunks;
+        const int64_t row = token_row(t0 + tt, page_list, num_pages, page_size, page_stride, tok_stride);
+        if (row >= 0) {
+          p1[it] = pool + row + (int64_t)h * head_stride + c * N;
+          a[it] = *reinterpret_cast<const V*>(p1[it]);
+          b[it] = *reinterpret_cast<const V*>(p1[it] + half);
+          csi[it] = tt * half + c * N;
+        }
+      }
     }
-    *reinterpret_cast<V*>(p1) = y1;
-    *reinterpret_cast<V*>(p2) = y2;
+    if (round == 0) {
+      const int n_ang = ntok * half;
+      for (int i = threadIdx.x; i < n_ang; i += kRemapThreads) {
+        const int tt = i / half;
+        const int j = i - tt * half;
+        const int t = t0 + tt;
+        const float delta = (float)(tgt_pos[t] - orig_pos[t]);
+        const float ang = delta * inv_freq_at(inv_freq, theta, j, half);
+        float s, c;
+        sincosf(ang, &s, &c);
+        cs[i] = make_float2(c, s);
+      }
+      __syncthreads();
+    }
+#pragma unroll
+    for (int it = 0; it < kRemapItems; ++it) {
+      if (p1[it] == nullptr) continue;
+      const float2* csr = cs + csi[it];
+      V y1, y2;
+#pragma unroll
+      for (int e = 0; e < N; ++e) {
+        const float2 q = csr[e];
+        const float x1 = to_f32(a[it][e]);
+        const float x2 = to_f32(b[it][e]);
+        const float u1 = x1 * q.x;
+        const float u2 = x2 * q.y;
+        const float w1 = x1 * q.y;
+        const float w2 = x2 * q.x;
+        y1[e] = from_f32<T>(u1 - u2);
+        y2[e] = from_f32<T>(w1 + w2);
+      }
+      *reinterpret_cast<V*>(p1[it]) = y1;
+      *reinterpret_cast<V*>(p1[it] + half) = y2;
+    }
   }
 }
 
