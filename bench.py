@@ -39,6 +39,14 @@ def events(n):
     return [torch.cuda.Event(enable_timing=True) for _ in range(n)]
 
 
+def backlog(ms: float = 5.0) -> None:
+    """Queue a GPU spin of ~ms before a timed loop, so the launches behind it
+    pile up and per-launch events time the kernels, not host launch gaps."""
+    import torch
+
+    torch.cuda._sleep(int(ms * 1e-3 * 2.4e9))
+
+
 def decode_bytes(b, ctx, hq, hkv, d, es, page_size, fog=True):
     pages = (ctx + page_size - 1) // page_size
     kv = b * ctx * hkv * d * 2 * es
@@ -116,6 +124,7 @@ def time_decode(s, steps, warmup):
     torch.cuda.synchronize()
     e0, e1 = events(steps), events(steps)
     start, end = events(2)
+    backlog()
     start.record()
     for i in range(steps):
         e0[i].record()
@@ -200,6 +209,7 @@ def bench_remap(dev, reps=20, sets=4, n_tok=65536, page_size=16, hkv=8, d=128, t
         ops.rope_remap_paged(pool, orig, tgt, theta, page_list=lists[i % sets])
     torch.cuda.synchronize()
     e0, e1 = events(reps), events(reps)
+    backlog()
     for i in range(reps):
         e0[i].record()
         ops.rope_remap_paged(pool, orig, tgt, theta, page_list=lists[i % sets])
@@ -264,6 +274,7 @@ def bench_gather_evict(dev, reps=5):
         pipeline()
     torch.cuda.synchronize()
     e0, e1, e2 = events(reps), events(reps), events(reps)
+    backlog()
     for i in range(reps):
         valid.fill_(1)
         e0[i].record()
@@ -299,6 +310,7 @@ def bench_decode_fp32(dev, reps=20):
         run_decode_step(s)
     torch.cuda.synchronize()
     e0, e1 = events(reps), events(reps)
+    backlog()
     for i in range(reps):
         e0[i].record()
         run_decode_step(s)

@@ -163,14 +163,21 @@ __global__ __launch_bounds__(kThreads) void mark_evicted_kernel(const int32_t* l
 // Radix select (one workgroup): the key of rank k-1 among valid pages.
 // Keys are 64-bit (ordered score << 32 | page id), so they are unique and the
 // k smallest form exactly the set the total order (score, id) puts first.
-// Passes 0-3 resolve the ordered score a byte at a time, passes 4-7 the page
-// id among keys whose score equals the resolved one, in 32-bit arithmetic.
-// Each pass streams scores/valid from L2 in batches of kSelBatch independent
-// loads per thread, so a pass costs a couple of round trips, not one per key.
+//   pass A  streams every page: counts the valid ones and histograms the top
+//           12 bits of the ordered score (4096 bins);
+//   pass B  streams again and copies the keys of the bucket holding rank k-1
+//           into LDS (up to kSelCap of them);
+//   then    the low 20 score bits (two 10-bit passes) and, when several
+//           candidates share that score, the page id (11+11+10 bits) are
+//           resolved on the LDS copy.
+// A bucket larger than kSelCap (heavily tied scores) takes the fallback: eight
+// byte-wide passes that each stream the pages again.  Streaming loads are
+// issued kSelBatch at a time per thread.  Histogram atomics only count.
 // ---------------------------------------------------------------------------
 constexpr int kSelThreads = 1024;
 constexpr int kSelWaves = kSelThreads / 64;
 constexpr int kSelBatch = 32;
+constexpr int kSelCap = 12288;  // candidate keys held in LDS
 
 struct SelectOut {
   unsigned long long key_thr;  // largest evicted key
@@ -184,8 +191,58 @@ __device__ __forceinline__ uint32_t ordered_score(float s) {
   return (bits & 0x80000000u) ? ~bits : (bits | 0x80000000u);
 }
 
-// Wave 0: the digit whose cumulative count range holds `rank`; 4 bins a lane.
-__device__ __forceinline__ void pick_digit(const int* tot, int rank, int* s_digit, int* s_rank) {
+// Exclusive scan of one int per thread across the 1024-thread block.
+__device__ __forceinline__ int sel_block_scan(int v, int* sm) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) sm[wave] = x;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int acc = 0;
+    for (int w = 0; w < kSelWaves; ++w) {
+      const int t = sm[w];
+      sm[w] = acc;
+      acc += t;
+    }
+  }
+  __syncthreads();
+  const int res = x - v + sm[wave];
+  __syncthreads();
+  return res;
+}
+
+// The bin of `bins[0..nb)` (nb = 1024, 2048 or 4096) whose cumulative count
+// range holds `rank`, and the rank within it; every thread must call.
+__device__ __forceinline__ void sel_pick(const int* bins, int nb, int rank, int* sm, int* s_digit, int* s_rank) {
+  const int per = nb / kSelThreads;
+  const int first = threadIdx.x * per;
+  int c[4] = {0, 0, 0, 0};
+  int sum = 0;
+  for (int j = 0; j < per; ++j) {
+    c[j] = bins[first + j];
+    sum += c[j];
+  }
+  const int excl = sel_block_scan(sum, sm);
+  if (rank >= excl && rank < excl + sum) {
+    int r = rank - excl, d = first;
+    for (int j = 0; j < per; ++j) {
+      if (r < c[j]) break;
+      r -= c[j];
+      ++d;
+    }
+    *s_digit = d;
+    *s_rank = r;
+  }
+  __syncthreads();
+}
+
+// Wave 0: the digit of a 256-bin histogram whose range holds `rank`.
+__device__ __forceinline__ void pick_digit256(const int* tot, int rank, int* s_digit, int* s_rank) {
   const int lane = threadIdx.x;
   const int c0 = tot[4 * lane], c1 = tot[4 * lane + 1], c2 = tot[4 * lane + 2], c3 = tot[4 * lane + 3];
   const int sum = c0 + c1 + c2 + c3;
@@ -219,23 +276,36 @@ __global__ __launch_bounds__(kSelThreads) void radix_select_kernel(const float* 
                                                                    const int8_t* __restrict__ valid, int n,
                                                                    int k_evict, float evict_fraction,
                                                                    SelectOut* out) {
-  __shared__ int hist[kSelWaves][256];
-  __shared__ int tot[256];
-  __shared__ int s_digit, s_rank, s_nvalid;
-  const int tid = threadIdx.x, wave = tid >> 6;
+  __shared__ int hist[4096];
+  __shared__ uint32_t cand_s[kSelCap];  // low 20 bits of the ordered score
+  __shared__ uint32_t cand_i[kSelCap];  // page id
+  __shared__ int sm[kSelWaves + 1];
+  __shared__ int s_digit, s_rank, s_nvalid, s_ncand, s_id;
+  const int tid = threadIdx.x;
 
-  if (tid == 0) s_nvalid = 0;
+  // Pass A.
+  for (int e = tid; e < 4096; e += kSelThreads) hist[e] = 0;
+  if (tid == 0) {
+    s_nvalid = 0;
+    s_ncand = 0;
+  }
   __syncthreads();
   int c = 0;
   for (int b0 = 0; b0 < n; b0 += kSelBatch * kSelThreads) {
+    float sc[kSelBatch];
     int8_t vv[kSelBatch];
 #pragma unroll
     for (int j = 0; j < kSelBatch; ++j) {
       const int i = b0 + j * kSelThreads + tid;
       vv[j] = i < n ? valid[i] : (int8_t)0;
+      sc[j] = i < n ? scores[i] : 0.0f;
     }
 #pragma unroll
-    for (int j = 0; j < kSelBatch; ++j) c += vv[j] == 1;
+    for (int j = 0; j < kSelBatch; ++j) {
+      if (vv[j] != 1) continue;
+      ++c;
+      atomicAdd(&hist[ordered_score(sc[j]) >> 20], 1);
+    }
   }
   for (int o = 32; o >= 1; o >>= 1) c += __shfl_xor(c, o, 64);
   if ((tid & 63) == 0) atomicAdd(&s_nvalid, c);
@@ -257,13 +327,17 @@ __global__ __launch_bounds__(kSelThreads) void radix_select_kernel(const float* 
     }
     return;
   }
-  uint32_t pre_s = 0, pre_i = 0;  // resolved high bits of score / id
-  int rank = (int)k - 1;          // rank of the wanted key among candidates
-  for (int pass = 0; pass < 8; ++pass) {
-    const bool id_pass = pass >= 4;
-    const int sh = 24 - 8 * (pass & 3);  // digit shift within the 32-bit half
-    for (int e = tid; e < kSelWaves * 256; e += kSelThreads) (&hist[0][0])[e] = 0;
-    __syncthreads();
+  int rank = (int)k - 1;
+  sel_pick(hist, 4096, rank, sm, &s_digit, &s_rank);
+  const uint32_t top = (uint32_t)s_digit;
+  rank = s_rank;
+  const int bucket = hist[top];
+  __syncthreads();
+
+  uint32_t score = 0, idp = 0;
+  if (bucket <= kSelCap) {
+    // Pass B: the bucket's keys into LDS (slot order is irrelevant: only
+    // counts are taken from here on).
     for (int b0 = 0; b0 < n; b0 += kSelBatch * kSelThreads) {
       float sc[kSelBatch];
       int8_t vv[kSelBatch];
@@ -277,38 +351,116 @@ __global__ __launch_bounds__(kSelThreads) void radix_select_kernel(const float* 
       for (int j = 0; j < kSelBatch; ++j) {
         if (vv[j] != 1) continue;
         const uint32_t ks = ordered_score(sc[j]);
-        const uint32_t id = (uint32_t)(b0 + j * kSelThreads + tid);
-        bool match;
-        uint32_t digit;
-        if (!id_pass) {
-          match = (pass == 0) || ((ks >> (sh + 8)) == pre_s);
-          digit = (ks >> sh) & 255u;
-        } else {
-          match = (ks == pre_s) && (pass == 4 || (id >> (sh + 8)) == pre_i);
-          digit = (id >> sh) & 255u;
-        }
-        if (match) atomicAdd(&hist[wave][digit], 1);
+        if ((ks >> 20) != top) continue;
+        const int pos = atomicAdd(&s_ncand, 1);
+        cand_s[pos] = ks & 0xFFFFFu;
+        cand_i[pos] = (uint32_t)(b0 + j * kSelThreads + tid);
       }
     }
     __syncthreads();
-    if (tid < 256) {
-      int sum = 0;
-#pragma unroll
-      for (int w = 0; w < kSelWaves; ++w) sum += hist[w][tid];
-      tot[tid] = sum;
+    const int nc = s_ncand;
+    uint32_t low = 0;
+    int ties = 0;
+    for (int pass = 0; pass < 2; ++pass) {
+      const int sh = 10 - 10 * pass;
+      for (int e = tid; e < 1024; e += kSelThreads) hist[e] = 0;
+      __syncthreads();
+      for (int q = tid; q < nc; q += kSelThreads) {
+        const uint32_t v = cand_s[q];
+        if (pass == 0 || (v >> 10) == low) atomicAdd(&hist[(v >> sh) & 1023u], 1);
+      }
+      __syncthreads();
+      sel_pick(hist, 1024, rank, sm, &s_digit, &s_rank);
+      low = (low << 10) | (uint32_t)s_digit;
+      rank = s_rank;
+      ties = hist[s_digit];
+      __syncthreads();
     }
-    __syncthreads();
-    if (wave == 0) pick_digit(tot, rank, &s_digit, &s_rank);
-    __syncthreads();
-    if (!id_pass)
-      pre_s = (pre_s << 8) | (uint32_t)s_digit;
-    else
-      pre_i = (pre_i << 8) | (uint32_t)s_digit;
-    rank = s_rank;
-    __syncthreads();
+    score = (top << 20) | low;
+    if (ties == 1) {
+      for (int q = tid; q < nc; q += kSelThreads)
+        if (cand_s[q] == low) s_id = (int)cand_i[q];
+      __syncthreads();
+      idp = (uint32_t)s_id;
+    } else {
+      for (int pass = 0; pass < 3; ++pass) {
+        const int width = pass < 2 ? 11 : 10;
+        const int sh = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
+        for (int e = tid; e < 2048; e += kSelThreads) hist[e] = 0;
+        __syncthreads();
+        for (int q = tid; q < nc; q += kSelThreads) {
+          if (cand_s[q] != low) continue;
+          const uint32_t id = cand_i[q];
+          if (pass == 0 || (id >> (sh + width)) == idp) atomicAdd(&hist[(id >> sh) & ((1u << width) - 1u)], 1);
+        }
+        __syncthreads();
+        sel_pick(hist, 2048, rank, sm, &s_digit, &s_rank);
+        idp = (idp << width) | (uint32_t)s_digit;
+        rank = s_rank;
+        __syncthreads();
+      }
+    }
+  } else {
+    // Fallback: byte-wide passes streaming the pages each time; passes 0-3
+    // resolve the score, 4-7 the id.  hist[] serves as 16 per-wave 256-bin
+    // histograms here.
+    const int wave = tid >> 6;
+    uint32_t pre_s = 0, pre_i = 0;
+    rank = (int)k - 1;
+    for (int pass = 0; pass < 8; ++pass) {
+      const bool id_pass = pass >= 4;
+      const int sh = 24 - 8 * (pass & 3);
+      for (int e = tid; e < 4096; e += kSelThreads) hist[e] = 0;
+      __syncthreads();
+      for (int b0 = 0; b0 < n; b0 += kSelBatch * kSelThreads) {
+        float sc[kSelBatch];
+        int8_t vv[kSelBatch];
+#pragma unroll
+        for (int j = 0; j < kSelBatch; ++j) {
+          const int i = b0 + j * kSelThreads + tid;
+          vv[j] = i < n ? valid[i] : (int8_t)0;
+          sc[j] = i < n ? scores[i] : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < kSelBatch; ++j) {
+          if (vv[j] != 1) continue;
+          const uint32_t ks = ordered_score(sc[j]);
+          const uint32_t id = (uint32_t)(b0 + j * kSelThreads + tid);
+          bool match;
+          uint32_t digit;
+          if (!id_pass) {
+            match = (pass == 0) || ((ks >> (sh + 8)) == pre_s);
+            digit = (ks >> sh) & 255u;
+          } else {
+            match = (ks == pre_s) && (pass == 4 || (id >> (sh + 8)) == pre_i);
+            digit = (id >> sh) & 255u;
+          }
+          if (match) atomicAdd(&hist[wave * 256 + digit], 1);
+        }
+      }
+      __syncthreads();
+      // Reduce the 16 per-wave histograms into cand_s[0..256) (unused here).
+      if (tid < 256) {
+        int sum = 0;
+#pragma unroll
+        for (int w = 0; w < kSelWaves; ++w) sum += hist[w * 256 + tid];
+        cand_s[tid] = (uint32_t)sum;
+      }
+      __syncthreads();
+      if (tid < 64) pick_digit256(reinterpret_cast<const int*>(cand_s), rank, &s_digit, &s_rank);
+      __syncthreads();
+      if (!id_pass)
+        pre_s = (pre_s << 8) | (uint32_t)s_digit;
+      else
+        pre_i = (pre_i << 8) | (uint32_t)s_digit;
+      rank = s_rank;
+      __syncthreads();
+    }
+    score = pre_s;
+    idp = pre_i;
   }
   if (tid == 0) {
-    out->key_thr = ((unsigned long long)pre_s << 32) | pre_i;
+    out->key_thr = ((unsigned long long)score << 32) | idp;
     out->k = (int)k;
     out->n_valid = n_valid;
   }

@@ -65,16 +65,22 @@ struct Vec16<float> {
 // workgroup barrier that publishes cos/sin keeps those loads ahead of it.
 constexpr int kRemapItems = 4;  // chunk pairs per thread per round
 
-template <typename T>
+// kHalf / kHeads / kPage > 0 fix head_dim/2, the head count and the page size
+// at compile time (the index arithmetic then has no runtime divisions); 0
+// takes them from the arguments.
+template <typename T, int kHalf, int kHeads, int kPage>
 __global__ __launch_bounds__(kRemapThreads) void rope_remap_vec(
     T* __restrict__ pool, int64_t page_stride, int64_t tok_stride, int64_t head_stride,
     const int32_t* __restrict__ page_list, int num_pages, const int32_t* __restrict__ orig_pos,
     const int32_t* __restrict__ tgt_pos, const float* __restrict__ inv_freq, float theta, int num_tokens,
-    int num_heads, int half, int page_size) {
+    int num_heads_arg, int half_arg, int page_size_arg) {
 #pragma clang fp contract(off)
   typedef typename Vec16<T>::type V;
   constexpr int N = Vec16<T>::N;
   __shared__ float2 cs[kRemapTile * kVecMaxHalf];  // [token][j] = (cos, sin)
+  const int half = kHalf > 0 ? kHalf : half_arg;
+  const int num_heads = kHeads > 0 ? kHeads : num_heads_arg;
+  const int page_size = kPage > 0 ? kPage : page_size_arg;
 
   const int t0 = blockIdx.x * kRemapTile;
   const int ntok = min(kRemapTile, num_tokens - t0);
@@ -100,8 +106,10 @@ __global__ __launch_bounds__(kRemapThreads) void rope_remap_vec(
         const int64_t row = token_row(t0 + tt, page_list, num_pages, page_size, page_stride, tok_stride);
         if (row >= 0) {
           p1[it] = pool + row + (int64_t)h * head_stride + c * N;
-          a[it] = *reinterpret_cast<const V*>(p1[it]);
-          b[it] = *reinterpret_cast<const V*>(p1[it] + half);
+          // Streaming accesses: every byte is touched once, so non-temporal
+          // loads/stores keep the in-place update from churning the caches.
+          a[it] = __builtin_nontemporal_load(reinterpret_cast<const V*>(p1[it]));
+          b[it] = __builtin_nontemporal_load(reinterpret_cast<const V*>(p1[it] + half));
           csi[it] = tt * half + c * N;
         }
       }
@@ -137,8 +145,8 @@ __global__ __launch_bounds__(kRemapThreads) void rope_remap_vec(
         y1[e] = from_f32<T>(u1 - u2);
         y2[e] = from_f32<T>(w1 + w2);
       }
-      *reinterpret_cast<V*>(p1[it]) = y1;
-      *reinterpret_cast<V*>(p1[it] + half) = y2;
+      __builtin_nontemporal_store(y1, reinterpret_cast<V*>(p1[it]));
+      __builtin_nontemporal_store(y2, reinterpret_cast<V*>(p1[it] + half));
     }
   }
 }
@@ -190,9 +198,16 @@ int launch_remap(void* pool, int64_t page_stride, int64_t tok_stride, int64_t he
   T* p = static_cast<T*>(pool);
   if (vec_ok) {
     const int grid = div_up(num_tokens, kRemapTile);
-    hipLaunchKernelGGL(rope_remap_vec<T>, dim3(grid), dim3(kRemapThreads), 0, stream, p, page_stride,
-                       tok_stride, head_stride, page_list, num_pages, orig_pos, tgt_pos, inv_freq, theta,
-                       num_tokens, num_heads, half, page_size);
+    // Specialised instance for the Llama-style K layout (8 kv heads x 128,
+    // 16-token pages or dense rows).
+    if (half == 64 && num_heads == 8 && (page_list == nullptr || page_size == 16))
+      hipLaunchKernelGGL((rope_remap_vec<T, 64, 8, 16>), dim3(grid), dim3(kRemapThreads), 0, stream, p,
+                         page_stride, tok_stride, head_stride, page_list, num_pages, orig_pos, tgt_pos, inv_freq,
+                         theta, num_tokens, num_heads, half, page_size);
+    else
+      hipLaunchKernelGGL((rope_remap_vec<T, 0, 0, 0>), dim3(grid), dim3(kRemapThreads), 0, stream, p,
+                         page_stride, tok_stride, head_stride, page_list, num_pages, orig_pos, tgt_pos, inv_freq,
+                         theta, num_tokens, num_heads, half, page_size);
   } else {
     const int64_t total = (int64_t)num_tokens * num_heads * half;
     const int64_t grid = (total + kRemapThreads - 1) / kRemapThreads;

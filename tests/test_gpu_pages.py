@@ -74,6 +74,29 @@ def test_select_evict_bit_exact(dev, n, frac, k):
     assert np.array_equal(_np(dv), ref_valid)
 
 
+@pytest.mark.parametrize("n,distinct,frac", [
+    (5000, 50, 0.25),       # many ties at the threshold score: id resolution on the LDS copy
+    (65536, 1, 0.25),       # one score for every page: the bucket overflows LDS -> streaming passes
+    (40000, 3, 0.5),        # three values, buckets above the LDS capacity
+    (20000, 20000, 0.999),  # nearly everything evicted
+])
+def test_select_evict_ties_bit_exact(dev, n, distinct, frac):
+    from kessie_amd import ops
+
+    g = torch.Generator().manual_seed(distinct)
+    values = torch.rand(distinct, generator=g)
+    scores = values[torch.randint(0, distinct, (n,), generator=g)]
+    valid = (torch.rand(n, generator=g) < 0.95).to(torch.int8)
+    ref_valid, ref_list = P.select_evict(scores.numpy(), valid.numpy(), -1, frac)
+    dv = valid.to(dev)
+    lst, cnt = ops.page_select_evict(scores.to(dev), dv, -1, frac)
+    torch.cuda.synchronize()
+    c = int(cnt.item())
+    assert c == len(ref_list)
+    assert np.array_equal(_np(lst[:c]), ref_list)
+    assert np.array_equal(_np(dv), ref_valid)
+
+
 def test_compact_and_gather_bit_exact(dev):
     from kessie_amd import ops
 
