@@ -321,6 +321,31 @@ def bench_decode_fp32(dev, reps=20):
             "ms": round(ms, 5), "gbs": round(s["bytes"] / (ms * 1e-3) / 1e9, 1)}
 
 
+def pmc_run(dev) -> None:
+    """A short fixed sequence of launches for hardware-counter passes
+    (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE): a 1 GiB device copy of
+    known size (the calibration kernel), then one decode, one remap and one
+    gather + evict pipeline of the bench workloads."""
+    import torch
+
+    src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    src.fill_(3)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    s = setup_decode(dev)
+    run_decode_step(s)
+    torch.cuda.synchronize()
+    del s
+    torch.cuda.empty_cache()
+    bench_remap(dev, reps=1, sets=1)
+    torch.cuda.empty_cache()
+    bench_gather_evict(dev, reps=1)
+    torch.cuda.synchronize()
+    log("pmc run done")
+
+
 # ---------------------------------------------------------------------------
 def main():
     ap = argparse.ArgumentParser()
@@ -329,7 +354,14 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-secondary", action="store_true", help="skip remap / gather / fp32 lines")
+    ap.add_argument("--pmc-run", action="store_true",
+                    help="only run the launch sequence used for rocprofv3 --pmc traffic passes")
     args = ap.parse_args()
+    if args.pmc_run:
+        import torch
+
+        pmc_run(torch.device("cuda:0"))
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (the hot path is built and measured on a single MI355X); "
               f"--gpus {args.gpus} is not supported", file=sys.stderr)
