@@ -300,6 +300,49 @@ def bench_gather_evict(dev, reps=5):
     }
 
 
+def bench_prefill(dev, reps=3, c=2048, L=1 << 20, hq=32, hkv=8, d=128):
+    """Chunked prefill, bf16 on MFMA: a 2,048-query chunk appended to a
+    1,048,576-token paged KV (65,664 pages, random table), 32 q / 8 kv heads,
+    D=128, causal, V-fog over the full context."""
+    import torch
+
+    from kessie_amd import ops
+
+    ctx = L + c
+    n_pages = ctx // 16
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    q = torch.randn(1, c, hq, d, generator=g, device=dev).bfloat16()
+    pool = torch.empty(n_pages, 16, 2, hkv, d, device=dev, dtype=torch.bfloat16)
+    for p0 in range(0, n_pages, 8192):
+        p1 = min(n_pages, p0 + 8192)
+        pool[p0:p1] = torch.randn(p1 - p0, 16, 2, hkv, d, generator=g, device=dev).bfloat16()
+    g1 = torch.Generator(device=dev)
+    g1.manual_seed(1)
+    table = torch.randperm(n_pages, generator=g1, device=dev).to(torch.int32).view(1, n_pages).contiguous()
+    lens = torch.tensor([ctx], dtype=torch.int32, device=dev)
+    cf = int(ctx * 0.5)
+    fog = torch.ones(ctx, dtype=torch.float32, device=dev)
+    fog[:cf] = (torch.arange(cf, dtype=torch.float32, device=dev) / max(cf - 1, 1)).pow(0.5)
+    out = torch.empty_like(q)
+    ops.fog_prefill(q, pool, table, lens, ctx, fog_vscale=fog, out=out)
+    torch.cuda.synchronize()
+    e0, e1 = events(reps), events(reps)
+    backlog()
+    for i in range(reps):
+        e0[i].record()
+        ops.fog_prefill(q, pool, table, lens, ctx, fog_vscale=fog, out=out)
+        e1[i].record()
+    torch.cuda.synchronize()
+    ms = sum(a.elapsed_time(b) for a, b in zip(e0, e1)) / reps
+    flops = 4 * d * hq * (c * L + c * (c + 1) // 2)
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"workload": "chunked prefill bf16: 2048 queries on a 1,048,576-token paged context, 32q/8kv, D=128, "
+                        "causal, V-fog", "ms": round(ms, 3), "tflops": round(tf, 1),
+            "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(tf / BF16_PEAK_TFLOPS, 4), "algorithmic_flops": flops}}
+
+
 def bench_decode_fp32(dev, reps=20):
     """Fog decode on the reference CPU path's shape, fp32: B=1, 32q/8kv, D=128,
     4,096-token context in 16-token pages."""
@@ -432,6 +475,9 @@ def main():
         torch.cuda.empty_cache()
         log("secondary: fp32 decode 4K")
         sec["decode_fp32_4k"] = bench_decode_fp32(dev)
+        torch.cuda.empty_cache()
+        log("secondary: chunked prefill 2048 x 1M")
+        sec["prefill_1m"] = bench_prefill(dev)
         result["secondary"] = sec
     print(json.dumps(result), flush=True)
 

@@ -25,94 +25,10 @@
 #include <cmath>
 #include <cstdlib>
 
-#include "common.h"
+#include "attn_common.h"
 
 namespace kessie {
 namespace attn {
-
-constexpr float kNegInf = -__builtin_huge_valf();
-
-struct Params {
-  // Query row (b, i, h) at q + b*q_bs + i*q_is + h*q_hs; output likewise.
-  const void* q;
-  int64_t q_bs, q_is, q_hs;
-  void* out;
-  int64_t o_bs, o_is, o_hs;
-  // Key/value element (page, slot, h, d) at k + page*page_stride +
-  // slot*tok_stride + h*head_stride + d (v likewise).  page_table == nullptr:
-  // dense, sequence b's token t at b*page_stride + t*tok_stride.
-  const void* k;
-  const void* v;
-  int num_pages;
-  int64_t page_stride, tok_stride, head_stride;
-  int page_size;
-  const int32_t* page_table;
-  int64_t table_stride;
-  const int32_t* ctx_lens;  // nullptr: every sequence has ctx_const tokens
-  int ctx_const;
-  int max_ctx;
-  const float* vscale;
-  int64_t vs_bs;
-  const float* bias;
-  int64_t bias_bs;
-  int B, C, Hq, Hkv, G, D;
-  int window, causal;
-  float sm_scale;
-  int num_splits;
-  int direct_out;      // 1: the main kernel writes the normalised output
-  int launch_combine;  // host side: follow the main kernel with the combine
-  float* ws_o;  // [B*C*Hq][S][D]
-  float* ws_m;  // [B*C*Hq][S]
-  float* ws_l;  // [B*C*Hq][S]
-};
-
-__device__ __forceinline__ int seq_ctx(const Params& p, int b) {
-  int ctx = p.ctx_lens ? p.ctx_lens[b] : p.ctx_const;
-  ctx = min(ctx, p.max_ctx);
-  if (p.page_table) {
-    const int64_t cap = p.table_stride * (int64_t)p.page_size;
-    if ((int64_t)ctx > cap) ctx = (int)cap;
-  }
-  return max(ctx, 0);
-}
-
-// Element offset of token t of sequence b, or -1 when its page id is invalid.
-__device__ __forceinline__ int64_t token_offset(const Params& p, int b, int t) {
-  if (p.page_table == nullptr) return (int64_t)b * p.page_stride + (int64_t)t * p.tok_stride;
-  const int pid = p.page_table[(int64_t)b * p.table_stride + t / p.page_size];
-  if (pid < 0 || pid >= p.num_pages) return -1;
-  return (int64_t)pid * p.page_stride + (int64_t)(t % p.page_size) * p.tok_stride;
-}
-
-__device__ __forceinline__ bool key_visible(int q_pos, int t, int window, int causal) {
-  const int dist = q_pos - t;
-  if (causal && dist < 0) return false;
-  if (window > 0 && (dist < 0 || dist >= window)) return false;
-  return true;
-}
-
-// Row index into the partial workspace / output for (b, i, h).
-__device__ __forceinline__ int64_t row_id(const Params& p, int b, int i, int h) {
-  return ((int64_t)b * p.C + i) * p.Hq + h;
-}
-
-template <typename T>
-__device__ __forceinline__ void store_out(const Params& p, int b, int i, int h, int d, float val) {
-  T* o = static_cast<T*>(p.out);
-  o[(int64_t)b * p.o_bs + (int64_t)i * p.o_is + (int64_t)h * p.o_hs + d] = from_f32<T>(val);
-}
-
-// Key range [lo, hi) a set of query positions [qmin, qmax] can see.
-__device__ __forceinline__ void key_range(const Params& p, int ctx, int qmin, int qmax, int* lo, int* hi) {
-  int h = p.causal ? min(ctx, qmax + 1) : ctx;
-  int l = 0;
-  if (p.window > 0) {
-    l = max(0, qmin - p.window + 1);
-    h = min(h, qmax + 1);
-  }
-  *lo = l;
-  *hi = max(h, l);
-}
 
 // ---------------------------------------------------------------------------
 // Generic kernel
@@ -593,11 +509,6 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4, 4))) 
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
-int env_int(const char* name, int dflt) {
-  const char* v = getenv(name);
-  if (v == nullptr || *v == '\0') return dflt;
-  return atoi(v);
-}
 
 // Number of key splits per (sequence, kv-head group); identical for the
 // workspace query and the launch.
@@ -621,20 +532,6 @@ int prefill_splits(int B, int C, int Hkv, int G, int max_ctx, int page_size) {
   return max(s, 1);
 }
 
-size_t partial_bytes(int64_t rows, int S, int D) {
-  const size_t o = (size_t)rows * S * D * sizeof(float);
-  const size_t ml = (size_t)rows * S * sizeof(float);
-  return o + 2 * ((ml + 255) / 256 * 256);
-}
-
-void carve_workspace(Params& p, void* ws, int64_t rows) {
-  char* c = static_cast<char*>(ws);
-  p.ws_o = reinterpret_cast<float*>(c);
-  c += (size_t)rows * p.num_splits * p.D * sizeof(float);
-  p.ws_m = reinterpret_cast<float*>(c);
-  c += ((size_t)rows * p.num_splits * sizeof(float) + 255) / 256 * 256;
-  p.ws_l = reinterpret_cast<float*>(c);
-}
 
 template <typename T>
 int launch_generic(Params& p, hipStream_t stream) {
@@ -950,6 +847,12 @@ extern "C" int kessie_fog_prefill_paged(const void* q, const void* kv_pool, int 
                  "fog prefill: page_table and ctx_lens are required");
   KESSIE_REQUIRE(kv_stride >= 0, KESSIE_ERR_INVALID, "fog prefill: kv_stride %lld", (long long)kv_stride);
   if (batch == 0) return KESSIE_OK;
+  if (prefill_mfma_ok(p, dtype)) {  // MFMA kernel: one pass over the keys, no workspace
+    p.num_splits = 1;
+    p.direct_out = 1;
+    p.launch_combine = 0;
+    return prefill_mfma(p, dtype, as_stream(stream));
+  }
   p.num_splits = prefill_splits(batch, num_q_tokens, num_kv_heads, p.G, max_ctx, page_size);
   p.direct_out = p.num_splits == 1 ? 1 : 0;
   p.launch_combine = 1;

@@ -134,6 +134,65 @@ def paged_prefill_ref(q: torch.Tensor, pool: torch.Tensor, page_table: torch.Ten
     return out
 
 
+def paged_prefill_blockwise(q: torch.Tensor, pool: torch.Tensor, page_table: torch.Tensor,
+                            ctx_lens: torch.Tensor, rows: torch.Tensor,
+                            fog_vscale: Optional[torch.Tensor] = None, window: int = 0, causal: bool = True,
+                            sm_scale: Optional[float] = None, block_pages: int = 512) -> torch.Tensor:
+    """paged_prefill_ref for selected chunk rows, blockwise with an online
+    softmax so a million-token context fits in CPU memory.  ``pool`` may live
+    on the GPU: each block of pages is gathered there and copied over.
+    q [B, C, Hq, D] (CPU); returns fp32 [B, len(rows), Hq, D]."""
+    b_, c, hq, d = q.shape
+    p = pool.shape[1]
+    hkv = pool.shape[3]
+    g = hq // hkv
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(d)
+    rows = rows.long()
+    r = len(rows)
+    out = torch.zeros(b_, r, hq, d, dtype=torch.float32)
+    for b in range(b_):
+        ctx = int(ctx_lens[b])
+        qpos = ctx - c + rows                                          # [R]
+        qg = q[b, rows].float().view(r, hkv, g, d).permute(1, 2, 0, 3).reshape(hkv, g * r, d)
+        pos_col = qpos.repeat(g)                                       # column (g, r) -> qpos[r]
+        m = torch.full((hkv, g * r), float("-inf"))
+        l = torch.zeros(hkv, g * r)
+        acc = torch.zeros(hkv, g * r, d)
+        hi = ctx if not causal else min(ctx, int(qpos.max()) + 1)
+        lo = 0 if window <= 0 else max(0, int(qpos.min()) - window + 1)
+        n_pages = (hi + p - 1) // p
+        for p0 in range(lo // p, n_pages, block_pages):
+            p1 = min(n_pages, p0 + block_pages)
+            kv = pool[page_table[b, p0:p1].long().to(pool.device)].cpu().reshape((p1 - p0) * p, 2, hkv, d).float()
+            t0 = p0 * p
+            t1 = min(hi, p1 * p)
+            kb = kv[: t1 - t0, 0].permute(1, 2, 0)                    # [Hkv, D, n]
+            vb = kv[: t1 - t0, 1]
+            if fog_vscale is not None:
+                vs = (fog_vscale if fog_vscale.dim() == 1 else fog_vscale[b])[t0:t1].float().cpu()
+                vb = vb * vs[:, None, None]
+            s = torch.bmm(qg, kb) * sm_scale                          # [Hkv, G*R, n]
+            j = torch.arange(t0, t1)
+            dist = pos_col[:, None] - j[None, :]
+            keep = torch.ones_like(dist, dtype=torch.bool)
+            if causal:
+                keep &= dist >= 0
+            if window > 0:
+                keep &= (dist >= 0) & (dist < window)
+            s = s.masked_fill(~keep[None], float("-inf"))
+            m_new = torch.maximum(m, s.amax(-1))
+            m_safe = torch.where(torch.isinf(m_new), torch.zeros_like(m_new), m_new)
+            corr = torch.where(torch.isinf(m), torch.zeros_like(m), torch.exp(m - m_safe))
+            pexp = torch.exp(s - m_safe[..., None])
+            l = l * corr + pexp.sum(-1)
+            acc = acc * corr[..., None] + torch.bmm(pexp, vb.permute(1, 0, 2).contiguous())
+            m = m_new
+        o = acc / l[..., None]                                         # [Hkv, G*R, D]
+        out[b] = o.view(hkv, g, r, d).permute(2, 0, 1, 3).reshape(r, hq, d)
+    return out
+
+
 def paged_decode_blockwise(q: torch.Tensor, pool: torch.Tensor, page_table: torch.Tensor,
                            ctx_lens: torch.Tensor, fog_vscale: Optional[torch.Tensor] = None,
                            window: int = 0, sm_scale: Optional[float] = None,

@@ -1,0 +1,137 @@
+"""GPU parity: chunked-prefill fog attention (MFMA kernel and the generic
+kernel) vs the CPU oracle.  bf16/fp16: |gpu - ref| <= 2e-2 + 1e-2*|ref|;
+fp32 (generic kernel): 1e-5."""
+import pytest
+import torch
+
+from oracle.attention import paged_prefill_blockwise, paged_prefill_ref
+from oracle.fog import build_fog_weights, fog_bias
+from tests.inputs import gen, paged_pool, randperm
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.bfloat16: (2e-2, 1e-2), torch.float16: (2e-2, 1e-2), torch.float32: (1e-5, 1e-5)}
+
+
+def _check(got, ref, dtype):
+    atol, rtol = TOL[dtype]
+    g = got.float().cpu()
+    diff = (g - ref).abs()
+    bad = diff > atol + rtol * ref.abs()
+    assert not bad.any(), f"{int(bad.sum())}/{bad.numel()} outside tol, max diff {diff.max().item():.3e}"
+
+
+def _case(dev, b, c, ctxs, hq, hkv, dtype, seed=0):
+    p, d = 16, 128
+    pages_per = max((x + p - 1) // p for x in ctxs)
+    num_pages = b * pages_per + 3
+    pool = paged_pool(num_pages, p, hkv, d, dtype, dev, seed)
+    table = randperm(num_pages, dev, seed + 1)[: b * pages_per].view(b, pages_per).contiguous()
+    q = torch.randn(b, c, hq, d, generator=gen(dev, seed + 2), device=dev).to(dtype)
+    lens = torch.tensor(ctxs, dtype=torch.int32, device=dev)
+    return q, pool, table, lens
+
+
+@pytest.mark.parametrize("hq,hkv", [(32, 8), (8, 8), (16, 8), (64, 8)])
+def test_prefill_bf16_gqa(dev, hq, hkv):
+    from kessie_amd import ops
+
+    q, pool, table, lens = _case(dev, 2, 100, [1000, 777], hq, hkv, torch.bfloat16)
+    fog = build_fog_weights(1000).to(dev)
+    out = ops.fog_prefill(q, pool, table, lens, 1000, fog_vscale=fog)
+    torch.cuda.synchronize()
+    ref = paged_prefill_ref(q.cpu(), pool.cpu(), table.cpu(), lens.cpu(), fog.cpu())
+    _check(out, ref, torch.bfloat16)
+
+
+@pytest.mark.parametrize("c,ctx", [(1, 1), (1, 64), (17, 17), (64, 200), (300, 300), (129, 4000)])
+def test_prefill_chunk_shapes(dev, c, ctx):
+    from kessie_amd import ops
+
+    q, pool, table, lens = _case(dev, 1, c, [ctx], 32, 8, torch.bfloat16, seed=c)
+    out = ops.fog_prefill(q, pool, table, lens, ctx)
+    torch.cuda.synchronize()
+    ref = paged_prefill_ref(q.cpu(), pool.cpu(), table.cpu(), lens.cpu())
+    _check(out, ref, torch.bfloat16)
+
+
+@pytest.mark.parametrize("window", [1, 16, 37, 100, 10000])
+def test_prefill_window(dev, window):
+    from kessie_amd import ops
+
+    q, pool, table, lens = _case(dev, 1, 90, [700], 32, 8, torch.bfloat16, seed=5)
+    out = ops.fog_prefill(q, pool, table, lens, 700, window=window)
+    torch.cuda.synchronize()
+    ref = paged_prefill_ref(q.cpu(), pool.cpu(), table.cpu(), lens.cpu(), window=window)
+    _check(out, ref, torch.bfloat16)
+
+
+def test_prefill_bias_and_fp16(dev):
+    from kessie_amd import ops
+
+    q, pool, table, lens = _case(dev, 2, 70, [500, 333], 32, 8, torch.float16, seed=6)
+    bias = fog_bias(500, 0.5, 0.5, {3, 99, 498}, 0.1).to(dev)
+    out = ops.fog_prefill(q, pool, table, lens, 500, fog_bias=bias)
+    torch.cuda.synchronize()
+    ref = paged_prefill_ref(q.cpu(), pool.cpu(), table.cpu(), lens.cpu(), None, bias.cpu())
+    _check(out, ref, torch.float16)
+
+
+def test_prefill_non_causal_and_bad_pages(dev):
+    from kessie_amd import ops
+
+    q, pool, table, lens = _case(dev, 1, 40, [400], 32, 8, torch.bfloat16, seed=7)
+    table[0, 3] = -1
+    out = ops.fog_prefill(q, pool, table, lens, 400, causal=False)
+    torch.cuda.synchronize()
+    keep = [i for i in range(table.shape[1]) if i != 3]
+    pool_c = pool.cpu()
+    # Oracle: the same context without logical page 3 (non-causal, so only membership matters).
+    t2 = table.cpu()[:, keep].contiguous()
+    ref = paged_prefill_ref(q.cpu(), pool_c, t2, torch.tensor([400 - 16]), causal=False)
+    _check(out, ref, torch.bfloat16)
+
+
+def test_prefill_fp32_generic(dev):
+    from kessie_amd import ops
+
+    q, pool, table, lens = _case(dev, 1, 33, [300], 32, 8, torch.float32, seed=8)
+    fog = build_fog_weights(300).to(dev)
+    out = ops.fog_prefill(q, pool, table, lens, 300, fog_vscale=fog)
+    torch.cuda.synchronize()
+    ref = paged_prefill_ref(q.cpu(), pool.cpu(), table.cpu(), lens.cpu(), fog.cpu())
+    _check(out, ref, torch.float32)
+
+
+def test_prefill_mfma_matches_generic(dev, monkeypatch):
+    from kessie_amd import ops
+
+    q, pool, table, lens = _case(dev, 2, 150, [2000, 1500], 32, 8, torch.bfloat16, seed=9)
+    fog = build_fog_weights(2000).to(dev)
+    a = ops.fog_prefill(q, pool, table, lens, 2000, fog_vscale=fog)
+    monkeypatch.setenv("KESSIE_FORCE_GENERIC", "1")
+    b = ops.fog_prefill(q, pool, table, lens, 2000, fog_vscale=fog)
+    torch.cuda.synchronize()
+    assert (a.float() - b.float()).abs().max().item() < 2e-2
+
+
+def test_prefill_1m_context_sampled(dev):
+    """Config: bf16, 2,048-query chunk appended to a 1,048,576-token paged KV
+    (65,664 pages), 32 q / 8 kv heads, D=128, causal, V-fog over the full
+    context.  Full-size GPU run; 6 rows checked against the blockwise oracle."""
+    from kessie_amd import ops
+
+    c, L = 2048, 1 << 20
+    ctx = L + c
+    n_pages = ctx // 16
+    pool = paged_pool(n_pages, 16, 8, 128, torch.bfloat16, dev, 0)
+    table = randperm(n_pages, dev, 1).view(1, n_pages).contiguous()
+    q = torch.randn(1, c, 32, 128, generator=gen(dev, 2), device=dev).bfloat16()
+    lens = torch.tensor([ctx], dtype=torch.int32, device=dev)
+    fog = build_fog_weights(ctx).to(dev)
+    out = ops.fog_prefill(q, pool, table, lens, ctx, fog_vscale=fog)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    rows = torch.tensor([0, 1, 777, 1500, 2046, 2047])
+    ref = paged_prefill_blockwise(q.cpu(), pool, table.cpu(), lens.cpu(), rows, fog.cpu(), block_pages=4096)
+    _check(out[:, rows], ref, torch.bfloat16)

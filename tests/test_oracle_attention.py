@@ -127,3 +127,18 @@ def test_blockwise_decode_equals_direct():
     a = paged_decode_ref(q, pool, table, torch.tensor([ctx]), w, window=61)
     b = paged_decode_blockwise(q, pool, table, torch.tensor([ctx]), w, window=61, block_pages=3)
     assert torch.allclose(a, b, atol=1e-5)
+
+
+def test_blockwise_prefill_equals_direct():
+    from oracle.attention import paged_prefill_blockwise
+
+    hq, hkv, d, p, ctx, c = 8, 2, 16, 4, 150, 40
+    pool = _paged(17, 40, p, hkv, d)
+    table = torch.randperm(40, generator=torch.Generator().manual_seed(18)).to(torch.int32).view(1, 40)
+    q = torch.randn(1, c, hq, d, generator=torch.Generator().manual_seed(19))
+    w = build_fog_weights(ctx)
+    rows = torch.tensor([0, 7, 39])
+    for window in (0, 23):
+        a = paged_prefill_ref(q, pool, table, torch.tensor([ctx]), w, window=window, rows=rows)
+        b = paged_prefill_blockwise(q, pool, table, torch.tensor([ctx]), rows, w, window=window, block_pages=3)
+        assert torch.allclose(a, b, atol=1e-5)
