@@ -1,23 +1,28 @@
 // Chunked-prefill fog attention on MFMA for gfx950 (bf16 / f16, head_dim 128,
-// 16-token pages, GQA ratio G dividing 32).
+// 16-token pages, GQA ratio G dividing 32, sm_scale > 0).
 //
 // Math: the last C rows of kessie_hip_kernels.py:577-593 over ctx = L + C
 // tokens (query i at position ctx-C+i, causal, window, fog weights scaling V
-// rows or a logit bias), fp32 accumulation, online softmax.
+// rows or a logit bias), fp32 accumulation, online softmax in base 2.
 //
 // Work decomposition: one workgroup = 256 query rows (256/G positions x the G
 // heads of one kv head) of one sequence; 8 waves x 32 rows.  The workgroup
-// streams its kv head's keys in tiles of 64 (4 pages): K row-major and V
-// transposed ([d][key], key pairs packed into 32-bit LDS writes) into LDS,
-// the next tile's global loads in flight while the current one is consumed.
-// Per wave and tile:
-//   S^T (64 keys x 32 rows) = K Q^T   on v_mfma_f32_32x32x16 (16 MFMAs);
-//     row i of a 32-key A operand is key swap23(i), so the accumulator's
-//     register v of lane l holds key 16(v/8) + 8(l/32) + (v%8) of row l%32:
-//     the softmax is lane-local plus one xor-32 shuffle, and p is already in
-//     the B-operand layout of PV (8 consecutive keys per lane half);
-//   O^T (128 d x 32 rows) += V^T P^T  on v_mfma_f32_32x32x16 (16 MFMAs),
-//     the V^T A operand is one 16-byte LDS read.
+// streams its kv head's keys in tiles of 64 (4 pages) through a three-stage
+// LDS ring, one barrier per tile:
+//   iteration t:  global loads of tile t+2 (page ids fetched one iteration
+//                 earlier, wave-uniform, so no load waits on another);
+//                 S^T(t+1) = K Q^T on MFMA, independent of ...
+//                 ... the softmax of tile t (VALU), then O^T += V^T P^T(t);
+//                 tile t+2 to LDS; barrier.
+// Per wave and tile: S^T (64 keys x 32 rows) on v_mfma_f32_32x32x16 (16
+// MFMAs) and O^T (128 d x 32 rows) likewise (16 MFMAs).  Key j of a 32-key
+// block sits in LDS row swap23(j), so register v of lane l of the S^T
+// accumulator holds key 16(v/8) + 8(l/32) + (v%8) of row l%32: the softmax is
+// lane-local plus one xor-32 shuffle, and p is already in the B-operand
+// layout of PV.  V is stored transposed ([d][key], key pairs packed into
+// 32-bit words) with the 16-byte key chunks XOR-swizzled by d/16, so both the
+// transposing stores and the 16-byte operand reads are free of bank
+// conflicts; the K rows are padded to 68 words for the same reason.
 // Grid index x = qtile * Hkv + g, so with 8 kv heads (and the hardware's
 // round-robin of workgroups over the 8 XCDs) every workgroup of kv head g
 // sits on one XCD and the query tiles of that head share its keys in L2.
@@ -31,10 +36,16 @@ constexpr int kPfWaves = 8;
 constexpr int kPfThreads = kPfWaves * 64;
 constexpr int kPfRows = kPfWaves * 32;  // query rows (position, head) per workgroup
 constexpr int kPfKT = 64;               // keys per tile (4 pages)
-constexpr int kPfKRow = 128 + 8;        // K tile row stride (elements)
-constexpr int kPfVRow = kPfKT + 8;      // V^T tile row stride (elements)
+constexpr int kPfStages = 3;            // LDS ring depth
+constexpr int kKRow = 128 + 8;          // K tile row stride (elements)
+constexpr int kVRowW = kPfKT / 2 + 4;   // V^T tile row stride (32-bit words)
+constexpr int kKStage = kPfKT * kKRow;  // elements per K stage
+constexpr int kVStage = 128 * kVRowW;   // words per V^T stage
+constexpr size_t kPfLdsBytes = (size_t)kPfStages * (kKStage * 2 + kVStage * 4 + 2 * kPfKT * 4);
+constexpr float kLog2e = 1.4426950408889634f;
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 template <typename T>
 struct Mma32;
@@ -62,18 +73,23 @@ __device__ __forceinline__ uint32_t bits16(T x) {
   return (uint32_t)__builtin_bit_cast(uint16_t, x);
 }
 
-template <typename T, int G>
+__device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+__device__ __forceinline__ bool page_ok(int pid, int num_pages) { return pid >= 0 && pid < num_pages; }
+
+template <typename T, int G, bool kBias, bool kVs>
 __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
   typedef typename Mma32<T>::v8 v8;
   typedef typename Mma32<T>::v4 v4;
   constexpr int kPos = kPfRows / G;  // query positions per workgroup
-  __shared__ __align__(16) T ks[kPfKT * kPfKRow];
-  __shared__ __align__(16) T vts[128 * kPfVRow];
-  __shared__ float fws[kPfKT];  // fog weight per key of the tile (V mode)
-  __shared__ float fbs[kPfKT];  // fog bias per key of the tile
-  __shared__ int kok[kPfKT];    // key present (in range, valid page)
+  extern __shared__ __align__(16) unsigned char smem[];
+  T* ks = reinterpret_cast<T*>(smem);                                                // [stage][64][kKRow]
+  uint32_t* vts = reinterpret_cast<uint32_t*>(smem + (size_t)kPfStages * kKStage * 2);  // [stage][128][kVRowW]
+  float* fws = reinterpret_cast<float*>(vts + kPfStages * kVStage);                   // [stage][64] V weight
+  float* fbs = fws + kPfStages * kPfKT;                                               // [stage][64] bias*log2(e)
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = uniform(tid >> 6);
   const int col = lane & 31, half = lane >> 5;
   const int g = blockIdx.x % p.Hkv;
   const int qtile = blockIdx.x / p.Hkv;
@@ -90,6 +106,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
   key_range(p, ctx, qmin, qmax, &lo, &hi);
   const int t_begin = (lo / kPfKT) * kPfKT;
   const int n_tiles = hi > t_begin ? div_up(hi - t_begin, kPfKT) : 0;
+  const int n_tab = div_up(hi, 16);  // table entries that may be read
 
   // This lane's query row.
   const int frow = wave * 32 + col;
@@ -114,156 +131,210 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
     }
   }
 
-  // Loader mapping: K rows kr and kr+32, V key pair (2kr, 2kr+1), chunk kc.
+  // Loader: K keys kr and kr+32 (page slots kr/16 and 2+kr/16, both
+  // wave-uniform), V keys 2kr and 2kr+1 (page slot kr/8 = wave/2), 16-byte
+  // chunk kc of the 256-byte token row.
   const int kc = tid & 15, kr = tid >> 4;
   const T* kbase = static_cast<const T*>(p.k) + (int64_t)g * p.head_stride + 8 * kc;
   const T* vbase = static_cast<const T*>(p.v) + (int64_t)g * p.head_stride + 8 * kc;
   const int32_t* table = p.page_table + (int64_t)b * p.table_stride;
-  auto key_off = [&](int key) -> int64_t {
-    if (key < lo || key >= hi) return -1;
-    const int pid = table[key >> 4];
-    if (pid < 0 || pid >= p.num_pages) return -1;
-    return (int64_t)pid * p.page_stride + (int64_t)(key & 15) * p.tok_stride;
+  const int kslot = wave >> 2, vslot = wave >> 1;
+
+  // Page ids of a tile (4 uniform values; -1 past the end).
+  auto fetch_ids = [&](int tile) {
+    const int pg0 = (t_begin + tile * kPfKT) >> 4;
+    i32x4 ids;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ids[j] = (tile < n_tiles && pg0 + j < n_tab) ? table[pg0 + j] : -1;
+    return ids;
   };
+  auto valid_mask = [&](i32x4 ids) {
+    int m = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) m |= page_ok(uniform(ids[j]), p.num_pages) ? (1 << j) : 0;
+    return m;
+  };
+
   v8 kreg[2], vreg[2];
-  float fw_r = 0.0f, fb_r = 0.0f;
-  int ok_r = 0;
-  auto load_tile = [&](int t0) {
+  float fw_r = 1.0f, fb_r = 0.0f;
+  auto issue = [&](int tile, i32x4 ids) {
+    const int t0 = t_begin + tile * kPfKT;
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
-      const int64_t o = key_off(t0 + kr + 32 * r);
-      if (o >= 0) {
-        kreg[r] = *reinterpret_cast<const v8*>(kbase + o);
+      const int pid = uniform(kslot ? ids[2 * r + 1] : ids[2 * r]);
+      if (page_ok(pid, p.num_pages)) {
+        kreg[r] = *reinterpret_cast<const v8*>(kbase + (int64_t)pid * p.page_stride + (int64_t)(kr & 15) * p.tok_stride);
       } else {
 #pragma unroll
         for (int e = 0; e < 8; ++e) kreg[r][e] = static_cast<T>(0.0f);
       }
     }
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int64_t o = key_off(t0 + 2 * kr + r);
-      if (o >= 0) {
-        vreg[r] = *reinterpret_cast<const v8*>(vbase + o);
+    {
+      const int pid = uniform(vslot & 2 ? (vslot & 1 ? ids[3] : ids[2]) : (vslot & 1 ? ids[1] : ids[0]));
+      if (page_ok(pid, p.num_pages)) {
+        const T* vp = vbase + (int64_t)pid * p.page_stride + (int64_t)((2 * kr) & 15) * p.tok_stride;
+        vreg[0] = *reinterpret_cast<const v8*>(vp);
+        vreg[1] = *reinterpret_cast<const v8*>(vp + p.tok_stride);
       } else {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) vreg[r][e] = static_cast<T>(0.0f);
+        for (int e = 0; e < 8; ++e) vreg[0][e] = vreg[1][e] = static_cast<T>(0.0f);
       }
     }
-    if (tid < kPfKT) {
+    if ((kVs || kBias) && tid < kPfKT) {
       const int key = t0 + tid;
-      ok_r = key_off(key) >= 0 ? 1 : 0;
-      fw_r = (ok_r && p.vscale) ? p.vscale[(int64_t)b * p.vs_bs + key] : 1.0f;
-      fb_r = (ok_r && p.bias) ? p.bias[(int64_t)b * p.bias_bs + key] : 0.0f;
+      const bool in = key < hi;
+      if (kVs) fw_r = in ? p.vscale[(int64_t)b * p.vs_bs + key] : 1.0f;
+      if (kBias) fb_r = in ? p.bias[(int64_t)b * p.bias_bs + key] * kLog2e : 0.0f;
     }
   };
-  auto store_tile = [&]() {
+  auto store = [&](int stage) {
+    T* kd = ks + stage * kKStage + 8 * kc;
 #pragma unroll
-    for (int r = 0; r < 2; ++r) *reinterpret_cast<v8*>(ks + (kr + 32 * r) * kPfKRow + 8 * kc) = kreg[r];
+    for (int r = 0; r < 2; ++r) *reinterpret_cast<v8*>(kd + (32 * r + swap23(kr)) * kKRow) = kreg[r];
+    uint32_t* vd = vts + stage * kVStage + 4 * ((kr >> 2) ^ (kc >> 1)) + (kr & 3);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const uint32_t packed = bits16(vreg[0][e]) | (bits16(vreg[1][e]) << 16);
-      *reinterpret_cast<uint32_t*>(vts + (8 * kc + e) * kPfVRow + 2 * kr) = packed;
-    }
-    if (tid < kPfKT) {
-      fws[tid] = fw_r;
-      fbs[tid] = fb_r;
-      kok[tid] = ok_r;
+    for (int e = 0; e < 8; ++e) vd[(8 * kc + e) * kVRowW] = bits16(vreg[0][e]) | (bits16(vreg[1][e]) << 16);
+    if ((kVs || kBias) && tid < kPfKT) {
+      if (kVs) fws[stage * kPfKT + tid] = fw_r;
+      if (kBias) fbs[stage * kPfKT + tid] = fb_r;
     }
   };
+
+  // S^T of the tile in a stage: lane (col, half) reads K row 32kb + col.
+  const T* kread = ks + col * kKRow + 8 * half;
+  auto qk = [&](int stage, f32x16 (&s)[2]) {
+    const T* kb0 = kread + stage * kKStage;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      s[kb] = f32x16{};
+#pragma unroll
+      for (int st = 0; st < 8; ++st)
+        s[kb] = Mma32<T>::mma(*reinterpret_cast<const v8*>(kb0 + 32 * kb * kKRow + 16 * st), qv[st], s[kb]);
+    }
+  };
+  // V^T operand: lane reads row d = 32db + col, key chunk (2s + half) stored
+  // at chunk (2s + half) ^ (d / 16) = 2(s ^ db) + (half ^ col / 16).
+  const uint32_t* vread = vts + col * kVRowW + 4 * (half ^ (col >> 4));
 
   f32x16 oacc[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) oacc[i] = f32x16{};
-  float m_run = kNegInf, l_run = 0.0f;
-  const float scale = p.sm_scale;
+  float m_run = kNegInf, l_half = 0.0f;
+  const float c2 = p.sm_scale * kLog2e;
 
+  i32x4 ids_a, ids_b;  // page ids of tiles t+2 and t+3
+  int pm0 = 0, pm1 = 0;    // valid-page masks of tiles t and t+1
+  f32x16 s_cur[2], s_nxt[2];
   if (n_tiles > 0) {
-    load_tile(t_begin);
-    store_tile();
+    const i32x4 ids0 = fetch_ids(0);
+    ids_a = fetch_ids(1);
+    pm0 = valid_mask(ids0);
+    issue(0, ids0);
+    store(0);
+    pm1 = valid_mask(ids_a);
+    issue(1, ids_a);
+    store(1);
+    ids_a = fetch_ids(2);
+    ids_b = fetch_ids(3);
+    __syncthreads();
+    qk(0, s_cur);
   }
-  __syncthreads();
-  for (int t = 0; t < n_tiles; ++t) {
+  // One tile: sc holds its scores, sn receives the next tile's.  Waves 0-3
+  // compute the next scores before this tile's softmax, waves 4-7 after it,
+  // so the two waves sharing a SIMD keep its MFMA and VALU pipes both busy.
+  const bool qk_first = (kBias && kVs) || wave < 4;  // both fog modes: no split (register budget)
+  auto step = [&](int t, f32x16 (&sc)[2], f32x16 (&sn)[2]) {
     const int t0 = t_begin + t * kPfKT;
-    const bool more = t + 1 < n_tiles;
-    if (more) load_tile(t0 + kPfKT);
-    // Interior tile: every key present and visible to every row of the
-    // workgroup (uniform), so no per-element mask.
-    bool pages_ok = t0 >= lo && t0 + kPfKT <= hi;
-    if (pages_ok) {
-#pragma unroll
-      for (int pg = 0; pg < kPfKT / 16; ++pg) {
-        const int pid = table[(t0 >> 4) + pg];
-        pages_ok = pages_ok && pid >= 0 && pid < p.num_pages;
-      }
-    }
-    const bool interior = pages_ok && t0 + kPfKT - 1 <= qmin && (p.window == 0 || t0 > qmax - p.window);
+    const int st_cur = t % kPfStages;
+    const int st_nxt = (t + 1) % kPfStages;
+    const int st_new = (t + 2) % kPfStages;
+    const bool more = t + 2 < n_tiles;
+    if (qk_first) qk(st_nxt, sn);
+    const int pm2 = valid_mask(ids_a);
+    if (more) issue(t + 2, ids_a);
+    ids_a = ids_b;
+    ids_b = fetch_ids(t + 4);
 
-    f32x16 sacc[2];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      sacc[kb] = f32x16{};
-      const T* krow = ks + (32 * kb + swap23(col)) * kPfKRow + 8 * half;
-#pragma unroll
-      for (int s = 0; s < 8; ++s) sacc[kb] = Mma32<T>::mma(*reinterpret_cast<const v8*>(krow + 16 * s), qv[s], sacc[kb]);
-    }
-    // Scores of this lane's row for keys 32kb + 16(v/8) + 8*half + (v%8).
+    // Interior tile: every key present and visible to every row (uniform).
+    const bool interior = pm0 == 0xF && t0 >= lo && t0 + kPfKT <= hi && t0 + kPfKT - 1 <= qmin &&
+                          (p.window == 0 || t0 > qmax - p.window);
+    const float* fwt = fws + st_cur * kPfKT + 8 * half;
+    const float* fbt = fbs + st_cur * kPfKT + 8 * half;
+    // Base-2 logits y = x * c2 (+ bias * log2 e); the tile max of y.
     float mloc = kNegInf;
+    if (!interior) {
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int kl = 32 * kb + 16 * (v >> 3) + 8 * half + (v & 7);
-        float s = sacc[kb][v] * scale;
-        if (p.bias) s += fbs[kl];
-        if (!(interior && row_ok)) {
-          const bool ok = row_ok && kok[kl] && key_visible(q_pos, t0 + kl, p.window, p.causal);
-          s = ok ? s : kNegInf;
+        for (int v = 0; v < 16; ++v) {
+          const int kl = 32 * kb + 16 * (v >> 3) + 8 * half + (v & 7);
+          const int key = t0 + kl;
+          const bool ok = row_ok && ((pm0 >> (2 * kb + (v >> 3))) & 1) && key >= lo && key < hi &&
+                          key_visible(q_pos, key, p.window, p.causal);
+          float y = kBias ? fmaf(sc[kb][v], c2, fbt[32 * kb + 16 * (v >> 3) + (v & 7)]) : sc[kb][v];
+          sc[kb][v] = ok ? y : kNegInf;
         }
-        sacc[kb][v] = s;
-        mloc = fmaxf(mloc, s);
-      }
-    if (!row_ok) mloc = kNegInf;
+    } else if (kBias) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) sc[kb][v] = fmaf(sc[kb][v], c2, fbt[32 * kb + 16 * (v >> 3) + (v & 7)]);
+    }
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int v = 0; v < 16; v += 2) mloc = fmaxf(mloc, fmaxf(sc[kb][v], sc[kb][v + 1]));
     mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+    if (!kBias) mloc *= c2;  // without a bias, y = x * c2 and c2 > 0
     const float mnew = fmaxf(m_run, mloc);
-    const float alpha = (m_run == kNegInf) ? 0.0f : __expf(m_run - mnew);
+    const float muse = mnew == kNegInf ? 0.0f : mnew;
+    const float alpha = mnew == kNegInf ? 1.0f : __builtin_amdgcn_exp2f(m_run - mnew);
     float psum = 0.0f;
+    v8 pb[4];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const float s = sacc[kb][v];
-        const float pr = (s == kNegInf) ? 0.0f : __expf(s - mnew);
+        const float y = sc[kb][v];
+        float pr = __builtin_amdgcn_exp2f(kBias ? y - muse : fmaf(y, c2, -muse));
         psum += pr;
-        const int kl = 32 * kb + 16 * (v >> 3) + 8 * half + (v & 7);
-        sacc[kb][v] = p.vscale ? pr * fws[kl] : pr;
+        if (kVs) pr *= fwt[32 * kb + 16 * (v >> 3) + (v & 7)];
+        pb[2 * kb + (v >> 3)][v & 7] = static_cast<T>(pr);
       }
-    psum += __shfl_xor(psum, 32);
-    l_run = l_run * alpha + psum;
+    if (!qk_first) qk(st_nxt, sn);
+    l_half = l_half * alpha + psum;
     m_run = mnew;
     if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) oacc[i] *= alpha;
     }
     // O^T += V^T P^T over four 16-key steps.
+    const uint32_t* vr = vread + st_cur * kVStage;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      v8 pb;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) pb[e] = static_cast<T>(sacc[s >> 1][8 * (s & 1) + e]);
+    for (int s = 0; s < 4; ++s)
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
-        const v8 a = *reinterpret_cast<const v8*>(vts + (32 * db + col) * kPfVRow + 16 * s + 8 * half);
-        oacc[db] = Mma32<T>::mma(a, pb, oacc[db]);
+        const v8 a = *reinterpret_cast<const v8*>(vr + 32 * db * kVRowW + 8 * (s ^ db));
+        oacc[db] = Mma32<T>::mma(a, pb[s], oacc[db]);
       }
-    }
-    __syncthreads();  // every wave is done with this tile's LDS
-    if (more) store_tile();
+
+    if (more) store(st_new);
+    pm0 = pm1;
+    pm1 = pm2;
     __syncthreads();
+  };
+  // (Unrolling by two to alternate sc/sn instead of copying them spills at
+  // 256 VGPRs, the budget of two waves per SIMD.)
+  for (int t = 0; t < n_tiles; ++t) {
+    step(t, s_cur, s_nxt);
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) s_cur[kb] = s_nxt[kb];
   }
 
   // Lane (col, half) holds row frow at d = 32*db + 8*(v/4) + 4*half + (v%4).
+  const float l = l_half + __shfl_xor(l_half, 32);
   if (!row_ok) return;
-  const float il = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+  const float il = l > 0.0f ? 1.0f / l : 0.0f;
   T* orow = static_cast<T*>(p.out) + (int64_t)b * p.o_bs + (int64_t)qi * p.o_is + (int64_t)head * p.o_hs;
 #pragma unroll
   for (int db = 0; db < 4; ++db)
@@ -276,20 +347,42 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
     }
 }
 
+template <typename T, int G, bool kBias, bool kVs>
+int launch_one(const Params& p, dim3 grid, hipStream_t stream) {
+  static bool lds_set[64] = {};  // per instance and device
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  const void* fn = reinterpret_cast<const void*>(prefill_mfma_kernel<T, G, kBias, kVs>);
+  if (!lds_set[dev]) {
+    if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPfLdsBytes) != hipSuccess) {
+      set_error(KESSIE_ERR_HIP, "fog prefill (mfma): %zu bytes of LDS unavailable", kPfLdsBytes);
+      return KESSIE_ERR_HIP;
+    }
+    lds_set[dev] = true;
+  }
+  hipLaunchKernelGGL((prefill_mfma_kernel<T, G, kBias, kVs>), grid, dim3(kPfThreads), kPfLdsBytes, stream, p);
+  return check_launch("fog prefill (mfma)");
+}
+
+template <typename T, int G>
+int launch_fog(const Params& p, dim3 grid, hipStream_t stream) {
+  if (p.bias) return p.vscale ? launch_one<T, G, true, true>(p, grid, stream) : launch_one<T, G, true, false>(p, grid, stream);
+  return p.vscale ? launch_one<T, G, false, true>(p, grid, stream) : launch_one<T, G, false, false>(p, grid, stream);
+}
+
 template <typename T>
 int launch_prefill(Params& p, hipStream_t stream) {
   const int kpos = kPfRows / p.G;
   dim3 grid(div_up(p.C, kpos) * p.Hkv, p.B);
   switch (p.G) {
-    case 1: hipLaunchKernelGGL((prefill_mfma_kernel<T, 1>), grid, dim3(kPfThreads), 0, stream, p); break;
-    case 2: hipLaunchKernelGGL((prefill_mfma_kernel<T, 2>), grid, dim3(kPfThreads), 0, stream, p); break;
-    case 4: hipLaunchKernelGGL((prefill_mfma_kernel<T, 4>), grid, dim3(kPfThreads), 0, stream, p); break;
-    case 8: hipLaunchKernelGGL((prefill_mfma_kernel<T, 8>), grid, dim3(kPfThreads), 0, stream, p); break;
+    case 1: return launch_fog<T, 1>(p, grid, stream);
+    case 2: return launch_fog<T, 2>(p, grid, stream);
+    case 4: return launch_fog<T, 4>(p, grid, stream);
+    case 8: return launch_fog<T, 8>(p, grid, stream);
     default:
       set_error(KESSIE_ERR_UNSUPPORTED, "fog prefill (mfma): GQA ratio %d", p.G);
       return KESSIE_ERR_UNSUPPORTED;
   }
-  return check_launch("fog prefill (mfma)");
 }
 
 }  // namespace
@@ -299,6 +392,7 @@ bool prefill_mfma_ok(const Params& p, int dtype) {
   if (dtype != KESSIE_DTYPE_BF16 && dtype != KESSIE_DTYPE_F16) return false;
   if (p.D != 128 || p.page_size != 16 || p.page_table == nullptr) return false;
   if (!(p.G == 1 || p.G == 2 || p.G == 4 || p.G == 8)) return false;
+  if (!(p.sm_scale > 0.0f)) return false;
   if (!aligned16(p.q) || !aligned16(p.k) || !aligned16(p.v) || !aligned16(p.out)) return false;
   if (p.page_stride % 8 || p.tok_stride % 8 || p.head_stride % 8) return false;
   if (p.q_bs % 8 || p.q_is % 8 || p.q_hs % 8 || p.o_bs % 4 || p.o_is % 4 || p.o_hs % 4) return false;
