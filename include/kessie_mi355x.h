@@ -298,6 +298,47 @@ int kessie_page_gather(const void* src_pool, int64_t page_bytes,
                        const int32_t* idx, const int32_t* count_dev, int n,
                        int num_pages, void* dst, void* stream);
 
+/* =========================================================================
+ * Producers around the attention call
+ * ========================================================================= */
+
+/* Fog logit bias of the serving path into buf[0:kv_len] (`dtype` elements),
+ * replacing _FogCache._compute_into (kessie_attention.py:114-139): with
+ * B = int(kv_len * (1.0 - fog_start)) (double arithmetic, as in Python),
+ * buf[p] = -fog_alpha * (1 - p/B)^2 for p < B, 0 otherwise, every op rounded
+ * to `dtype` as torch's device kernels round it (p/B as p * fp32(1/B)); then
+ * buf[r] = dtype(recall_boost) for each recall_positions[r] in [0, kv_len)
+ * (num_recall int32 device values; duplicates allowed).  One launch for the
+ * vector plus one for the recall scatter; no host synchronisation. */
+int kessie_fog_bias_fill(void* buf, int dtype, int kv_len, double fog_alpha,
+                         double fog_start, const int32_t* recall_positions,
+                         int num_recall, double recall_boost, void* stream);
+
+/* Fog V weights (fp32) into weights[0:seq_len], replacing
+ * kessie_build_fog_weights (kessie_hip_kernels.py:403-413): 1 everywhere;
+ * with c = int(seq_len * (1.0 - fog_start)) and fog_alpha > 0,
+ * weights[i] = (i * fp32(1/max(c-1,1)))^fog_alpha for i < c, the power taken
+ * the way torch's device pow(tensor, scalar) takes it (sqrt for 0.5, products
+ * for 2 and 3, powf otherwise). */
+int kessie_fog_weights_fill(float* weights, int seq_len, double fog_alpha,
+                            double fog_start, void* stream);
+
+/* Slot-mapped write of new K/V rows into the paged cache (the write a
+ * serving backend performs before attention): for token t < num_tokens with
+ * slot = slot_mapping[t] >= 0 and slot / page_size < num_pages, copies
+ * key[t][h][:] and value[t][h][:] (source strides in elements; innermost
+ * dimension contiguous) to page slot/page_size, offset slot%page_size of the
+ * pool.  Negative slots (padding) are skipped. */
+int kessie_kv_cache_write(void* kv_pool, int64_t page_stride,
+                          int64_t tok_stride, int64_t kv_stride,
+                          int64_t head_stride, const void* key,
+                          int64_t key_tok_stride, int64_t key_head_stride,
+                          const void* value, int64_t value_tok_stride,
+                          int64_t value_head_stride,
+                          const int64_t* slot_mapping, int num_tokens,
+                          int num_kv_heads, int head_dim, int page_size,
+                          int num_pages, int dtype, void* stream);
+
 #if defined(__GNUC__) || defined(__clang__)
 #pragma GCC visibility pop
 #endif

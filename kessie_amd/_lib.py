@@ -26,6 +26,7 @@ _P = C.c_void_p
 _I = C.c_int
 _I64 = C.c_int64
 _F = C.c_float
+_D = C.c_double
 _SZ = C.c_size_t
 
 # name -> (restype, argtypes).  Kept in the order of include/kessie_mi355x.h.
@@ -68,6 +69,13 @@ SIGNATURES = {
     "kessie_page_compact": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _SZ, _P]),
     "kessie_page_valid_list": (_I, [_P, _I, _P, _P, _P, _SZ, _P]),
     "kessie_page_gather": (_I, [_P, _I64, _P, _P, _I, _I, _P, _P]),
+    # buf, dtype, kv_len, fog_alpha, fog_start, recall, num_recall, boost, stream
+    "kessie_fog_bias_fill": (_I, [_P, _I, _I, _D, _D, _P, _I, _D, _P]),
+    "kessie_fog_weights_fill": (_I, [_P, _I, _D, _D, _P]),
+    # pool + 4 strides, key + 2 strides, value + 2 strides, slots, T, H, D, P, pages, dtype, stream
+    "kessie_kv_cache_write": (_I, [
+        _P, _I64, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P,
+        _I, _I, _I, _I, _I, _I, _P]),
 }
 
 _lock = threading.Lock()

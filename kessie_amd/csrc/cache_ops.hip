@@ -1,0 +1,255 @@
+// Producers around the attention call for gfx950:
+//   * the fog vectors -- the logit bias of the serving path
+//     (_FogCache._compute_into, kessie_attention.py:114-139) and the V weights
+//     (kessie_build_fog_weights, kessie_hip_kernels.py:403-413) -- computed in
+//     one pass on the device instead of a chain of torch ops plus one
+//     host-driven scalar write per recalled position;
+//   * the slot-mapped write of new K/V rows into the paged cache (the step the
+//     serving backend takes before attention: token t goes to page
+//     slot[t] / P, offset slot[t] % P).
+//
+// The fog arithmetic follows the reference's op sequence as torch runs it on
+// the device, rounding to the buffer dtype after every op:
+//   pos = dtype(i)                      arange in the buffer dtype
+//   x   = dtype(f32(pos) * (1/B))       tensor / python scalar: torch's device
+//                                       kernel multiplies by the fp32 reciprocal
+//   d   = dtype(1 - f32(x))
+//   d2  = dtype(f32(d) * f32(d))        decay.mul_(decay)
+//   b   = dtype(f32(d2) * f32(-alpha))  decay.mul_(-fog_alpha)
+// and recalled positions are overwritten with dtype(recall_boost).
+#include "common.h"
+
+namespace kessie {
+namespace cache {
+namespace {
+
+constexpr int kThreads = 256;
+
+template <typename T>
+__device__ __forceinline__ T round_to(float x) {
+  return from_f32<T>(x);
+}
+template <>
+__device__ __forceinline__ float round_to<float>(float x) {
+  return x;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void fog_bias_kernel(T* buf, int kv_len, int boundary, float inv_b,
+                                                            float neg_alpha) {
+#pragma clang fp contract(off)
+  const int i = blockIdx.x * kThreads + threadIdx.x;
+  if (i >= kv_len) return;
+  T v = round_to<T>(0.0f);
+  if (i < boundary) {
+    const T pos = round_to<T>((float)i);
+    const T x = round_to<T>(to_f32(pos) * inv_b);
+    const T d = round_to<T>(1.0f - to_f32(x));
+    const T d2 = round_to<T>(to_f32(d) * to_f32(d));
+    v = round_to<T>(to_f32(d2) * neg_alpha);
+  }
+  buf[i] = v;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void recall_scatter_kernel(T* buf, int kv_len, const int32_t* pos, int n,
+                                                                  float boost) {
+  const int r = blockIdx.x * kThreads + threadIdx.x;
+  if (r >= n) return;
+  const int p = pos[r];
+  if (p >= 0 && p < kv_len) buf[p] = round_to<T>(boost);
+}
+
+// Exponent forms torch's device pow(tensor, scalar) special-cases, so the
+// weights take the same arithmetic route (alpha > 0 only reaches here).
+enum PowForm { kPowGeneral = 0, kPowOne = 1, kPowHalf = 2, kPowTwo = 3, kPowThree = 4 };
+
+__global__ __launch_bounds__(kThreads) void fog_weights_kernel(float* w, int n, int clear_start, float inv_den,
+                                                               float alpha, int form) {
+#pragma clang fp contract(off)
+  const int i = blockIdx.x * kThreads + threadIdx.x;
+  if (i >= n) return;
+  float v = 1.0f;
+  if (i < clear_start) {
+    const float t = (float)i * inv_den;
+    switch (form) {
+      case kPowOne: v = t; break;
+      case kPowHalf: v = sqrtf(t); break;
+      case kPowTwo: v = t * t; break;
+      case kPowThree: v = t * t * t; break;
+      default: v = powf(t, alpha); break;
+    }
+  }
+  w[i] = v;
+}
+
+template <typename T>
+int fog_bias_launch(void* buf, int kv_len, int boundary, float inv_b, float neg_alpha, const int32_t* recall,
+                    int n_recall, float boost, hipStream_t s) {
+  T* b = static_cast<T*>(buf);
+  hipLaunchKernelGGL(fog_bias_kernel<T>, dim3(div_up(kv_len, kThreads)), dim3(kThreads), 0, s, b, kv_len, boundary,
+                     inv_b, neg_alpha);
+  if (n_recall > 0)
+    hipLaunchKernelGGL(recall_scatter_kernel<T>, dim3(div_up(n_recall, kThreads)), dim3(kThreads), 0, s, b, kv_len,
+                       recall, n_recall, boost);
+  return check_launch("fog bias");
+}
+
+// ---- slot-mapped K/V write -------------------------------------------------
+
+struct WriteArgs {
+  void* pool;
+  int64_t page_stride, tok_stride, kv_stride, head_stride;
+  const void* key;
+  const void* value;
+  int64_t k_ts, k_hs, v_ts, v_hs;  // source token / head strides (elements)
+  const int64_t* slots;
+  int T, H, D, page_size, num_pages;
+};
+
+// One thread per 16-byte chunk of one (token, head) row of K and of V.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void kv_write_vec_kernel(WriteArgs a) {
+  constexpr int N = 16 / (int)sizeof(T);
+  const int chunks = a.D / N;
+  const int64_t total = (int64_t)a.T * a.H * chunks;
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= total) return;
+  const int c = (int)(i % chunks);
+  const int64_t th = i / chunks;
+  const int h = (int)(th % a.H);
+  const int t = (int)(th / a.H);
+  const int64_t slot = a.slots[t];
+  if (slot < 0) return;
+  const int64_t page = slot / a.page_size;
+  if (page >= a.num_pages) return;
+  T* pool = static_cast<T*>(a.pool);
+  const int64_t dst = page * a.page_stride + (slot % a.page_size) * a.tok_stride + h * a.head_stride + c * N;
+  const u32x4 kx = *reinterpret_cast<const u32x4*>(static_cast<const T*>(a.key) + t * a.k_ts + h * a.k_hs + c * N);
+  const u32x4 vx = *reinterpret_cast<const u32x4*>(static_cast<const T*>(a.value) + t * a.v_ts + h * a.v_hs + c * N);
+  *reinterpret_cast<u32x4*>(pool + dst) = kx;
+  *reinterpret_cast<u32x4*>(pool + dst + a.kv_stride) = vx;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void kv_write_scalar_kernel(WriteArgs a) {
+  const int64_t total = (int64_t)a.T * a.H * a.D;
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= total) return;
+  const int d = (int)(i % a.D);
+  const int64_t th = i / a.D;
+  const int h = (int)(th % a.H);
+  const int t = (int)(th / a.H);
+  const int64_t slot = a.slots[t];
+  if (slot < 0) return;
+  const int64_t page = slot / a.page_size;
+  if (page >= a.num_pages) return;
+  T* pool = static_cast<T*>(a.pool);
+  const int64_t dst = page * a.page_stride + (slot % a.page_size) * a.tok_stride + h * a.head_stride + d;
+  pool[dst] = static_cast<const T*>(a.key)[t * a.k_ts + h * a.k_hs + d];
+  pool[dst + a.kv_stride] = static_cast<const T*>(a.value)[t * a.v_ts + h * a.v_hs + d];
+}
+
+template <typename T>
+int kv_write_launch(const WriteArgs& a, hipStream_t s) {
+  constexpr int N = 16 / (int)sizeof(T);
+  const bool vec = a.D % N == 0 && aligned16(a.pool) && aligned16(a.key) && aligned16(a.value) &&
+                   a.page_stride % N == 0 && a.tok_stride % N == 0 && a.kv_stride % N == 0 && a.head_stride % N == 0 &&
+                   a.k_ts % N == 0 && a.k_hs % N == 0 && a.v_ts % N == 0 && a.v_hs % N == 0;
+  const int64_t items = (int64_t)a.T * a.H * (vec ? a.D / N : a.D);
+  const int64_t grid = (items + kThreads - 1) / kThreads;
+  KESSIE_REQUIRE(grid <= 0x7fffffff, KESSIE_ERR_UNSUPPORTED, "kv cache write: %lld items exceed one launch",
+                 (long long)items);
+  if (vec)
+    hipLaunchKernelGGL(kv_write_vec_kernel<T>, dim3((unsigned)grid), dim3(kThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL(kv_write_scalar_kernel<T>, dim3((unsigned)grid), dim3(kThreads), 0, s, a);
+  return check_launch("kv cache write");
+}
+
+}  // namespace
+}  // namespace cache
+}  // namespace kessie
+
+using namespace kessie;
+using namespace kessie::cache;
+
+extern "C" int kessie_fog_bias_fill(void* buf, int dtype, int kv_len, double fog_alpha, double fog_start,
+                                    const int32_t* recall_positions, int num_recall, double recall_boost,
+                                    void* stream) {
+  clear_error();
+  KESSIE_REQUIRE(kv_len >= 0 && num_recall >= 0, KESSIE_ERR_INVALID, "fog bias: kv_len %d, num_recall %d", kv_len,
+                 num_recall);
+  if (kv_len == 0) return KESSIE_OK;
+  KESSIE_REQUIRE(buf != nullptr, KESSIE_ERR_INVALID, "fog bias: null buffer");
+  KESSIE_REQUIRE(num_recall == 0 || recall_positions != nullptr, KESSIE_ERR_INVALID, "fog bias: null recall list");
+  // B = int(kv_len * (1.0 - fog_start)) in double, as the reference's Python
+  // does; the decay divides by B itself and covers positions < min(B, kv_len).
+  const double bd = (double)kv_len * (1.0 - fog_start);
+  KESSIE_REQUIRE(bd < 2147483648.0, KESSIE_ERR_INVALID, "fog bias: fog boundary %.0f out of range", bd);
+  const int64_t big_b = bd <= 0.0 ? 0 : (int64_t)bd;
+  const int boundary = (int)(big_b < kv_len ? big_b : kv_len);
+  const float inv_b = big_b > 0 ? 1.0f / (float)big_b : 0.0f;
+  const float neg_alpha = (float)(-fog_alpha);
+  const float boost = (float)recall_boost;
+  const hipStream_t s = as_stream(stream);
+  switch (dtype) {
+    case KESSIE_DTYPE_F32:
+      return fog_bias_launch<float>(buf, kv_len, boundary, inv_b, neg_alpha, recall_positions, num_recall, boost, s);
+    case KESSIE_DTYPE_BF16:
+      return fog_bias_launch<bf16_t>(buf, kv_len, boundary, inv_b, neg_alpha, recall_positions, num_recall, boost, s);
+    case KESSIE_DTYPE_F16:
+      return fog_bias_launch<f16_t>(buf, kv_len, boundary, inv_b, neg_alpha, recall_positions, num_recall, boost, s);
+  }
+  set_error(KESSIE_ERR_UNSUPPORTED, "fog bias: dtype %d", dtype);
+  return KESSIE_ERR_UNSUPPORTED;
+}
+
+extern "C" int kessie_fog_weights_fill(float* weights, int seq_len, double fog_alpha, double fog_start, void* stream) {
+  clear_error();
+  KESSIE_REQUIRE(seq_len >= 0, KESSIE_ERR_INVALID, "fog weights: seq_len %d", seq_len);
+  if (seq_len == 0) return KESSIE_OK;
+  KESSIE_REQUIRE(weights != nullptr, KESSIE_ERR_INVALID, "fog weights: null buffer");
+  // c = int(N * (1.0 - fog_start)); c > N (fog_start < 0) is a shape error in
+  // the reference and is clamped to N here.
+  const double cd = (double)seq_len * (1.0 - fog_start);
+  int clear_start = cd <= 0.0 ? 0 : (cd >= (double)seq_len ? seq_len : (int)cd);
+  if (!(fog_alpha > 0.0)) clear_start = 0;  // weights stay 1
+  const float inv_den = 1.0f / (float)(clear_start - 1 > 1 ? clear_start - 1 : 1);
+  const float a = (float)fog_alpha;
+  int form = kPowGeneral;
+  if (fog_alpha == 1.0) form = kPowOne;
+  else if (fog_alpha == 0.5) form = kPowHalf;
+  else if (fog_alpha == 2.0) form = kPowTwo;
+  else if (fog_alpha == 3.0) form = kPowThree;
+  hipLaunchKernelGGL(fog_weights_kernel, dim3(div_up(seq_len, kThreads)), dim3(kThreads), 0, as_stream(stream),
+                     weights, seq_len, clear_start, inv_den, a, form);
+  return check_launch("fog weights");
+}
+
+extern "C" int kessie_kv_cache_write(void* kv_pool, int64_t page_stride, int64_t tok_stride, int64_t kv_stride,
+                                     int64_t head_stride, const void* key, int64_t key_tok_stride,
+                                     int64_t key_head_stride, const void* value, int64_t value_tok_stride,
+                                     int64_t value_head_stride, const int64_t* slot_mapping, int num_tokens,
+                                     int num_kv_heads, int head_dim, int page_size, int num_pages, int dtype,
+                                     void* stream) {
+  clear_error();
+  KESSIE_REQUIRE(num_tokens >= 0 && num_kv_heads > 0 && head_dim > 0 && page_size > 0 && num_pages >= 0,
+                 KESSIE_ERR_INVALID, "kv cache write: bad sizes T=%d H=%d D=%d P=%d pages=%d", num_tokens,
+                 num_kv_heads, head_dim, page_size, num_pages);
+  if (num_tokens == 0 || num_pages == 0) return KESSIE_OK;
+  KESSIE_REQUIRE(kv_pool && key && value && slot_mapping, KESSIE_ERR_INVALID, "kv cache write: null pointer");
+  KESSIE_REQUIRE(head_stride >= head_dim && tok_stride >= (int64_t)num_kv_heads * head_stride && kv_stride > 0,
+                 KESSIE_ERR_INVALID, "kv cache write: pool strides overlap");
+  WriteArgs a{kv_pool, page_stride, tok_stride, kv_stride, head_stride, key, value, key_tok_stride, key_head_stride,
+              value_tok_stride, value_head_stride, slot_mapping, num_tokens, num_kv_heads, head_dim, page_size,
+              num_pages};
+  const hipStream_t s = as_stream(stream);
+  switch (dtype) {
+    case KESSIE_DTYPE_BF16: return kv_write_launch<bf16_t>(a, s);
+    case KESSIE_DTYPE_F16: return kv_write_launch<f16_t>(a, s);
+    case KESSIE_DTYPE_F32: return kv_write_launch<float>(a, s);
+  }
+  set_error(KESSIE_ERR_UNSUPPORTED, "kv cache write: dtype %d", dtype);
+  return KESSIE_ERR_UNSUPPORTED;
+}

@@ -465,3 +465,69 @@ def page_gather(pool: torch.Tensor, idx: torch.Tensor, count: Optional[torch.Ten
         _ptr(pool), page_bytes, _ptr(_contig(idx, "idx")), _ptr(count), int(n), num_pages, _ptr(out),
         _stream_ptr(stream, pool.device)))
     return out
+
+
+# ---------------------------------------------------------------------------
+# Producers around the attention call
+# ---------------------------------------------------------------------------
+def fog_bias_fill(buf: torch.Tensor, kv_len: int, fog_alpha: float, fog_start: float,
+                  recall_positions: Optional[torch.Tensor] = None, recall_boost: float = 0.1,
+                  stream=None) -> torch.Tensor:
+    """Fog logit bias into buf[:kv_len] in buf's dtype (the device version of
+    _FogCache._compute_into, kessie_attention.py:114-139).  recall_positions:
+    int32 device tensor (any order, duplicates allowed) or None.  Returns the
+    buf[:kv_len] view."""
+    if buf.dim() != 1 or not buf.is_contiguous():
+        raise ValueError("buf must be a contiguous 1-D tensor")
+    if kv_len < 0 or kv_len > buf.numel():
+        raise ValueError(f"kv_len {kv_len} outside [0, {buf.numel()}]")
+    n = 0
+    if recall_positions is not None:
+        if recall_positions.dtype != torch.int32 or recall_positions.device != buf.device:
+            raise TypeError("recall_positions must be int32 on the buffer's device")
+        recall_positions = _contig(recall_positions.reshape(-1), "recall_positions")
+        n = recall_positions.numel()
+    lib = _lib.load()
+    _lib.check("kessie_fog_bias_fill", lib.kessie_fog_bias_fill(
+        _ptr(buf), dtype_code(buf.dtype), int(kv_len), float(fog_alpha), float(fog_start),
+        _ptr(recall_positions) if n else None, n, float(recall_boost), _stream_ptr(stream, buf.device)))
+    return buf[:kv_len]
+
+
+def fog_weights(seq_len: int, fog_alpha: float = 0.5, fog_start: float = 0.5, device=None,
+                out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """Fog V weights, fp32 [seq_len], computed on the device (the device
+    version of kessie_build_fog_weights, kessie_hip_kernels.py:403-413)."""
+    if out is None:
+        out = torch.empty(seq_len, dtype=torch.float32, device=device or "cuda")
+    if out.dtype != torch.float32 or out.dim() != 1 or not out.is_contiguous() or out.numel() < seq_len:
+        raise ValueError("out must be a contiguous fp32 vector of at least seq_len elements")
+    lib = _lib.load()
+    _lib.check("kessie_fog_weights_fill", lib.kessie_fog_weights_fill(
+        _ptr(out), int(seq_len), float(fog_alpha), float(fog_start), _stream_ptr(stream, out.device)))
+    return out[:seq_len]
+
+
+def kv_cache_write(pool: torch.Tensor, key: torch.Tensor, value: torch.Tensor, slot_mapping: torch.Tensor,
+                   layout: str = "native", stream=None) -> None:
+    """Write key/value [T, Hkv, D] (any token/head strides, D contiguous) into
+    the paged pool at slot_mapping[t] (int64; page = slot // P, offset
+    slot % P; negative slots skipped)."""
+    pv = pool_view(pool, layout)
+    if key.dim() != 3 or value.shape != key.shape:
+        raise ValueError("key/value must both be [T, Hkv, D]")
+    t, h, d = key.shape
+    if h != pv.num_kv_heads or d != pv.head_dim:
+        raise ValueError("key/value heads or head_dim do not match the pool")
+    if key.dtype != pool.dtype or value.dtype != pool.dtype:
+        raise TypeError("key/value dtype must match the pool")
+    if key.stride(2) != 1 or value.stride(2) != 1:
+        raise ValueError("key/value head_dim axis must be contiguous")
+    if slot_mapping.dtype != torch.int64 or slot_mapping.numel() < t:
+        raise ValueError("slot_mapping must be int64 with one entry per token")
+    lib = _lib.load()
+    _lib.check("kessie_kv_cache_write", lib.kessie_kv_cache_write(
+        C.c_void_p(pv.k_ptr), pv.page_stride, pv.tok_stride, pv.kv_stride, pv.head_stride,
+        _ptr(key), key.stride(0), key.stride(1), _ptr(value), value.stride(0), value.stride(1),
+        _ptr(_contig(slot_mapping, "slot_mapping")), t, h, d, pv.page_size, pv.num_pages,
+        dtype_code(pool.dtype), _stream_ptr(stream, pool.device)))

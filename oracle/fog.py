@@ -28,19 +28,24 @@ def build_fog_weights(seq_len: int, fog_alpha: float = 0.5, fog_start: float = 0
 
 def fog_bias(kv_len: int, fog_alpha: float, fog_start: float,
              recall_positions: Iterable[int] = (), recall_boost: float = 0.1,
-             dtype: torch.dtype = torch.float32, alloc_len: int | None = None) -> torch.Tensor:
+             dtype: torch.dtype = torch.float32, alloc_len: int | None = None,
+             device=None) -> torch.Tensor:
     """_FogCache._compute_into (kessie_attention.py:114-139), restated op for op.
 
     Returns buf[:kv_len] computed in ``dtype`` exactly as the reference does it
     (arange in that dtype, in-place mul_ chain), including the per-position
     recall overwrite.  ``alloc_len`` mimics the reference's larger buffer.
+    ``device`` runs the same ops where the reference runs them in serving (on
+    the query's device); torch's CPU kernel divides by the boundary where its
+    device kernel multiplies by the fp32 reciprocal, so the two can differ in
+    the last place.
     """
     n = max(kv_len, alloc_len or 0)
-    buf = torch.zeros(n, dtype=dtype)
+    buf = torch.zeros(n, dtype=dtype, device=device)
     fog_boundary = int(kv_len * (1.0 - fog_start))
     buf[:kv_len].zero_()
     if fog_boundary > 0:
-        pos = torch.arange(fog_boundary, dtype=buf.dtype)
+        pos = torch.arange(fog_boundary, dtype=buf.dtype, device=buf.device)
         decay = (1.0 - pos / fog_boundary)
         decay.mul_(decay)
         decay.mul_(-fog_alpha)

@@ -1,0 +1,171 @@
+"""CPU: the Python surface mirrored from kessie_attention.py and
+kessie_kv_connector.py -- state, backend metadata, impl argument parsing,
+the CPU KV store (eviction order pinned against the reference's linear-scan
+restatement in oracle/store.py) and the connector's scheduler-side hooks."""
+import random
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.store import StoreModel
+
+
+def test_attention_state_update_and_get():
+    from kessie_amd.kessie_attention import KESSIE_STATE, KeSSieAttentionState
+
+    st = KeSSieAttentionState()
+    assert st.get() == {"fog_alpha": 0.5, "fog_start": 0.5, "prompt_len": 0, "recall_positions": set(),
+                        "recall_boost": 0.1, "enabled": True, "generation": 0}
+    st.update(fog_alpha=0.8, recall_positions=[3, 5, 3])
+    g = st.get()
+    assert g["fog_alpha"] == 0.8 and g["recall_positions"] == {3, 5} and g["generation"] == 1
+    g["recall_positions"].add(99)  # get() returns a copy
+    assert st.get()["recall_positions"] == {3, 5}
+    st.update()
+    assert st.get()["generation"] == 2
+    assert isinstance(KESSIE_STATE, KeSSieAttentionState)
+
+
+def test_backend_surface_without_vllm():
+    from kessie_amd import kessie_attention as ka
+
+    assert ka.KeSSieAttentionBackend.get_name() == "KeSSie"
+    assert ka.KeSSieAttentionBackend.get_impl_cls() is ka.KeSSieAttentionImpl
+    if not ka.HAS_VLLM:
+        assert ka.register_kessie_attention() is False
+        assert ka.KeSSieAttentionBackend.get_metadata_cls() is ka.KeSSieAttentionMetadata
+        assert ka.KeSSieAttentionBackend.get_kv_cache_shape(100, 16, 8, 128) == (2, 100, 16, 8, 128)
+
+
+def test_impl_arguments_follow_vllm_order():
+    from kessie_amd.kessie_attention import KeSSieAttentionImpl
+
+    a = KeSSieAttentionImpl(32, 128, 0.125, 8, None, 1024)
+    assert (a.num_heads, a.head_size, a.scale, a.num_kv_heads, a.window) == (32, 128, 0.125, 8, 1024)
+    b = KeSSieAttentionImpl(num_heads=8, head_size=64, scale=None, sliding_window=(127, 0))
+    assert b.num_kv_heads == 8 and b.window == 128 and b.scale == pytest.approx(64 ** -0.5)
+    assert not b.unsupported
+    assert KeSSieAttentionImpl(8, 64, 0.1, 8, None, None, "auto", 30.0).unsupported
+    with pytest.raises(AttributeError):
+        _ = a.some_inner_attribute  # no inner impl without vLLM
+
+
+def _block(nbytes):
+    return torch.zeros(nbytes, dtype=torch.uint8)
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2, 3])
+def test_store_eviction_matches_reference_scan(seed):
+    """Random saves (new keys, replacements, timestamp ties) under a byte
+    budget: the heap-based store evicts exactly what the reference's
+    min-over-dict scan evicts, and keeps the same byte count."""
+    from kessie_amd.kessie_kv_connector import KeSSieCPUKVStore
+
+    rng = random.Random(seed)
+    budget = 2000
+    store = KeSSieCPUKVStore(max_cpu_bytes=budget)
+    model = StoreModel(max_cpu_bytes=budget)
+    evicted = []
+    orig = store._evict_oldest
+
+    def spy():
+        before = set(store._blocks)
+        orig()
+        evicted.extend(sorted(before - set(store._blocks)))
+    store._evict_oldest = spy
+    for step in range(400):
+        key = (f"layer{rng.randrange(3)}", rng.randrange(40))
+        nbytes = rng.choice([50, 100, 150, 200])
+        ts = float(rng.randrange(60))  # many ties
+        pos = rng.randrange(10) * 16
+        store._insert(key[0], key[1], _block(nbytes), [], pos, timestamp=ts)
+        model.save(key, nbytes, pos, ts)
+        assert store.total_bytes == model.total_bytes
+        assert set(store._blocks) == set(model.blocks)
+    assert evicted == model.evicted
+    assert len(evicted) > 50
+
+
+def test_store_lookup_and_stats():
+    from kessie_amd.kessie_kv_connector import KeSSieCPUKVStore
+
+    s = KeSSieCPUKVStore()
+    s.save_block("L0", 7, torch.ones(2, 16, 2, 4), list(range(16)), 32)
+    s.save_block("L1", 7, torch.ones(2, 16, 2, 4), list(range(16)), 32)
+    b = s.get_blocks_for_positions(32, 48, "L1")
+    assert b is not None and b.layer_name == "L1" and b.position_end == 48
+    assert s.get_blocks_for_positions(16, 32, "L1") is None
+    assert set(s.get_all_blocks_for_range(0, 64)) == {"L0", "L1"}
+    st = s.stats()
+    assert st["total_blocks"] == 2 and st["total_bytes"] == 2 * 2 * 16 * 2 * 4 * 4
+
+
+def test_semantic_search_ranks_by_cosine():
+    from kessie_amd.kessie_kv_connector import KeSSieCPUKVStore
+
+    vecs = {"a": np.array([1.0, 0.0]), "b": np.array([0.6, 0.8]), "c": np.array([0.0, 1.0]),
+            "q": np.array([1.0, 0.1])}
+
+    class Tok:
+        def decode(self, ids, skip_special_tokens=True):
+            return ids[0]
+
+    s = KeSSieCPUKVStore()
+    s.set_embedder(lambda text: vecs[text])
+    for i, name in enumerate("abc"):
+        s.save_semantic_entry([name], i * 100, tokenizer=Tok())
+    res = s.semantic_search("q", top_k=2)
+    assert [r[0] for r in res] == [0, 100]
+    assert res[0][2] == pytest.approx(float(vecs["q"] @ vecs["a"] / np.linalg.norm(vecs["q"])))
+    assert [r[0] for r in s.semantic_search("q", top_k=5, exclude_positions={0})] == [100, 200]
+
+
+class _Req:
+    def __init__(self, rid, toks):
+        self.request_id = rid
+        self.prompt_token_ids = toks
+
+
+class _Blocks:
+    def __init__(self, ids):
+        self._ids = ids
+
+    def get_block_ids(self):
+        return [self._ids]
+
+
+def test_connector_scheduler_hooks(monkeypatch):
+    from kessie_amd import kessie_kv_connector as kc
+
+    monkeypatch.setattr(kc, "_KESSIE_STORE", None)
+    monkeypatch.setattr(kc, "_RECALL_STATES", {})
+    conn = kc.KeSSieKVConnector(kv_connector_extra_config={"max_cpu_gb": 1})
+    hits = [(0, 48, 0.9), (64, 80, 0.2), (128, 160, 0.5)]
+    monkeypatch.setattr(conn.store, "semantic_search", lambda text, top_k=5, exclude_positions=None: hits)
+    req = _Req("r1", list(range(200)))
+    assert conn.get_num_new_matched_tokens(req) == 48 + 32
+    st = kc._RECALL_STATES["r1"]
+    assert st.recalled_positions == [(0, 48), (128, 160)] and st.load_pending
+    assert conn.get_num_new_matched_tokens(req) == 80  # cached per request
+    conn.update_state_after_alloc(req, _Blocks([9, 4, 7, 1, 3, 8, 2]), 80)
+    assert st.target_block_ids == [9, 4, 7, 1, 3]
+    assert conn.get_num_new_matched_tokens(_Req("r2", [])) == 0
+    assert conn.build_connector_meta(None) is None
+    assert conn.request_finished(req, [9, 4]) == (False, None)
+    assert "r1" not in kc._RECALL_STATES
+
+
+def test_connector_save_plan_uses_slot_mapping():
+    from kessie_amd import kessie_kv_connector as kc
+
+    class Meta:
+        block_table = torch.tensor([[5, 2, 9, 0], [7, 1, 0, 0]], dtype=torch.int32)
+        seq_lens = torch.tensor([40, 20], dtype=torch.int32)
+        # Step wrote seq 0's tokens 32..39 (block 9) and seq 1's token 19 (block 1).
+        slot_mapping = torch.tensor([9 * 16 + i for i in range(8)] + [1 * 16 + 3, -1], dtype=torch.int64)
+
+    conn = kc.KeSSieKVConnector()
+    meta = Meta()
+    assert conn._save_plan(meta) == [(9, 32, 8), (1, 16, 4)]
+    assert conn._save_plan(meta) is conn._plan  # cached per metadata object
