@@ -364,6 +364,103 @@ def bench_decode_fp32(dev, reps=20):
             "ms": round(ms, 5), "gbs": round(s["bytes"] / (ms * 1e-3) / 1e9, 1)}
 
 
+def bench_fog_bias(dev, reps=50, kv_len=131072, n_recall=1000):
+    """Fog logit bias of the serving path, bf16 over a 131,072-token context
+    with 1,000 recalled positions (alpha 0.5, fog_start 0.5, boost 0.1): the
+    device producer, and the reference's torch op sequence with its
+    per-position recall writes on the host cores as the CPU baseline."""
+    import torch
+
+    from kessie_amd import ops
+
+    g = torch.Generator().manual_seed(5)
+    recall = torch.randperm(kv_len, generator=g)[:n_recall].to(torch.int32)
+    rec_dev = recall.to(dev)
+    buf = torch.empty(kv_len, dtype=torch.bfloat16, device=dev)
+    ops.fog_bias_fill(buf, kv_len, 0.5, 0.5, rec_dev, 0.1)
+    torch.cuda.synchronize()
+    e0, e1 = events(reps), events(reps)
+    backlog()
+    for i in range(reps):
+        e0[i].record()
+        ops.fog_bias_fill(buf, kv_len, 0.5, 0.5, rec_dev, 0.1)
+        e1[i].record()
+    torch.cuda.synchronize()
+    us = 1000.0 * sum(a.elapsed_time(b) for a, b in zip(e0, e1)) / reps
+    from oracle.fog import fog_bias
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    rl = recall.tolist()
+    fog_bias(kv_len, 0.5, 0.5, rl, 0.1, dtype=torch.bfloat16)
+    t0 = time.perf_counter()
+    cpu_reps = 3
+    for _ in range(cpu_reps):
+        fog_bias(kv_len, 0.5, 0.5, rl, 0.1, dtype=torch.bfloat16)
+    cpu_ms = 1000.0 * (time.perf_counter() - t0) / cpu_reps
+    return {"workload": "fog bias bf16, 131,072 positions, 1,000 recalled positions", "us": round(us, 2),
+            "launches": 2, "cpu_baseline": {"value": round(cpu_ms, 3), "unit": "ms", "cores": cores,
+                                            "kind": "port", "sample": "the full vector, 3 reps"}}
+
+
+def bench_recall_inject(dev, reps=20, n_tok=65536, hkv=8, d=128, theta=500000.0):
+    """Recall-inject: 65,536 recalled tokens (K and V, bf16, 8 kv heads,
+    head_dim 128) already staged in HBM written into 4,096 random pages of an
+    8,192-page pool with K re-rotated from its original to its new positions
+    (fused insert + RoPE remap); also the pinned host-to-device rate of the
+    staging copy that precedes it."""
+    import torch
+
+    from kessie_amd import ops
+
+    n_pages = 2 * n_tok // 16
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    pool = torch.randn(n_pages, 16, 2, hkv, d, generator=g, device=dev).bfloat16()
+    new_k = torch.randn(n_tok, hkv, d, generator=g, device=dev).bfloat16()
+    new_v = torch.randn(n_tok, hkv, d, generator=g, device=dev).bfloat16()
+    g.manual_seed(1)
+    tgt_pages = torch.randperm(n_pages, generator=g, device=dev)[: n_tok // 16].to(torch.int32)
+    orig = torch.randint(0, 1_000_000, (n_tok,), generator=g, device=dev, dtype=torch.int32)
+    tgt = torch.arange(n_tok, dtype=torch.int32, device=dev)
+    valid = torch.zeros(n_pages, dtype=torch.int8, device=dev)
+    positions = torch.zeros(n_pages, dtype=torch.int32, device=dev)
+
+    def run():
+        ops.page_insert(pool, new_k, new_v, tgt_pages, valid, positions, 0, orig_pos=orig, tgt_pos=tgt,
+                        rope_theta=theta)
+
+    run()
+    torch.cuda.synchronize()
+    e0, e1 = events(reps), events(reps)
+    backlog()
+    for i in range(reps):
+        e0[i].record()
+        run()
+        e1[i].record()
+    torch.cuda.synchronize()
+    ms = sum(a.elapsed_time(b) for a, b in zip(e0, e1)) / reps
+    kv_bytes = n_tok * hkv * d * 2
+    nbytes = 4 * kv_bytes + 2 * 4 * n_tok + 4 * (n_tok // 16)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    host = torch.empty(2, n_tok, hkv, d, dtype=torch.bfloat16, pin_memory=True)
+    stage = torch.empty(2, n_tok, hkv, d, dtype=torch.bfloat16, device=dev)
+    stage.copy_(host, non_blocking=True)
+    torch.cuda.synchronize()
+    h0, h1 = events(1)[0], events(1)[0]
+    h0.record()
+    for _ in range(5):
+        stage.copy_(host, non_blocking=True)
+    h1.record()
+    torch.cuda.synchronize()
+    h2d = 5 * 2 * kv_bytes / (h0.elapsed_time(h1) * 1e-3) / 1e9
+    return {"workload": "recall-inject: 65,536 tokens K+V bf16 into 4,096 random pages with fused RoPE remap "
+                        "(theta 5e5)", "ms": round(ms, 4), "gbs": round(gbs, 1),
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": nbytes},
+            "h2d_pinned_gbs": round(h2d, 1)}
+
+
 def pmc_run(dev) -> None:
     """A short fixed sequence of launches for hardware-counter passes
     (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE): a 1 GiB device copy of
@@ -390,6 +487,16 @@ def pmc_run(dev) -> None:
 
 
 # ---------------------------------------------------------------------------
+SECONDARY = {
+    "remap": bench_remap,
+    "gather": bench_gather_evict,
+    "fp32": bench_decode_fp32,
+    "prefill": bench_prefill,
+    "fog_bias": bench_fog_bias,
+    "recall": bench_recall_inject,
+}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -399,11 +506,18 @@ def main():
     ap.add_argument("--no-secondary", action="store_true", help="skip remap / gather / fp32 lines")
     ap.add_argument("--pmc-run", action="store_true",
                     help="only run the launch sequence used for rocprofv3 --pmc traffic passes")
+    ap.add_argument("--only", choices=sorted(SECONDARY),
+                    help="run one secondary workload and print its JSON (for profiling it alone)")
     args = ap.parse_args()
     if args.pmc_run:
         import torch
 
         pmc_run(torch.device("cuda:0"))
+        return
+    if args.only:
+        import torch
+
+        print(json.dumps(SECONDARY[args.only](torch.device("cuda:0"))), flush=True)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (the hot path is built and measured on a single MI355X); "
@@ -478,6 +592,11 @@ def main():
         torch.cuda.empty_cache()
         log("secondary: chunked prefill 2048 x 1M")
         sec["prefill_1m"] = bench_prefill(dev)
+        torch.cuda.empty_cache()
+        log("secondary: fog bias producer")
+        sec["fog_bias_131k"] = bench_fog_bias(dev)
+        log("secondary: recall inject")
+        sec["recall_inject_65k"] = bench_recall_inject(dev)
         result["secondary"] = sec
     print(json.dumps(result), flush=True)
 
