@@ -339,6 +339,31 @@ int kessie_kv_cache_write(void* kv_pool, int64_t page_stride,
                           int num_kv_heads, int head_dim, int page_size,
                           int num_pages, int dtype, void* stream);
 
+/* =========================================================================
+ * Semantic index query
+ * ========================================================================= */
+
+/* Workspace bytes for kessie_index_query (0 when top_k == 0). */
+size_t kessie_index_query_workspace_bytes(int num_chunks, int top_k);
+
+/* Cosine similarity of query_embed (fp32 [embed_dim]) against every row of
+ * index_embeds ([num_chunks][row_stride] elements of `dtype`, 16-byte aligned
+ * rows, embed_dim <= 1024): sim_i = dot(q, e_i) * inv(|q|) * inv(|e_i|) with
+ * fp32 accumulation, into similarities[num_chunks].  norm_mode picks the
+ * normalisation of the search being replaced: 0 = 1/sqrt(n^2+1e-8)
+ * (_kessie_index_query_kernel, kessie_hip_kernels.py:344-360), 1 =
+ * 1/(n+1e-8) (the numpy searches, kessie_exp3.py:1866-1869), 2 = 1/n with
+ * norms below 1e-8 taken as 1 (VectorIndex, kessie_exp3.py:74-76,89-105).
+ * Then, when top_k > 0 (<= 1024), the top_k rows ordered by similarity
+ * descending, ties by ascending row index, into top_ids / top_scores (either
+ * may be NULL); entries past num_chunks are -1 / -inf. */
+int kessie_index_query(const void* index_embeds, int64_t row_stride,
+                       int num_chunks, int embed_dim, int dtype,
+                       int norm_mode, const float* query_embed,
+                       float* similarities,
+                       int top_k, int32_t* top_ids, float* top_scores,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
 #if defined(__GNUC__) || defined(__clang__)
 #pragma GCC visibility pop
 #endif

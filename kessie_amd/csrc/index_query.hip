@@ -1,0 +1,356 @@
+// Semantic index query for gfx950: cosine similarity of one query embedding
+// against every chunk embedding of the conversation index, then the exact
+// top-k.  Replaces _kessie_index_query_kernel (kessie_hip_kernels.py:344-360)
+// and the numpy / FAISS flat searches of VectorIndex.search
+// (kessie_exp3.py:89-105).
+//
+// Similarity: sim_i = dot(q, e_i) * inv(|q|) * inv(|e_i|), fp32 accumulation
+// (rows may be fp32, bf16 or fp16), with the normalisation of the call site
+// being replaced (norm_mode):
+//   0  inv(n) = 1 / sqrt(n^2 + 1e-8)       _kessie_index_query_kernel
+//   1  inv(n) = 1 / (n + 1e-8)             the numpy searches, kessie_exp3.py:1866-1869
+//   2  inv(n) = n < 1e-8 ? 1 : 1 / n       VectorIndex.rebuild / search, kessie_exp3.py:74-76,90-93  The scan is HBM-bound: 16 lanes own one row
+// (16 bytes per lane per load, 256 contiguous bytes per 16 lanes), four rows
+// per wave per step, the 16-lane dot / norm reductions on DPP row shuffles.
+//
+// Top-k order: score descending, ties by ascending chunk index -- a total
+// order, encoded as the 64-bit key (~ordered(score) << 32 | index) sorted
+// ascending.  Exact: each pass reduces groups of keys to their first k, sorted
+// -- k <= 64: a wave per 512 keys, in registers (lane shuffles); larger k: a
+// block per 2,048 keys, bitonic in LDS -- and passes repeat until one group
+// remains, whose first k keys are the answer.
+#include "common.h"
+
+namespace kessie {
+namespace index {
+namespace {
+
+constexpr int kScanThreads = 256;
+constexpr int kSortN = 2048;  // keys per block in a top-k pass
+constexpr int kSortThreads = 256;
+constexpr int kMaxTopK = 1024;
+
+template <typename T>
+struct Row16;  // 16-byte vector of T and its element count
+template <>
+struct Row16<float> {
+  typedef f32x4 type;
+  static constexpr int N = 4;
+};
+template <>
+struct Row16<bf16_t> {
+  typedef bf16x8 type;
+  static constexpr int N = 8;
+};
+template <>
+struct Row16<f16_t> {
+  typedef f16x8 type;
+  static constexpr int N = 8;
+};
+
+__device__ __forceinline__ float inv_norm(float sumsq, int mode) {
+  if (mode == 0) return 1.0f / sqrtf(sumsq + 1e-8f);
+  const float n = sqrtf(sumsq);
+  if (mode == 1) return 1.0f / (n + 1e-8f);
+  return n < 1e-8f ? 1.0f : 1.0f / n;
+}
+
+__device__ __forceinline__ float sum16(float v) {
+  // Reduce over the 16 lanes of a DPP row (xor 8, 4, 2, 1 within the row).
+  v += __shfl_xor(v, 8, 16);
+  v += __shfl_xor(v, 4, 16);
+  v += __shfl_xor(v, 2, 16);
+  v += __shfl_xor(v, 1, 16);
+  return v;
+}
+
+// q_scale = inv(|q|), computed once per block from the query.
+template <typename T>
+__global__ __launch_bounds__(kScanThreads) void cosine_scan_kernel(const T* __restrict__ rows, int64_t row_stride,
+                                                                   int n, int d, const float* __restrict__ q,
+                                                                   float* __restrict__ sims, int mode) {
+  typedef typename Row16<T>::type V;
+  constexpr int N = Row16<T>::N;
+  __shared__ float qs[1024];
+  __shared__ float red[kScanThreads / 64];
+  float part = 0.0f;
+  for (int i = threadIdx.x; i < d; i += kScanThreads) {
+    const float x = q[i];
+    qs[i] = x;
+    part += x * x;
+  }
+  for (int off = 32; off > 0; off >>= 1) part += __shfl_xor(part, off);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = part;
+  __syncthreads();
+  float qq = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kScanThreads / 64; ++w) qq += red[w];
+  const float q_scale = inv_norm(qq, mode);
+
+  const int sub = threadIdx.x & 15;              // lane within the row group
+  const int group = (blockIdx.x * kScanThreads + threadIdx.x) >> 4;
+  const int groups = (gridDim.x * kScanThreads) >> 4;
+  const int chunks = d / N;                      // 16-byte chunks per row
+  for (int r = group; r < n; r += groups) {
+    const T* row = rows + (int64_t)r * row_stride;
+    float dot = 0.0f, ee = 0.0f;
+    for (int c = sub; c < chunks; c += 16) {
+      const V v = __builtin_nontemporal_load(reinterpret_cast<const V*>(row) + c);
+#pragma unroll
+      for (int e = 0; e < N; ++e) {
+        const float x = to_f32(v[e]);
+        dot += x * qs[c * N + e];
+        ee += x * x;
+      }
+    }
+    dot = sum16(dot);
+    ee = sum16(ee);
+    if (sub == 0) sims[r] = dot * q_scale * inv_norm(ee, mode);
+  }
+}
+
+// Monotone map of a float to uint32 (ascending), -0 folded into +0.
+__device__ __forceinline__ uint32_t ordered(float s) {
+  uint32_t b = __float_as_uint(s == 0.0f ? 0.0f : s);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+__device__ __forceinline__ float unordered(uint32_t o) {
+  const uint32_t b = (o & 0x80000000u) ? (o & 0x7fffffffu) : ~o;
+  return __uint_as_float(b);
+}
+
+// Keys of the first pass: (~ordered(score) << 32) | index; ascending = best first.
+__device__ __forceinline__ uint64_t make_key(float s, uint32_t i) {
+  return ((uint64_t)(~ordered(s)) << 32) | i;
+}
+
+// One pass: block b sorts keys [b*kSortN, ...) (scores from `sims` when
+// keys_in is null) and writes its first `keep` keys to keys_out[b*keep ...].
+__global__ __launch_bounds__(kSortThreads) void topk_pass_kernel(const float* __restrict__ sims,
+                                                                 const uint64_t* __restrict__ keys_in, int n,
+                                                                 int keep, uint64_t* __restrict__ keys_out) {
+  __shared__ uint64_t sk[kSortN];
+  const int base = blockIdx.x * kSortN;
+  for (int i = threadIdx.x; i < kSortN; i += kSortThreads) {
+    const int g = base + i;
+    uint64_t key = ~0ull;  // padding sorts last
+    if (g < n) key = keys_in ? keys_in[g] : make_key(sims[g], (uint32_t)g);
+    sk[i] = key;
+  }
+  __syncthreads();
+  for (int size = 2; size <= kSortN; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int t = threadIdx.x; t < kSortN / 2; t += kSortThreads) {
+        const int lo = 2 * t - (t & (stride - 1));
+        const int hi = lo + stride;
+        const bool up = (lo & size) == 0;
+        const uint64_t a = sk[lo], b = sk[hi];
+        if ((a > b) == up) {
+          sk[lo] = b;
+          sk[hi] = a;
+        }
+      }
+      __syncthreads();
+    }
+  }
+  for (int i = threadIdx.x; i < keep; i += kSortThreads) keys_out[(int64_t)blockIdx.x * keep + i] = sk[i];
+}
+
+// Small-k path (k <= 64): one key per lane, a wave holds its running best 64
+// keys sorted across its lanes and folds in one 64-key segment at a time:
+// sort the segment (bitonic, lane shuffles), take the lane-wise min against
+// the running list reversed (that keeps the 64 smallest of the union, as a
+// bitonic sequence), and re-sort it with the six merge stages.  No LDS, no
+// barriers.  Each wave consumes kWaveKeys keys and writes its first `keep`
+// (short chains: the shuffles are latency-bound, so more waves with fewer
+// segments each).  The last pass (one wave) writes ids / scores directly.
+constexpr int kWaveSegs = 2;
+constexpr int kWaveKeys = 64 * kWaveSegs;
+constexpr int kWaveThreads = 256;
+
+__device__ __forceinline__ uint64_t shfl_xor64(uint64_t x, int m) {
+  const uint32_t lo = __shfl_xor((uint32_t)x, m), hi = __shfl_xor((uint32_t)(x >> 32), m);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ uint64_t shfl64(uint64_t x, int src) {
+  const uint32_t lo = __shfl((uint32_t)x, src), hi = __shfl((uint32_t)(x >> 32), src);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ uint64_t wave_sort64(uint64_t x, int lane) {
+#pragma unroll
+  for (int size = 2; size <= 64; size <<= 1)
+#pragma unroll
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      const uint64_t y = shfl_xor64(x, stride);
+      const bool up = (lane & size) == 0 || size == 64;
+      const bool lower = (lane & stride) == 0;
+      x = (lower == up) ? (x < y ? x : y) : (x < y ? y : x);
+    }
+  return x;
+}
+
+__global__ __launch_bounds__(kWaveThreads) void topk_wave_kernel(const float* __restrict__ sims,
+                                                                 const uint64_t* __restrict__ keys_in, int n,
+                                                                 int keep, uint64_t* __restrict__ keys_out,
+                                                                 int32_t* __restrict__ ids, float* __restrict__ scores,
+                                                                 int top_k) {
+  const int lane = threadIdx.x & 63;
+  const int wave = (blockIdx.x * kWaveThreads + threadIdx.x) >> 6;
+  const int64_t base = (int64_t)wave * kWaveKeys;
+  if (base >= n) return;  // whole wave leaves together
+  uint64_t best = ~0ull;
+  for (int seg = 0; seg < kWaveSegs; ++seg) {
+    const int64_t g = base + seg * 64 + lane;
+    uint64_t x = ~0ull;
+    if (g < n) x = keys_in ? keys_in[g] : make_key(sims[g], (uint32_t)g);
+    x = wave_sort64(x, lane);
+    const uint64_t rev = shfl64(x, 63 - lane);
+    uint64_t m = best < rev ? best : rev;  // the 64 smallest of the union, bitonic
+#pragma unroll
+    for (int stride = 32; stride > 0; stride >>= 1) {
+      const uint64_t y = shfl_xor64(m, stride);
+      m = ((lane & stride) == 0) ? (m < y ? m : y) : (m < y ? y : m);
+    }
+    best = m;
+  }
+  if (top_k == 0) {
+    if (lane < keep) keys_out[(int64_t)wave * keep + lane] = best;
+    return;
+  }
+  for (int i = lane; i < top_k; i += 64) {  // final pass: i < keep only when i == lane
+    const bool ok = i < keep;
+    if (ids) ids[i] = ok ? (int32_t)(best & 0xffffffffu) : -1;
+    if (scores) scores[i] = ok ? unordered(~(uint32_t)(best >> 32)) : -__builtin_huge_valf();
+  }
+}
+
+__global__ void topk_unpack_kernel(const uint64_t* __restrict__ keys, int k, int n, int32_t* __restrict__ ids,
+                                   float* __restrict__ scores) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= k) return;
+  const bool ok = i < n;
+  const uint64_t key = ok ? keys[i] : 0;
+  if (ids) ids[i] = ok ? (int32_t)(key & 0xffffffffu) : -1;
+  if (scores) scores[i] = ok ? unordered(~(uint32_t)(key >> 32)) : -__builtin_huge_valf();
+}
+
+// Keys written by pass p, and the number of passes, for n inputs and top k.
+struct Plan {
+  int passes;
+  int64_t max_keys;  // largest intermediate key array
+};
+
+// Keys consumed per group (a wave on the small-k path, a block otherwise).
+inline int group_keys(int k) { return k <= 64 ? kWaveKeys : kSortN; }
+
+Plan plan_for(int n, int k) {
+  Plan p{0, 0};
+  int64_t cur = n;
+  const int per = group_keys(k);
+  do {
+    const int64_t blocks = div_up(cur, (int64_t)per);
+    cur = blocks * (int64_t)k;
+    if (cur > p.max_keys) p.max_keys = cur;
+    ++p.passes;
+    if (blocks == 1) break;
+  } while (true);
+  return p;
+}
+
+template <typename T>
+int scan_launch(const void* rows, int64_t stride, int n, int d, const float* q, float* sims, int mode,
+                hipStream_t s) {
+  // One 16-lane group per row, at most 4,096 workgroups (groups then loop).
+  const int blocks = (int)std::min<int64_t>(div_up((int64_t)n * 16, (int64_t)kScanThreads), 4096);
+  hipLaunchKernelGGL(cosine_scan_kernel<T>, dim3(blocks), dim3(kScanThreads), 0, s, static_cast<const T*>(rows),
+                     stride, n, d, q, sims, mode);
+  return check_launch("index query scan");
+}
+
+}  // namespace
+}  // namespace index
+}  // namespace kessie
+
+using namespace kessie;
+using namespace kessie::index;
+
+extern "C" size_t kessie_index_query_workspace_bytes(int num_chunks, int top_k) {
+  if (num_chunks <= 0 || top_k <= 0) return 0;
+  const int k = top_k < num_chunks ? top_k : num_chunks;
+  const Plan p = plan_for(num_chunks, k);
+  // Two ping-pong key arrays.
+  return 2 * (size_t)((p.max_keys * sizeof(uint64_t) + 255) / 256 * 256);
+}
+
+extern "C" int kessie_index_query(const void* index_embeds, int64_t row_stride, int num_chunks, int embed_dim,
+                                  int dtype, int norm_mode, const float* query_embed, float* similarities, int top_k,
+                                  int32_t* top_ids, float* top_scores, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+  clear_error();
+  KESSIE_REQUIRE(num_chunks >= 0 && embed_dim > 0 && embed_dim <= 1024 && top_k >= 0, KESSIE_ERR_INVALID,
+                 "index query: num_chunks %d, embed_dim %d (1..1024), top_k %d", num_chunks, embed_dim, top_k);
+  KESSIE_REQUIRE(top_k <= kMaxTopK, KESSIE_ERR_UNSUPPORTED, "index query: top_k %d above %d", top_k, kMaxTopK);
+  if (num_chunks == 0 && top_k == 0) return KESSIE_OK;
+  KESSIE_REQUIRE(num_chunks == 0 || (query_embed && similarities), KESSIE_ERR_INVALID,
+                 "index query: null query or similarities");
+  KESSIE_REQUIRE(num_chunks == 0 || index_embeds, KESSIE_ERR_INVALID, "index query: null index");
+  KESSIE_REQUIRE(top_k == 0 || top_ids || top_scores, KESSIE_ERR_INVALID, "index query: no top-k output");
+  const int esz = dtype_size(dtype);
+  KESSIE_REQUIRE(esz > 0, KESSIE_ERR_UNSUPPORTED, "index query: dtype %d", dtype);
+  KESSIE_REQUIRE((embed_dim * esz) % 16 == 0 && (row_stride * esz) % 16 == 0 && aligned16(index_embeds),
+                 KESSIE_ERR_UNSUPPORTED, "index query: rows must be 16-byte aligned multiples of 16 bytes");
+  KESSIE_REQUIRE(row_stride >= embed_dim, KESSIE_ERR_INVALID, "index query: row_stride %lld < embed_dim %d",
+                 (long long)row_stride, embed_dim);
+  KESSIE_REQUIRE(norm_mode >= 0 && norm_mode <= 2, KESSIE_ERR_INVALID, "index query: norm_mode %d", norm_mode);
+  const hipStream_t s = as_stream(stream);
+  if (num_chunks > 0) {
+    int st = KESSIE_OK;
+    switch (dtype) {
+      case KESSIE_DTYPE_F32: st = scan_launch<float>(index_embeds, row_stride, num_chunks, embed_dim, query_embed, similarities, norm_mode, s); break;
+      case KESSIE_DTYPE_BF16: st = scan_launch<bf16_t>(index_embeds, row_stride, num_chunks, embed_dim, query_embed, similarities, norm_mode, s); break;
+      case KESSIE_DTYPE_F16: st = scan_launch<f16_t>(index_embeds, row_stride, num_chunks, embed_dim, query_embed, similarities, norm_mode, s); break;
+      default: st = KESSIE_ERR_UNSUPPORTED; set_error(st, "index query: dtype %d", dtype);
+    }
+    if (st != KESSIE_OK) return st;
+  }
+  if (top_k == 0) return KESSIE_OK;
+  const int k = top_k < num_chunks ? top_k : num_chunks;
+  if (k == 0) {  // nothing to rank: -1 / -inf
+    hipLaunchKernelGGL(topk_unpack_kernel, dim3(div_up(top_k, 256)), dim3(256), 0, s, nullptr, top_k, 0, top_ids,
+                       top_scores);
+    return check_launch("index query top-k");
+  }
+  const size_t need = kessie_index_query_workspace_bytes(num_chunks, k);
+  KESSIE_REQUIRE(workspace && workspace_bytes >= need, KESSIE_ERR_WORKSPACE,
+                 "index query: workspace of %zu bytes needed, got %zu", need, workspace_bytes);
+  KESSIE_REQUIRE(aligned16(workspace), KESSIE_ERR_INVALID, "index query: workspace not 16-byte aligned");
+  const Plan plan = plan_for(num_chunks, k);
+  const size_t half = need / 2;
+  uint64_t* buf[2] = {static_cast<uint64_t*>(workspace),
+                      reinterpret_cast<uint64_t*>(static_cast<char*>(workspace) + half)};
+  int64_t cur = num_chunks;
+  const uint64_t* in = nullptr;
+  const int per = group_keys(k);
+  for (int pass = 0; pass < plan.passes; ++pass) {
+    const int groups = (int)div_up(cur, (int64_t)per);
+    uint64_t* out = buf[pass & 1];
+    if (k <= 64) {
+      const int blocks = div_up(groups, kWaveThreads / 64);
+      const bool last = pass + 1 == plan.passes;
+      hipLaunchKernelGGL(topk_wave_kernel, dim3(blocks), dim3(kWaveThreads), 0, s, similarities, in, (int)cur, k,
+                         out, last ? top_ids : nullptr, last ? top_scores : nullptr, last ? top_k : 0);
+      if (last) return check_launch("index query top-k");
+    } else {
+      hipLaunchKernelGGL(topk_pass_kernel, dim3(groups), dim3(kSortThreads), 0, s, similarities, in, (int)cur, k,
+                         out);
+    }
+    in = out;
+    cur = (int64_t)groups * k;
+  }
+  hipLaunchKernelGGL(topk_unpack_kernel, dim3(div_up(top_k, 256)), dim3(256), 0, s, in, top_k, k, top_ids,
+                     top_scores);
+  return check_launch("index query top-k");
+}

@@ -531,3 +531,36 @@ def kv_cache_write(pool: torch.Tensor, key: torch.Tensor, value: torch.Tensor, s
         _ptr(key), key.stride(0), key.stride(1), _ptr(value), value.stride(0), value.stride(1),
         _ptr(_contig(slot_mapping, "slot_mapping")), t, h, d, pv.page_size, pv.num_pages,
         dtype_code(pool.dtype), _stream_ptr(stream, pool.device)))
+
+
+# ---------------------------------------------------------------------------
+# Semantic index query
+# ---------------------------------------------------------------------------
+def index_query(embeds: torch.Tensor, query: torch.Tensor, top_k: int = 0, norm_mode: int = 0,
+                sims: Optional[torch.Tensor] = None, stream=None):
+    """Cosine similarity of ``query`` (fp32 [D]) against every row of
+    ``embeds`` ([N, D], fp32/bf16/fp16, rows contiguous) and the top_k rows
+    (similarity descending, ties by ascending row).  Returns (sims [N] fp32,
+    ids [top_k] int32 or None, scores [top_k] fp32 or None); ids past N are -1."""
+    if embeds.dim() != 2 or embeds.stride(1) != 1:
+        raise ValueError("embeds must be [N, D] with contiguous rows")
+    n, d = embeds.shape
+    dev = embeds.device
+    query = query.reshape(-1)
+    if query.dtype != torch.float32 or query.numel() != d or query.device != dev:
+        raise ValueError("query must be fp32 [D] on the embeddings' device")
+    query = _contig(query, "query")
+    if sims is None:
+        sims = torch.empty(n, dtype=torch.float32, device=dev)
+    ids = scores = None
+    lib = _lib.load()
+    need = lib.kessie_index_query_workspace_bytes(n, int(top_k)) if top_k > 0 else 0
+    ws = workspace(need, dev, "index") if need else None
+    if top_k > 0:
+        ids = torch.empty(top_k, dtype=torch.int32, device=dev)
+        scores = torch.empty(top_k, dtype=torch.float32, device=dev)
+    _lib.check("kessie_index_query", lib.kessie_index_query(
+        _ptr(embeds) if n else None, embeds.stride(0), n, d, dtype_code(embeds.dtype), int(norm_mode),
+        _ptr(query), _ptr(sims), int(top_k), _ptr(ids), _ptr(scores), _ptr(ws),
+        0 if ws is None else ws.numel(), _stream_ptr(stream, dev)))
+    return sims, ids, scores
