@@ -513,6 +513,76 @@ def bench_index_query(dev, reps=50, n=78125, d=256, k=5):
                              "kind": "port", "sample": "numpy matrix-vector product + argsort, 20 reps"}}
 
 
+def bench_hf_cache(dev, layers=32, heads=8, d=128, window=4096, prefill=8000, steps=50):
+    """HF tiered cache (KeSSieCache) decode steps: 32 layers x (append one
+    token, return K and the fog-weighted V over the ~8K-token window), bf16, 8
+    kv heads, head_dim 128, window_size 4096 (no eviction in the timed steps);
+    plus the fused fog kernel alone over an 8,192-token window (its HBM
+    roofline).  CPU baseline: the reference's torch.cat / fog op sequence on
+    the host cores for 2 steps."""
+    import torch
+
+    from kessie_amd import ops
+    from kessie_amd.hf_cache import KeSSieCache
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    cache = KeSSieCache(window_size=window)
+    kv0 = torch.randn(1, heads, prefill, d, generator=g, device=dev).bfloat16()
+    for li in range(layers):
+        cache.update(kv0, kv0, li)
+    tok = torch.randn(1, heads, 1, d, generator=g, device=dev).bfloat16()
+    for li in range(layers):
+        cache.update(tok, tok, li)
+    torch.cuda.synchronize()
+    e0, e1 = events(1)[0], events(1)[0]
+    e0.record()
+    for _ in range(steps):
+        for li in range(layers):
+            cache.update(tok, tok, li)
+    e1.record()
+    torch.cuda.synchronize()
+    step_ms = e0.elapsed_time(e1) / steps
+    n = 8192
+    v = torch.randn(1, heads, n, d, generator=g, device=dev).bfloat16()
+    out = torch.empty_like(v)
+    ops.hf_fog_apply(v, 0.5, 0.5, out=out)
+    reps = 50
+    a, b = events(reps), events(reps)
+    backlog()
+    for i in range(reps):
+        a[i].record()
+        ops.hf_fog_apply(v, 0.5, 0.5, out=out)
+        b[i].record()
+    torch.cuda.synchronize()
+    fog_us = 1000.0 * sum(x.elapsed_time(y) for x, y in zip(a, b)) / reps
+    fog_bytes = 2 * v.numel() * 2
+    fog_gbs = fog_bytes / (fog_us * 1e-6) / 1e9
+    from oracle.hf_cache import HFCacheModel
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    model = HFCacheModel(window_size=window)
+    kc = kv0.cpu()
+    for li in range(layers):
+        model.update(kc, kc, li)
+    tc = tok.cpu()
+    t0 = time.perf_counter()
+    for _ in range(2):
+        for li in range(layers):
+            model.update(tc, tc, li)
+    cpu_ms = 1000.0 * (time.perf_counter() - t0) / 2
+    return {"workload": "HF tiered cache decode step: 32 layers, bf16, 8 kv heads, D=128, ~8K-token window "
+                        "(window_size 4096), K + fog-weighted V returned per layer",
+            "step_ms": round(step_ms, 4), "per_layer_us": round(1000.0 * step_ms / layers, 2),
+            "fog_apply_8k_us": round(fog_us, 2),
+            "roofline": {"bound": "hbm", "kernel": "hf_fog_apply_kernel", "achieved": round(fog_gbs, 1),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(fog_gbs / HBM_PEAK_GBS, 4),
+                         "algorithmic_bytes": fog_bytes},
+            "cpu_baseline": {"value": round(cpu_ms, 2), "unit": "ms per step", "cores": cores, "kind": "port",
+                             "sample": "2 decode steps of the reference's torch.cat / fog op sequence"}}
+
+
 def pmc_run(dev) -> None:
     """A short fixed sequence of launches for hardware-counter passes
     (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE): a 1 GiB device copy of
@@ -547,6 +617,7 @@ SECONDARY = {
     "fog_bias": bench_fog_bias,
     "recall": bench_recall_inject,
     "index": bench_index_query,
+    "hf_cache": bench_hf_cache,
 }
 
 
@@ -652,6 +723,8 @@ def main():
         sec["recall_inject_65k"] = bench_recall_inject(dev)
         log("secondary: index query")
         sec["index_query_78k"] = bench_index_query(dev)
+        log("secondary: HF tiered cache")
+        sec["hf_cache_step"] = bench_hf_cache(dev)
         result["secondary"] = sec
     print(json.dumps(result), flush=True)
 

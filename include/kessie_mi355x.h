@@ -339,6 +339,25 @@ int kessie_kv_cache_write(void* kv_pool, int64_t page_stride,
                           int num_kv_heads, int head_dim, int page_size,
                           int num_pages, int dtype, void* stream);
 
+/* Fog weights of the HF tiered cache (KeSSieCache._compute_fog_mask,
+ * kessie_exp3.py:415-425) into weights[0:seq_len] (fp32): with
+ * cc = max(1, int(seq_len * fog_start)) and fc = seq_len - cc,
+ * w[p] = max((p * fp32(1/max(fc-1,1)))^fog_alpha, 0.01) for p < fc and 1
+ * otherwise (all ones when fc <= 0 or fog_alpha <= 0). */
+int kessie_hf_fog_weights_fill(float* weights, int seq_len, double fog_alpha,
+                               double fog_start, void* stream);
+
+/* out[b][h][t][:] = dtype(fp32(v[b][h][t][:]) * w[t]) with the weights
+ * above over seq_len positions (KeSSieCache.update's fog step,
+ * kessie_exp3.py:443-445), in one pass; strides in elements, head_dim
+ * contiguous, 16-byte aligned rows. */
+int kessie_hf_fog_apply(const void* v, int64_t v_batch_stride,
+                        int64_t v_head_stride, int64_t v_tok_stride, void* out,
+                        int64_t out_batch_stride, int64_t out_head_stride,
+                        int64_t out_tok_stride, int batch, int num_heads,
+                        int seq_len, int head_dim, double fog_alpha,
+                        double fog_start, int dtype, void* stream);
+
 /* =========================================================================
  * Semantic index query
  * ========================================================================= */

@@ -95,6 +95,81 @@ int fog_bias_launch(void* buf, int kv_len, int boundary, float inv_b, float neg_
   return check_launch("fog bias");
 }
 
+// ---- fog of the HF tiered cache (KeSSieCache, kessie_exp3.py:415-445) ------
+// cc = max(1, int(N * fog_start)) clear tokens at the end, fc = N - cc fogged
+// ones: w[p] = max(fp32(p) * fp32(1/max(fc-1,1)) ^ alpha, 0.01) for p < fc, 1
+// otherwise (torch's device arange / division by a Python scalar / pow /
+// clamp, in fp32), and V' = dtype(fp32(V) * w).
+
+__device__ __forceinline__ float hf_fog_weight(int p, int fc, float inv_den, float alpha, int form) {
+#pragma clang fp contract(off)
+  if (p >= fc) return 1.0f;
+  const float t = (float)p * inv_den;
+  float w;
+  switch (form) {
+    case kPowOne: w = t; break;
+    case kPowHalf: w = sqrtf(t); break;
+    case kPowTwo: w = t * t; break;
+    case kPowThree: w = t * t * t; break;
+    default: w = powf(t, alpha); break;
+  }
+  return fmaxf(w, 0.01f);
+}
+
+__global__ __launch_bounds__(kThreads) void hf_fog_weights_kernel(float* w, int n, int fc, float inv_den, float alpha,
+                                                                  int form) {
+  const int i = blockIdx.x * kThreads + threadIdx.x;
+  if (i < n) w[i] = hf_fog_weight(i, fc, inv_den, alpha, form);
+}
+
+// V' rows (b, h, t) = V rows * w[t]; one thread per 16-byte chunk.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void hf_fog_apply_kernel(const T* __restrict__ v, T* __restrict__ out, int BH,
+                                                                int H, int n, int D, int64_t v_bs, int64_t v_hs,
+                                                                int64_t v_ts, int64_t o_bs, int64_t o_hs, int64_t o_ts,
+                                                                int fc, float inv_den, float alpha, int form) {
+#pragma clang fp contract(off)
+  constexpr int N = 16 / (int)sizeof(T);
+  const int chunks = D / N;
+  const int64_t total = (int64_t)BH * n * chunks;
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= total) return;
+  const int c = (int)(i % chunks);
+  const int64_t r = i / chunks;
+  const int t = (int)(r % n);
+  const int bh = (int)(r / n);
+  const int b = bh / H, h = bh - b * H;
+  const float w = hf_fog_weight(t, fc, inv_den, alpha, form);
+  typedef T V8 __attribute__((ext_vector_type(16 / sizeof(T))));
+  const V8 x = *reinterpret_cast<const V8*>(v + b * v_bs + h * v_hs + t * v_ts + c * N);
+  V8 y;
+#pragma unroll
+  for (int e = 0; e < N; ++e) y[e] = round_to<T>(to_f32(x[e]) * w);
+  *reinterpret_cast<V8*>(out + b * o_bs + h * o_hs + t * o_ts + c * N) = y;
+}
+
+struct HfFog {
+  int fc;
+  float inv_den;
+  float alpha;
+  int form;
+};
+
+HfFog hf_fog_params(int n, double fog_alpha, double fog_start) {
+  // cc = max(1, int(N * fog_start)) (C's cast truncates toward zero like int());
+  // fc <= 0 or fog_alpha <= 0 leaves V unweighted, as the reference does.
+  const double prod = (double)n * fog_start;
+  const int cc = prod >= (double)n ? n : (prod < 1.0 ? 1 : (int)prod);
+  HfFog f{n - cc, 0.0f, (float)fog_alpha, kPowGeneral};
+  if (f.fc < 0 || !(fog_alpha > 0.0)) f.fc = 0;
+  f.inv_den = 1.0f / (float)(f.fc - 1 > 1 ? f.fc - 1 : 1);
+  if (fog_alpha == 1.0) f.form = kPowOne;
+  else if (fog_alpha == 0.5) f.form = kPowHalf;
+  else if (fog_alpha == 2.0) f.form = kPowTwo;
+  else if (fog_alpha == 3.0) f.form = kPowThree;
+  return f;
+}
+
 // ---- slot-mapped K/V write -------------------------------------------------
 
 struct WriteArgs {
@@ -252,4 +327,59 @@ extern "C" int kessie_kv_cache_write(void* kv_pool, int64_t page_stride, int64_t
   }
   set_error(KESSIE_ERR_UNSUPPORTED, "kv cache write: dtype %d", dtype);
   return KESSIE_ERR_UNSUPPORTED;
+}
+
+extern "C" int kessie_hf_fog_weights_fill(float* weights, int seq_len, double fog_alpha, double fog_start,
+                                          void* stream) {
+  clear_error();
+  KESSIE_REQUIRE(seq_len >= 0, KESSIE_ERR_INVALID, "hf fog weights: seq_len %d", seq_len);
+  if (seq_len == 0) return KESSIE_OK;
+  KESSIE_REQUIRE(weights != nullptr, KESSIE_ERR_INVALID, "hf fog weights: null buffer");
+  const HfFog f = hf_fog_params(seq_len, fog_alpha, fog_start);
+  hipLaunchKernelGGL(hf_fog_weights_kernel, dim3(div_up(seq_len, kThreads)), dim3(kThreads), 0, as_stream(stream),
+                     weights, seq_len, f.fc, f.inv_den, f.alpha, f.form);
+  return check_launch("hf fog weights");
+}
+
+extern "C" int kessie_hf_fog_apply(const void* v, int64_t v_bs, int64_t v_hs, int64_t v_ts, void* out, int64_t o_bs,
+                                   int64_t o_hs, int64_t o_ts, int batch, int num_heads, int seq_len, int head_dim,
+                                   double fog_alpha, double fog_start, int dtype, void* stream) {
+  clear_error();
+  KESSIE_REQUIRE(batch >= 0 && num_heads > 0 && seq_len >= 0 && head_dim > 0, KESSIE_ERR_INVALID,
+                 "hf fog apply: B=%d H=%d N=%d D=%d", batch, num_heads, seq_len, head_dim);
+  if (batch == 0 || seq_len == 0) return KESSIE_OK;
+  KESSIE_REQUIRE(v && out, KESSIE_ERR_INVALID, "hf fog apply: null pointer");
+  const int esz = dtype_size(dtype);
+  KESSIE_REQUIRE(esz > 0, KESSIE_ERR_UNSUPPORTED, "hf fog apply: dtype %d", dtype);
+  const int N = 16 / esz;
+  KESSIE_REQUIRE(head_dim % N == 0 && aligned16(v) && aligned16(out) && v_bs % N == 0 && v_hs % N == 0 &&
+                     v_ts % N == 0 && o_bs % N == 0 && o_hs % N == 0 && o_ts % N == 0,
+                 KESSIE_ERR_UNSUPPORTED, "hf fog apply: rows must be 16-byte aligned multiples of 16 bytes");
+  const HfFog f = hf_fog_params(seq_len, fog_alpha, fog_start);
+  const int64_t items = (int64_t)batch * num_heads * seq_len * (head_dim / N);
+  const int64_t grid = (items + kThreads - 1) / kThreads;
+  KESSIE_REQUIRE(grid <= 0x7fffffff, KESSIE_ERR_UNSUPPORTED, "hf fog apply: too large");
+  const hipStream_t s = as_stream(stream);
+  const int BH = batch * num_heads;
+  switch (dtype) {
+    case KESSIE_DTYPE_BF16:
+      hipLaunchKernelGGL(hf_fog_apply_kernel<bf16_t>, dim3((unsigned)grid), dim3(kThreads), 0, s,
+                         static_cast<const bf16_t*>(v), static_cast<bf16_t*>(out), BH, num_heads, seq_len, head_dim,
+                         v_bs, v_hs, v_ts, o_bs, o_hs, o_ts, f.fc, f.inv_den, f.alpha, f.form);
+      break;
+    case KESSIE_DTYPE_F16:
+      hipLaunchKernelGGL(hf_fog_apply_kernel<f16_t>, dim3((unsigned)grid), dim3(kThreads), 0, s,
+                         static_cast<const f16_t*>(v), static_cast<f16_t*>(out), BH, num_heads, seq_len, head_dim,
+                         v_bs, v_hs, v_ts, o_bs, o_hs, o_ts, f.fc, f.inv_den, f.alpha, f.form);
+      break;
+    case KESSIE_DTYPE_F32:
+      hipLaunchKernelGGL(hf_fog_apply_kernel<float>, dim3((unsigned)grid), dim3(kThreads), 0, s,
+                         static_cast<const float*>(v), static_cast<float*>(out), BH, num_heads, seq_len, head_dim,
+                         v_bs, v_hs, v_ts, o_bs, o_hs, o_ts, f.fc, f.inv_den, f.alpha, f.form);
+      break;
+    default:
+      set_error(KESSIE_ERR_UNSUPPORTED, "hf fog apply: dtype %d", dtype);
+      return KESSIE_ERR_UNSUPPORTED;
+  }
+  return check_launch("hf fog apply");
 }

@@ -564,3 +564,37 @@ def index_query(embeds: torch.Tensor, query: torch.Tensor, top_k: int = 0, norm_
         _ptr(query), _ptr(sims), int(top_k), _ptr(ids), _ptr(scores), _ptr(ws),
         0 if ws is None else ws.numel(), _stream_ptr(stream, dev)))
     return sims, ids, scores
+
+
+# ---------------------------------------------------------------------------
+# Fog of the HF tiered cache
+# ---------------------------------------------------------------------------
+def hf_fog_weights(seq_len: int, fog_alpha: float, fog_start: float, device=None,
+                   out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """KeSSieCache fog weights, fp32 [seq_len] (kessie_exp3.py:415-425)."""
+    if out is None:
+        out = torch.empty(seq_len, dtype=torch.float32, device=device or "cuda")
+    if out.dtype != torch.float32 or out.dim() != 1 or not out.is_contiguous() or out.numel() < seq_len:
+        raise ValueError("out must be a contiguous fp32 vector of at least seq_len elements")
+    lib = _lib.load()
+    _lib.check("kessie_hf_fog_weights_fill", lib.kessie_hf_fog_weights_fill(
+        _ptr(out), int(seq_len), float(fog_alpha), float(fog_start), _stream_ptr(stream, out.device)))
+    return out[:seq_len]
+
+
+def hf_fog_apply(v: torch.Tensor, fog_alpha: float, fog_start: float, out: Optional[torch.Tensor] = None,
+                 stream=None) -> torch.Tensor:
+    """out = dtype(fp32(v) * w[t]) for v [B, H, N, D] (head_dim contiguous) with
+    KeSSieCache's fog weights over N positions, in one pass."""
+    if v.dim() != 4 or v.stride(3) != 1:
+        raise ValueError("v must be [B, H, N, D] with a contiguous head_dim")
+    if out is None:
+        out = torch.empty_like(v)
+    if out.shape != v.shape or out.dtype != v.dtype or out.stride(3) != 1:
+        raise ValueError("out must match v")
+    b, h, n, d = v.shape
+    lib = _lib.load()
+    _lib.check("kessie_hf_fog_apply", lib.kessie_hf_fog_apply(
+        _ptr(v), v.stride(0), v.stride(1), v.stride(2), _ptr(out), out.stride(0), out.stride(1), out.stride(2),
+        b, h, n, d, float(fog_alpha), float(fog_start), dtype_code(v.dtype), _stream_ptr(stream, v.device)))
+    return out
