@@ -385,6 +385,25 @@ class KeSSieAttentionImpl:
         return getattr(inner, name)
 
     # -- the kernels --------------------------------------------------------------
+    _split_meta = None
+    _split_val = None
+
+    @classmethod
+    def _split(cls, meta):
+        """(query_start_loc on the host, decode sequences, prefill sequences),
+        computed once per metadata object: every layer of a step shares it, so
+        the one device-to-host copy happens once per step, not per layer."""
+        if cls._split_meta is meta:
+            return cls._split_val
+        qsl = meta.query_start_loc_cpu if getattr(meta, "query_start_loc_cpu", None) is not None \
+            else meta.query_start_loc.cpu()
+        qsl = [int(x) for x in qsl.tolist()]
+        nseq = len(qsl) - 1
+        decode = [i for i in range(nseq) if qsl[i + 1] - qsl[i] == 1]
+        prefill = [i for i in range(nseq) if qsl[i + 1] - qsl[i] > 1]
+        cls._split_meta, cls._split_val = meta, (qsl, decode, prefill)
+        return cls._split_val
+
     def _attend(self, args, kwargs, state):
         from . import ops
 
@@ -417,15 +436,10 @@ class KeSSieAttentionImpl:
         if state is not None and kv_len > 0:
             bias = _FOG_CACHE.get_fog_bias_f32(kv_len, query.device, query.dtype, state)
 
-        qsl = meta.query_start_loc_cpu if getattr(meta, "query_start_loc_cpu", None) is not None \
-            else meta.query_start_loc.cpu()
-        qsl = [int(x) for x in qsl.tolist()]
+        qsl, decode, prefill = self._split(meta)
         nseq = len(qsl) - 1
-        qlens = [qsl[i + 1] - qsl[i] for i in range(nseq)]
         table = meta.block_table[:nseq]
         lens = meta.seq_lens[:nseq]
-        decode = [i for i in range(nseq) if qlens[i] == 1]
-        prefill = [i for i in range(nseq) if qlens[i] > 1]
 
         if decode:
             if decode == list(range(decode[0], decode[0] + len(decode))):
