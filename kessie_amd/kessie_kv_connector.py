@@ -261,8 +261,15 @@ class KeSSieKVConnector(KVConnectorBase_v1):
     """
 
     def __init__(self, *args, **kwargs):
+        # The extra config comes as a keyword (as the reference reads it) or
+        # inside vllm_config.kv_transfer_config (as vLLM hands it over); it is
+        # not passed on to the base class, whose signature does not take it.
+        extra = kwargs.pop("kv_connector_extra_config", None)
+        if extra is None:
+            vc = args[0] if args else kwargs.get("vllm_config")
+            extra = getattr(getattr(vc, "kv_transfer_config", None), "kv_connector_extra_config", None)
+        extra = extra or {}
         super().__init__(*args, **kwargs)
-        extra = kwargs.get("kv_connector_extra_config", {}) or {}
         max_gb = float(extra.get("max_cpu_gb", 64))
         self.store = get_kessie_store(max_cpu_bytes=int(max_gb * 1073741824))
         self.rope_theta = extra.get("rope_theta")
