@@ -583,6 +583,60 @@ def bench_hf_cache(dev, layers=32, heads=8, d=128, window=4096, prefill=8000, st
                              "sample": "2 decode steps of the reference's torch.cat / fog op sequence"}}
 
 
+def bench_hbm_ceilings(dev, reps=10):
+    """Practical HBM ceilings of the hot path's access patterns on this device
+    (kessie_probe_*): a 4 GiB read-only stream (the decode kernel's pattern at
+    its best), a 2 GiB copy (gather, insert), and the remap's pattern -- read
+    and rewrite the 2 KiB K half of every 4 KiB token row of 4,096 random
+    64 KiB pages (4 rotating page sets, so the 256 MB MALL does not serve it)."""
+    import ctypes as C
+
+    import torch
+
+    from kessie_amd import _lib
+
+    lib = _lib.load()
+    s = C.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+    def timed(fn, n):
+        fn(0)
+        torch.cuda.synchronize()
+        a, b = events(n), events(n)
+        backlog()
+        for i in range(n):
+            a[i].record()
+            fn(i)
+            b[i].record()
+        torch.cuda.synchronize()
+        return sum(x.elapsed_time(y) for x, y in zip(a, b)) / n
+
+    out = {}
+    big = torch.empty(4 << 30, dtype=torch.uint8, device=dev)
+    big.fill_(1)
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    ms = timed(lambda i: _lib.check("kessie_probe_stream_read", lib.kessie_probe_stream_read(
+        C.c_void_p(big.data_ptr()), big.numel(), C.c_void_p(sink.data_ptr()), s)), reps)
+    out["stream_read_gbs"] = round(big.numel() / (ms * 1e-3) / 1e9, 1)
+    half = big.numel() // 2
+    ms = timed(lambda i: _lib.check("kessie_probe_copy", lib.kessie_probe_copy(
+        C.c_void_p(big.data_ptr() + half), C.c_void_p(big.data_ptr()), half, s)), reps)
+    out["copy_gbs"] = round(2 * half / (ms * 1e-3) / 1e9, 1)
+    del big
+    torch.cuda.empty_cache()
+    n_pages, sets = 4096, 4
+    pool = torch.zeros(n_pages * sets * 2, 16, 2, 8, 128, dtype=torch.bfloat16, device=dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(1)
+    lists = [torch.randperm(pool.shape[0], generator=g, device=dev)[:n_pages].to(torch.int32) for _ in range(sets)]
+    page_bytes = pool[0].numel() * 2
+    ms = timed(lambda i: _lib.check("kessie_probe_page_rmw", lib.kessie_probe_page_rmw(
+        C.c_void_p(pool.data_ptr()), page_bytes, 4096, 16, 2048, C.c_void_p(lists[i % sets].data_ptr()), n_pages,
+        pool.shape[0], s)), 4 * reps)
+    out["remap_pattern_rmw_gbs"] = round(2 * n_pages * 16 * 2048 / (ms * 1e-3) / 1e9, 1)
+    out["note"] = "bandwidth of the access pattern alone, no arithmetic; spec peak 8000 GB/s"
+    return out
+
+
 def pmc_run(dev) -> None:
     """A short fixed sequence of launches for hardware-counter passes
     (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE): a 1 GiB device copy of
@@ -618,6 +672,7 @@ SECONDARY = {
     "recall": bench_recall_inject,
     "index": bench_index_query,
     "hf_cache": bench_hf_cache,
+    "ceilings": bench_hbm_ceilings,
 }
 
 
@@ -725,6 +780,9 @@ def main():
         sec["index_query_78k"] = bench_index_query(dev)
         log("secondary: HF tiered cache")
         sec["hf_cache_step"] = bench_hf_cache(dev)
+        torch.cuda.empty_cache()
+        log("secondary: HBM ceilings of the access patterns")
+        sec["hbm_ceilings"] = bench_hbm_ceilings(dev)
         result["secondary"] = sec
     print(json.dumps(result), flush=True)
 

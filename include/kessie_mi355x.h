@@ -383,6 +383,20 @@ int kessie_index_query(const void* index_embeds, int64_t row_stride,
                        int top_k, int32_t* top_ids, float* top_scores,
                        void* workspace, size_t workspace_bytes, void* stream);
 
+/* =========================================================================
+ * Measurement probes: the practical HBM bandwidth of the hot path's access
+ * patterns with no arithmetic in the way (read-only stream, copy, and the
+ * remap's read-modify-write of the first row_bytes of every token row of the
+ * listed pages).  `sink` is one uint32 the read probe may write.
+ * ========================================================================= */
+int kessie_probe_stream_read(const void* buf, int64_t bytes, void* sink,
+                             void* stream);
+int kessie_probe_copy(void* dst, const void* src, int64_t bytes, void* stream);
+int kessie_probe_page_rmw(void* pool, int64_t page_bytes,
+                          int64_t row_stride_bytes, int rows_per_page,
+                          int row_bytes, const int32_t* pages, int n_pages,
+                          int num_pages, void* stream);
+
 #if defined(__GNUC__) || defined(__clang__)
 #pragma GCC visibility pop
 #endif

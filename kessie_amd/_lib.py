@@ -73,6 +73,9 @@ SIGNATURES = {
     "kessie_fog_bias_fill": (_I, [_P, _I, _I, _D, _D, _P, _I, _D, _P]),
     "kessie_fog_weights_fill": (_I, [_P, _I, _D, _D, _P]),
     # pool + 4 strides, key + 2 strides, value + 2 strides, slots, T, H, D, P, pages, dtype, stream
+    "kessie_probe_stream_read": (_I, [_P, _I64, _P, _P]),
+    "kessie_probe_copy": (_I, [_P, _P, _I64, _P]),
+    "kessie_probe_page_rmw": (_I, [_P, _I64, _I64, _I, _I, _P, _I, _I, _P]),
     "kessie_hf_fog_weights_fill": (_I, [_P, _I, _D, _D, _P]),
     # v + 3 strides, out + 3 strides, B, H, N, D, fog_alpha, fog_start, dtype, stream
     "kessie_hf_fog_apply": (_I, [_P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _I, _I, _I, _I, _D, _D, _I, _P]),

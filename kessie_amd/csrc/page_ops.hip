@@ -537,47 +537,32 @@ __global__ __launch_bounds__(kThreads) void threshold_evict_kernel(int8_t* valid
 }
 
 // ---------------------------------------------------------------------------
-// Gather: whole-page byte copies, 16 bytes per lane.
+// Gather: whole-page byte copies.  Each workgroup copies one 4 KiB tile of one
+// page slot, one non-temporal 16-byte load and store per lane: a 64 KiB page is
+// spread over 16 workgroups.  (Measured on 49,152 random 64 KiB pages: 0.99 ms
+// against 1.17-1.21 ms for one workgroup per page at 1-8 chunks per lane.)
 // ---------------------------------------------------------------------------
 constexpr int kGatherThreads = 256;
 
-template <bool kNtLoad, bool kNtStore, int kUnroll>
 __global__ __launch_bounds__(kGatherThreads) void gather_kernel(const u32x4* __restrict__ src, int64_t page_vecs,
-                                                                const int32_t* __restrict__ idx,
+                                                                int tiles_per_page, const int32_t* __restrict__ idx,
                                                                 const int32_t* __restrict__ count_dev, int n,
                                                                 int num_pages, u32x4* __restrict__ dst) {
   const int cnt = count_dev ? min(n, *count_dev) : n;
-  const int64_t step = (int64_t)kGatherThreads * kUnroll;
-  for (int i = blockIdx.x; i < cnt; i += gridDim.x) {
-    const int pid = idx[i];
-    if (pid < 0 || pid >= num_pages) continue;
-    const u32x4* s = src + (int64_t)pid * page_vecs;
-    u32x4* d = dst + (int64_t)i * page_vecs;
-    for (int64_t v0 = threadIdx.x; v0 < page_vecs; v0 += step) {
-      u32x4 r[kUnroll];
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const int64_t v = v0 + (int64_t)u * kGatherThreads;
-        if (v < page_vecs) r[u] = kNtLoad ? __builtin_nontemporal_load(s + v) : s[v];
-      }
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const int64_t v = v0 + (int64_t)u * kGatherThreads;
-        if (v < page_vecs) {
-          if (kNtStore)
-            __builtin_nontemporal_store(r[u], d + v);
-          else
-            d[v] = r[u];
-        }
-      }
-    }
-  }
+  const int i = blockIdx.x / tiles_per_page;
+  if (i >= cnt) return;
+  const int pid = idx[i];
+  if (pid < 0 || pid >= num_pages) return;
+  const int64_t v = (int64_t)(blockIdx.x % tiles_per_page) * kGatherThreads + threadIdx.x;
+  if (v < page_vecs)
+    __builtin_nontemporal_store(__builtin_nontemporal_load(src + (int64_t)pid * page_vecs + v),
+                                dst + (int64_t)i * page_vecs + v);
 }
 
 // ---------------------------------------------------------------------------
 // Insert (optionally remapping K)
 // ---------------------------------------------------------------------------
-constexpr int kInsTile = 16;  // tokens per workgroup
+constexpr int kInsTile = 8;  // tokens per workgroup
 constexpr int kInsMaxHalf = 128;
 
 template <typename T>
@@ -658,7 +643,14 @@ __global__ __launch_bounds__(kThreads) void insert_scalar_kernel(InsertArgs a) {
   }
 }
 
-// Vectorised insert: 16-byte chunks; per tile of tokens, cos/sin in LDS.
+// Vectorised insert: 16-byte chunks, one (token, head, chunk pair) per item.
+// Each thread issues the non-temporal loads of its first kInsEarly items before
+// the tile's cos/sin are evaluated into LDS, so the trigonometry runs under the
+// load latency; items past kInsEarly x kThreads (large H x D) load as they go.
+// (Measured, 65,536 bf16 tokens, 8 heads x 128, remap on: 105 us against 112 us
+// for 16-token tiles with plain loads/stores issued after the cos/sin phase.)
+constexpr int kInsEarly = 2;
+
 template <typename T>
 __global__ __launch_bounds__(kThreads) void insert_vec_kernel(InsertArgs a) {
 #pragma clang fp contract(off)
@@ -669,37 +661,32 @@ __global__ __launch_bounds__(kThreads) void insert_vec_kernel(InsertArgs a) {
   const bool remap = a.inv_freq != nullptr;
   const int t0 = blockIdx.x * kInsTile;
   const int ntok = min(kInsTile, a.T - t0);
-  if (remap) {
-    for (int i = threadIdx.x; i < ntok * half; i += kThreads) {
-      const int tt = i / half, j = i - tt * half;
-      const int t = t0 + tt;
-      const float delta = (float)(a.tgt_pos[t] - a.orig_pos[t]);
-      const float ang = delta * a.inv_freq[j];
-      float s, c;
-      sincosf(ang, &s, &c);
-      cs[i] = make_float2(c, s);
-    }
-    __syncthreads();
-  }
   T* pool = static_cast<T*>(a.pool);
   const T* nk = static_cast<const T*>(a.new_k);
   const T* nv = static_cast<const T*>(a.new_v);
   const int chunks = half / N;             // chunk pairs per head
   const int per_tok = a.H * chunks;
-  for (int i = threadIdx.x; i < ntok * per_tok; i += kThreads) {
+  const int total = ntok * per_tok;
+
+  auto load = [&](int i, V& k1, V& k2, V& v1, V& v2) {
+    const int tt = i / per_tok;
+    const int r = i - tt * per_tok;
+    const int h = r / chunks, c = r - h * chunks;
+    const int64_t src = ((int64_t)(t0 + tt) * a.H + h) * a.D + c * N;
+    k1 = __builtin_nontemporal_load(reinterpret_cast<const V*>(nk + src));
+    k2 = __builtin_nontemporal_load(reinterpret_cast<const V*>(nk + src + half));
+    v1 = __builtin_nontemporal_load(reinterpret_cast<const V*>(nv + src));
+    v2 = __builtin_nontemporal_load(reinterpret_cast<const V*>(nv + src + half));
+  };
+  auto store = [&](int i, const V& k1, const V& k2, const V& v1, const V& v2) {
     const int tt = i / per_tok;
     const int r = i - tt * per_tok;
     const int h = r / chunks, c = r - h * chunks;
     const int t = t0 + tt;
     const int phys = a.target_pages[t / a.page_size];
-    if (phys < 0 || phys >= a.num_pages) continue;
+    if (phys < 0 || phys >= a.num_pages) return;
     const int64_t dst = (int64_t)phys * a.page_stride + (int64_t)(t % a.page_size) * a.tok_stride +
                         (int64_t)h * a.head_stride + c * N;
-    const int64_t src = ((int64_t)t * a.H + h) * a.D + c * N;
-    const V k1 = *reinterpret_cast<const V*>(nk + src);
-    const V k2 = *reinterpret_cast<const V*>(nk + src + half);
-    const V v1 = *reinterpret_cast<const V*>(nv + src);
-    const V v2 = *reinterpret_cast<const V*>(nv + src + half);
     V y1 = k1, y2 = k2;
     if (remap) {
       const float2* csr = cs + tt * half + c * N;
@@ -716,14 +703,43 @@ __global__ __launch_bounds__(kThreads) void insert_vec_kernel(InsertArgs a) {
         y2[e] = from_f32<T>(w1 + w2);
       }
     }
-    *reinterpret_cast<V*>(pool + dst) = y1;
-    *reinterpret_cast<V*>(pool + dst + half) = y2;
-    *reinterpret_cast<V*>(pool + dst + a.kv_stride) = v1;
-    *reinterpret_cast<V*>(pool + dst + a.kv_stride + half) = v2;
+    __builtin_nontemporal_store(y1, reinterpret_cast<V*>(pool + dst));
+    __builtin_nontemporal_store(y2, reinterpret_cast<V*>(pool + dst + half));
+    __builtin_nontemporal_store(v1, reinterpret_cast<V*>(pool + dst + a.kv_stride));
+    __builtin_nontemporal_store(v2, reinterpret_cast<V*>(pool + dst + a.kv_stride + half));
     if (t % a.page_size == 0 && h == 0 && c == 0) {
       a.valid[phys] = 1;
       a.positions[phys] = a.conv_pos + t;
     }
+  };
+
+  V k1[kInsEarly], k2[kInsEarly], v1[kInsEarly], v2[kInsEarly];
+#pragma unroll
+  for (int u = 0; u < kInsEarly; ++u) {
+    const int i = threadIdx.x + u * kThreads;
+    if (i < total) load(i, k1[u], k2[u], v1[u], v2[u]);
+  }
+  if (remap) {
+    for (int i = threadIdx.x; i < ntok * half; i += kThreads) {
+      const int tt = i / half, j = i - tt * half;
+      const int t = t0 + tt;
+      const float delta = (float)(a.tgt_pos[t] - a.orig_pos[t]);
+      const float ang = delta * a.inv_freq[j];
+      float s, c;
+      sincosf(ang, &s, &c);
+      cs[i] = make_float2(c, s);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int u = 0; u < kInsEarly; ++u) {
+    const int i = threadIdx.x + u * kThreads;
+    if (i < total) store(i, k1[u], k2[u], v1[u], v2[u]);
+  }
+  for (int i = threadIdx.x + kInsEarly * kThreads; i < total; i += kThreads) {
+    V x1, x2, y1, y2;
+    load(i, x1, x2, y1, y2);
+    store(i, x1, x2, y1, y2);
   }
 }
 
@@ -929,12 +945,14 @@ extern "C" int kessie_page_gather(const void* src_pool, int64_t page_bytes, cons
   KESSIE_REQUIRE(src_pool && idx && dst, KESSIE_ERR_INVALID, "page gather: null pointer");
   KESSIE_REQUIRE(page_bytes % 16 == 0 && aligned16(src_pool) && aligned16(dst), KESSIE_ERR_UNSUPPORTED,
                  "page gather: page_bytes and pointers must be 16-byte multiples/aligned");
-  // One workgroup per page slot, non-temporal loads and stores (measured best
-  // among plain/non-temporal x unroll 4/8 x grid 1K..64K for 64 KiB pages).
+  const int64_t page_vecs = page_bytes / 16;
+  const int64_t tiles = div_up(page_vecs, (int64_t)kGatherThreads);
+  KESSIE_REQUIRE(tiles * n < (1LL << 31), KESSIE_ERR_UNSUPPORTED, "page gather: %d pages of %lld bytes is too large",
+                 n, (long long)page_bytes);
   const u32x4* s = static_cast<const u32x4*>(src_pool);
   u32x4* d = static_cast<u32x4*>(dst);
-  hipLaunchKernelGGL((gather_kernel<true, true, 4>), dim3(n), dim3(kGatherThreads), 0, as_stream(stream), s,
-                     page_bytes / 16, idx, count_dev, n, num_pages, d);
+  hipLaunchKernelGGL(gather_kernel, dim3((unsigned)(tiles * n)), dim3(kGatherThreads), 0, as_stream(stream), s,
+                     page_vecs, (int)tiles, idx, count_dev, n, num_pages, d);
   return check_launch("page gather");
 }
 
