@@ -37,6 +37,9 @@ def _run(dev, b, hq, hkv, ctx, dtype, fog="vscale", window=0, ctx_lens=None, lay
         bias = fog_bias(ctx, 0.5, 0.5, {3, 17, ctx - 2}, 0.1).to(dev)
     elif fog == "vscale_batched":
         vs = torch.rand(b, ctx, generator=gen(dev, 77), device=dev)
+    elif fog == "both":
+        vs = torch.rand(b, ctx, generator=gen(dev, 77), device=dev)
+        bias = fog_bias(ctx, 0.5, 0.5, {3, 17, ctx - 2}, 0.1).to(dev)
     pool_arg = pool
     if layout == "kv_first":
         pool_arg = pool.permute(2, 0, 1, 3, 4).contiguous()
@@ -67,9 +70,19 @@ def test_decode_fp32_cpu_path_shape(dev):
     _check(out, ref, torch.float32)
 
 
-@pytest.mark.parametrize("fog", ["none", "bias", "vscale_batched"])
+@pytest.mark.parametrize("fog", ["none", "bias", "vscale_batched", "both"])
 def test_decode_fog_modes(dev, fog):
     out, ref = _run(dev, 3, 32, 8, 530, torch.bfloat16, fog=fog)
+    _check(out, ref, torch.bfloat16)
+
+
+@pytest.mark.parametrize("fog", ["bias", "both"])
+@pytest.mark.parametrize("window", [15, 100])
+def test_decode_fog_modes_windowed_ragged(dev, fog, window):
+    """Per-token fog values on the window's first page and the last, partial
+    page of ragged sequences (both edges read only the visible tokens)."""
+    out, ref = _run(dev, 3, 32, 8, 530, torch.bfloat16, fog=fog, window=window,
+                    ctx_lens=[530, 301, 17])
     _check(out, ref, torch.bfloat16)
 
 
