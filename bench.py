@@ -140,6 +140,25 @@ def time_decode(s, steps, warmup):
     return total_ms / steps, sum(kern) / len(kern)
 
 
+def _cpu_median(fn, reps=3):
+    """1 warm-up, then the median of ``reps`` timed calls (seconds)."""
+    fn()
+    ts = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t)
+    return sorted(ts)[len(ts) // 2]
+
+
+def _cpu_threads():
+    import torch
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    return cores
+
+
 def cpu_decode_baseline(s, budget_s=12.0):
     """The CPU oracle (oracle.attention.paged_decode_blockwise) on the GPU box's
     host cores: whole sequences of the same workload until ~budget_s seconds."""
@@ -184,7 +203,7 @@ def cpu_decode_baseline(s, budget_s=12.0):
 # ---------------------------------------------------------------------------
 # Secondary workloads
 # ---------------------------------------------------------------------------
-def bench_remap(dev, reps=20, sets=4, n_tok=65536, page_size=16, hkv=8, d=128, theta=500000.0):
+def bench_remap(dev, reps=20, sets=4, n_tok=65536, page_size=16, hkv=8, d=128, theta=500000.0, cpu=False):
     """RoPE remap, bf16, 65,536 tokens in 16-token pages, 8 KV heads, D=128,
     theta 5e5, only K rotated.  ``sets`` disjoint page sets rotate across reps
     so the 256 MB MALL cannot serve the next rep."""
@@ -221,7 +240,20 @@ def bench_remap(dev, reps=20, sets=4, n_tok=65536, page_size=16, hkv=8, d=128, t
     mean_ms = sum(ts) / len(ts)
     nbytes = 2 * n_tok * hkv * d * 2 + 2 * n_tok * 4 + pages * 4
     achieved = nbytes / (mean_ms * 1e-3) / 1e9
+    res_cpu = None
+    if cpu:
+        from oracle.rope import rope_remap_ref
+
+        cores = _cpu_threads()
+        k0 = pool[lists[0].long(), :, 0].cpu().reshape(n_tok, hkv, d)
+        o_c, t_c = orig.cpu(), tgt.cpu()
+        k = k0.clone()
+        sec = _cpu_median(lambda: rope_remap_ref(k, o_c, t_c, theta))
+        res_cpu = {"value": round(n_tok / sec / 1e6, 2), "unit": "Mtok/s", "cores": cores, "kind": "port",
+                   "sample": f"the full workload ({n_tok} tokens, K [T, {hkv}, {d}] bf16 gathered from the "
+                             f"pages), torch {torch.__version__}, 1 warm-up + median of 3"}
     return {
+        "cpu_baseline": res_cpu,
         "workload": f"RoPE remap bf16, {n_tok} tokens in {page_size}-token pages, {hkv} KV heads, D={d}, "
                     f"theta {theta:g}, K only, {sets} rotating page sets",
         "mtok_s": round(n_tok / (mean_ms * 1e-3) / 1e6, 1),
@@ -233,7 +265,7 @@ def bench_remap(dev, reps=20, sets=4, n_tok=65536, page_size=16, hkv=8, d=128, t
     }
 
 
-def bench_gather_evict(dev, reps=5):
+def bench_gather_evict(dev, reps=5, cpu=False):
     """Paged-KV gather + eviction: 65,536-page pool (1,048,576 tokens, 16-token
     pages, 8 KV heads x D=128 bf16), 64 sequences x 1,024 pages (random
     tables), per-page scores ~ U(0,1); evict the lowest 25%, compact the
@@ -289,7 +321,30 @@ def bench_gather_evict(dev, reps=5):
     gather_bytes = 2 * survivors * page_bytes
     alg = gather_bytes + num_pages * 4 * 2 + s * w * 4 + survivors * 4 + int(ev_cnt.item()) * 4
     ach = gather_bytes / (gat * 1e-3) / 1e9
+    res_cpu = None
+    if cpu:
+        import numpy as np
+
+        from oracle.pages import compact, gather_pages, select_evict
+
+        cores = _cpu_threads()
+        sc, tb, ln = scores.cpu().numpy(), tables.cpu().numpy(), lens.cpu().numpy()
+        pool_bytes = pool.view(torch.uint8).reshape(num_pages, -1).cpu().numpy()
+        ones = np.ones(num_pages, dtype=np.int8)
+
+        def cpu_pipeline():
+            v, _ = select_evict(sc, ones, -1, 0.25)
+            _, _, gidx = compact(tb, ln, v)
+            gather_pages(pool_bytes, gidx)
+
+        sec = _cpu_median(cpu_pipeline)
+        res_cpu = {"value": round(gather_bytes / sec / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+                   "sample": "the full workload (numpy select + compact + fancy-index gather of the survivors), "
+                             "1 warm-up + median of 3; GB/s of gathered bytes over the whole pipeline",
+                   "pipeline_ms": round(1000 * sec, 1)}
+        del pool_bytes
     return {
+        "cpu_baseline": res_cpu,
         "workload": "score evict 25% of 65,536 pages + compact 64x1024 tables + gather survivors (bf16 pages)",
         "pipeline_ms": round(tot, 4),
         "gather_kernel_ms": round(gat, 4),
@@ -302,7 +357,7 @@ def bench_gather_evict(dev, reps=5):
     }
 
 
-def bench_prefill(dev, reps=3, c=2048, L=1 << 20, hq=32, hkv=8, d=128):
+def bench_prefill(dev, reps=3, c=2048, L=1 << 20, hq=32, hkv=8, d=128, cpu=False, cpu_L=8192):
     """Chunked prefill, bf16 on MFMA: a 2,048-query chunk appended to a
     1,048,576-token paged KV (65,664 pages, random table), 32 q / 8 kv heads,
     D=128, causal, V-fog over the full context."""
@@ -339,13 +394,37 @@ def bench_prefill(dev, reps=3, c=2048, L=1 << 20, hq=32, hkv=8, d=128):
     ms = sum(a.elapsed_time(b) for a, b in zip(e0, e1)) / reps
     flops = 4 * d * hq * (c * L + c * (c + 1) // 2)
     tf = flops / (ms * 1e-3) / 1e12
+    res_cpu = None
+    if cpu:
+        # The full context's score matrix does not fit host memory: the oracle
+        # (blockwise online softmax) runs the same chunk on the last cpu_L
+        # prior tokens, and the time is extrapolated linearly in FLOPs.
+        from oracle.attention import paged_prefill_blockwise
+
+        cores = _cpu_threads()
+        ctx_s = cpu_L + c
+        pages_s = ctx_s // 16
+        tab_s = table[:, n_pages - pages_s:].contiguous()
+        lens_s = torch.tensor([ctx_s], dtype=torch.int32)
+        fog_s = fog[ctx - ctx_s:].cpu()
+        q_c = q.cpu()
+        rows = torch.arange(c)
+        t = time.perf_counter()
+        paged_prefill_blockwise(q_c, pool, tab_s.cpu(), lens_s, rows, fog_vscale=fog_s, block_pages=256)
+        sec = time.perf_counter() - t
+        flops_s = 4 * d * hq * (c * cpu_L + c * (c + 1) // 2)
+        res_cpu = {"value": round(flops_s / sec / 1e12, 4), "unit": "TFLOP/s", "cores": cores, "kind": "port",
+                   "sample": f"the same 2,048-query chunk over the last {cpu_L:,} prior tokens (fp32 blockwise "
+                             f"online softmax, pages copied from the device per block), one timed call",
+                   "seconds": round(sec, 2),
+                   "extrapolated_full_ms": round(1000 * sec * flops / flops_s, 0)}
     return {"workload": "chunked prefill bf16: 2048 queries on a 1,048,576-token paged context, 32q/8kv, D=128, "
-                        "causal, V-fog", "ms": round(ms, 3), "tflops": round(tf, 1),
+                        "causal, V-fog", "ms": round(ms, 3), "tflops": round(tf, 1), "cpu_baseline": res_cpu,
             "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(tf / BF16_PEAK_TFLOPS, 4), "algorithmic_flops": flops}}
 
 
-def bench_decode_fp32(dev, reps=20):
+def bench_decode_fp32(dev, reps=20, cpu=False):
     """Fog decode on the reference CPU path's shape, fp32: B=1, 32q/8kv, D=128,
     4,096-token context in 16-token pages."""
     import torch
@@ -362,8 +441,19 @@ def bench_decode_fp32(dev, reps=20):
         e1[i].record()
     torch.cuda.synchronize()
     ms = sum(a.elapsed_time(b) for a, b in zip(e0, e1)) / reps
+    res_cpu = None
+    if cpu:
+        from oracle.attention import paged_decode_ref
+
+        cores = _cpu_threads()
+        q_c, pool_c, tab_c, lens_c, fog_c = (s["q"].cpu(), s["pool"].cpu(), s["table"].cpu(), s["lens"].cpu(),
+                                             s["fog"].cpu())
+        sec = _cpu_median(lambda: paged_decode_ref(q_c, pool_c, tab_c, lens_c, fog_c))
+        res_cpu = {"value": round(s["bytes"] / sec / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+                   "sample": "the full workload (fp32 paged decode oracle), 1 warm-up + median of 3",
+                   "ms": round(1000 * sec, 3)}
     return {"workload": "fog decode fp32, B=1, 32q/8kv, D=128, 4096-token context",
-            "ms": round(ms, 5), "gbs": round(s["bytes"] / (ms * 1e-3) / 1e9, 1)}
+            "ms": round(ms, 5), "gbs": round(s["bytes"] / (ms * 1e-3) / 1e9, 1), "cpu_baseline": res_cpu}
 
 
 def bench_fog_bias(dev, reps=50, kv_len=131072, n_recall=1000):
@@ -405,7 +495,7 @@ def bench_fog_bias(dev, reps=50, kv_len=131072, n_recall=1000):
                                             "kind": "port", "sample": "the full vector, 3 reps"}}
 
 
-def bench_recall_inject(dev, reps=20, n_tok=65536, hkv=8, d=128, theta=500000.0):
+def bench_recall_inject(dev, reps=20, n_tok=65536, hkv=8, d=128, theta=500000.0, cpu=False):
     """Recall-inject: 65,536 recalled tokens (K and V, bf16, 8 kv heads,
     head_dim 128) already staged in HBM written into 4,096 random pages of an
     8,192-page pool with K re-rotated from its original to its new positions
@@ -456,7 +546,28 @@ def bench_recall_inject(dev, reps=20, n_tok=65536, hkv=8, d=128, theta=500000.0)
     h1.record()
     torch.cuda.synchronize()
     h2d = 5 * 2 * kv_bytes / (h0.elapsed_time(h1) * 1e-3) / 1e9
-    return {"workload": "recall-inject: 65,536 tokens K+V bf16 into 4,096 random pages with fused RoPE remap "
+    res_cpu = None
+    if cpu:
+        from oracle.pages import page_insert
+        from oracle.rope import rope_remap_ref
+
+        cores = _cpu_threads()
+        pool_c = pool.cpu().view(torch.int16).numpy()
+        k_c, v_c = new_k.cpu(), new_v.cpu().view(torch.int16).numpy()
+        o_c, t_c, pages_c = orig.cpu(), tgt.cpu(), tgt_pages.cpu().numpy()
+        valid_c, pos_c = valid.cpu().numpy(), positions.cpu().numpy()
+
+        def cpu_inject():
+            k = k_c.clone()
+            rope_remap_ref(k, o_c, t_c, theta)
+            page_insert(pool_c, k.view(torch.int16).numpy(), v_c, pages_c, valid_c, pos_c, 0)
+
+        sec = _cpu_median(cpu_inject)
+        res_cpu = {"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+                   "sample": "the full workload (torch remap of K, then the per-token page insert), 1 warm-up + "
+                             "median of 3", "ms": round(1000 * sec, 1)}
+    return {
+        "cpu_baseline": res_cpu,"workload": "recall-inject: 65,536 tokens K+V bf16 into 4,096 random pages with fused RoPE remap "
                         "(theta 5e5)", "ms": round(ms, 4), "gbs": round(gbs, 1),
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": nbytes},
@@ -760,22 +871,22 @@ def main():
     if not args.no_secondary:
         sec = {}
         log("secondary: RoPE remap")
-        sec["rope_remap"] = bench_remap(dev)
+        sec["rope_remap"] = bench_remap(dev, cpu=not args.no_cpu)
         result["rope_remap_mtok_s"] = sec["rope_remap"]["mtok_s"]
         torch.cuda.empty_cache()
         log("secondary: gather + evict")
-        sec["gather_evict"] = bench_gather_evict(dev)
+        sec["gather_evict"] = bench_gather_evict(dev, cpu=not args.no_cpu)
         torch.cuda.empty_cache()
         log("secondary: fp32 decode 4K")
-        sec["decode_fp32_4k"] = bench_decode_fp32(dev)
+        sec["decode_fp32_4k"] = bench_decode_fp32(dev, cpu=not args.no_cpu)
         torch.cuda.empty_cache()
         log("secondary: chunked prefill 2048 x 1M")
-        sec["prefill_1m"] = bench_prefill(dev)
+        sec["prefill_1m"] = bench_prefill(dev, cpu=not args.no_cpu)
         torch.cuda.empty_cache()
         log("secondary: fog bias producer")
         sec["fog_bias_131k"] = bench_fog_bias(dev)
         log("secondary: recall inject")
-        sec["recall_inject_65k"] = bench_recall_inject(dev)
+        sec["recall_inject_65k"] = bench_recall_inject(dev, cpu=not args.no_cpu)
         log("secondary: index query")
         sec["index_query_78k"] = bench_index_query(dev)
         log("secondary: HF tiered cache")
