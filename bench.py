@@ -420,8 +420,9 @@ def bench_prefill(dev, reps=3, c=2048, L=1 << 20, hq=32, hkv=8, d=128, cpu=False
                    "extrapolated_full_ms": round(1000 * sec * flops / flops_s, 0)}
     return {"workload": "chunked prefill bf16: 2048 queries on a 1,048,576-token paged context, 32q/8kv, D=128, "
                         "causal, V-fog", "ms": round(ms, 3), "tflops": round(tf, 1), "cpu_baseline": res_cpu,
-            "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                         "frac": round(tf / BF16_PEAK_TFLOPS, 4), "algorithmic_flops": flops}}
+            "roofline": {"bound": "mfma", "kernel": "prefill_mfma_kernel", "achieved": round(tf, 1),
+                         "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 4),
+                         "traffic": read_traffic("prefill_mfma_kernel"), "algorithmic_flops": flops}}
 
 
 def bench_decode_fp32(dev, reps=20, cpu=False):
@@ -566,12 +567,12 @@ def bench_recall_inject(dev, reps=20, n_tok=65536, hkv=8, d=128, theta=500000.0,
         res_cpu = {"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
                    "sample": "the full workload (torch remap of K, then the per-token page insert), 1 warm-up + "
                              "median of 3", "ms": round(1000 * sec, 1)}
-    return {
-        "cpu_baseline": res_cpu,"workload": "recall-inject: 65,536 tokens K+V bf16 into 4,096 random pages with fused RoPE remap "
+    return {"workload": "recall-inject: 65,536 tokens K+V bf16 into 4,096 random pages with fused RoPE remap "
                         "(theta 5e5)", "ms": round(ms, 4), "gbs": round(gbs, 1),
-            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": nbytes},
-            "h2d_pinned_gbs": round(h2d, 1)}
+            "roofline": {"bound": "hbm", "kernel": "insert_vec_kernel", "achieved": round(gbs, 1),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                         "traffic": read_traffic("insert_vec_kernel"), "algorithmic_bytes": nbytes},
+            "h2d_pinned_gbs": round(h2d, 1), "cpu_baseline": res_cpu}
 
 
 def bench_index_query(dev, reps=50, n=78125, d=256, k=5):
@@ -619,7 +620,7 @@ def bench_index_query(dev, reps=50, n=78125, d=256, k=5):
             "launches": 4, "scan_us": round(scan_us, 2),
             "roofline": {"bound": "hbm", "kernel": "cosine_scan_kernel", "achieved": round(scan_gbs, 1),
                          "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(scan_gbs / HBM_PEAK_GBS, 4),
-                         "algorithmic_bytes": nbytes},
+                         "traffic": read_traffic("cosine_scan_kernel"), "algorithmic_bytes": nbytes},
             "cpu_baseline": {"value": round(cpu_ms, 3), "unit": "ms", "cores": len(os.sched_getaffinity(0)),
                              "kind": "port", "sample": "numpy matrix-vector product + argsort, 20 reps"}}
 
@@ -689,7 +690,7 @@ def bench_hf_cache(dev, layers=32, heads=8, d=128, window=4096, prefill=8000, st
             "fog_apply_8k_us": round(fog_us, 2),
             "roofline": {"bound": "hbm", "kernel": "hf_fog_apply_kernel", "achieved": round(fog_gbs, 1),
                          "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(fog_gbs / HBM_PEAK_GBS, 4),
-                         "algorithmic_bytes": fog_bytes},
+                         "traffic": read_traffic("hf_fog_apply_kernel"), "algorithmic_bytes": fog_bytes},
             "cpu_baseline": {"value": round(cpu_ms, 2), "unit": "ms per step", "cores": cores, "kind": "port",
                              "sample": "2 decode steps of the reference's torch.cat / fog op sequence"}}
 
@@ -751,8 +752,9 @@ def bench_hbm_ceilings(dev, reps=10):
 def pmc_run(dev) -> None:
     """A short fixed sequence of launches for hardware-counter passes
     (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE): a 1 GiB device copy of
-    known size (the calibration kernel), then one decode, one remap and one
-    gather + evict pipeline of the bench workloads."""
+    known size (the calibration kernel), then one decode, one remap, one
+    gather + evict pipeline, one recall-inject, one index query, one HF fog
+    pass and one chunked prefill of the bench workloads."""
     import torch
 
     src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
@@ -769,6 +771,17 @@ def pmc_run(dev) -> None:
     bench_remap(dev, reps=1, sets=1)
     torch.cuda.empty_cache()
     bench_gather_evict(dev, reps=1)
+    torch.cuda.empty_cache()
+    bench_recall_inject(dev, reps=1)
+    torch.cuda.empty_cache()
+    bench_index_query(dev, reps=1)
+    from kessie_amd import ops
+
+    v = torch.randn(1, 8, 8192, 128, device=dev).bfloat16()
+    ops.hf_fog_apply(v, 0.5, 0.5, out=torch.empty_like(v))
+    del v
+    torch.cuda.empty_cache()
+    bench_prefill(dev, reps=1)
     torch.cuda.synchronize()
     log("pmc run done")
 
