@@ -629,8 +629,8 @@ def bench_hf_cache(dev, layers=32, heads=8, d=128, window=4096, prefill=8000, st
     """HF tiered cache (KeSSieCache) decode steps: 32 layers x (append one
     token, return K and the fog-weighted V over the ~8K-token window), bf16, 8
     kv heads, head_dim 128, window_size 4096 (no eviction in the timed steps);
-    plus the fused fog kernel alone over an 8,192-token window (its HBM
-    roofline).  CPU baseline: the reference's torch.cat / fog op sequence on
+    plus the fused append + fog launch alone over an 8,192-token window (its
+    HBM roofline).  CPU baseline: the reference's torch.cat / fog op sequence on
     the host cores for 2 steps."""
     import torch
 
@@ -655,20 +655,28 @@ def bench_hf_cache(dev, layers=32, heads=8, d=128, window=4096, prefill=8000, st
     e1.record()
     torch.cuda.synchronize()
     step_ms = e0.elapsed_time(e1) / steps
+    # The fused per-layer launch alone: append one token to an 8,191-token
+    # window and write the fogged V of all 8,192 tokens.
     n = 8192
-    v = torch.randn(1, heads, n, d, generator=g, device=dev).bfloat16()
-    out = torch.empty_like(v)
-    ops.hf_fog_apply(v, 0.5, 0.5, out=out)
+    k_ar = torch.randn(1, heads, n + 64, d, generator=g, device=dev).bfloat16()
+    v_ar = torch.randn(1, heads, n + 64, d, generator=g, device=dev).bfloat16()
+    vf = torch.empty(1, heads, n, d, dtype=torch.bfloat16, device=dev)
+
+    def fused():
+        ops.hf_append_fog(k_ar, v_ar, 0, n - 1, tok, tok, vf, 0.5, 0.5)
+
+    fused()
     reps = 50
     a, b = events(reps), events(reps)
     backlog()
     for i in range(reps):
         a[i].record()
-        ops.hf_fog_apply(v, 0.5, 0.5, out=out)
+        fused()
         b[i].record()
     torch.cuda.synchronize()
     fog_us = 1000.0 * sum(x.elapsed_time(y) for x, y in zip(a, b)) / reps
-    fog_bytes = 2 * v.numel() * 2
+    row = heads * d * 2
+    fog_bytes = (n - 1) * row + 2 * row + 2 * row + n * row  # read V window + new K/V, write new K/V + V'
     fog_gbs = fog_bytes / (fog_us * 1e-6) / 1e9
     from oracle.hf_cache import HFCacheModel
 
@@ -687,10 +695,10 @@ def bench_hf_cache(dev, layers=32, heads=8, d=128, window=4096, prefill=8000, st
     return {"workload": "HF tiered cache decode step: 32 layers, bf16, 8 kv heads, D=128, ~8K-token window "
                         "(window_size 4096), K + fog-weighted V returned per layer",
             "step_ms": round(step_ms, 4), "per_layer_us": round(1000.0 * step_ms / layers, 2),
-            "fog_apply_8k_us": round(fog_us, 2),
-            "roofline": {"bound": "hbm", "kernel": "hf_fog_apply_kernel", "achieved": round(fog_gbs, 1),
+            "append_fog_8k_us": round(fog_us, 2),
+            "roofline": {"bound": "hbm", "kernel": "hf_append_fog_kernel", "achieved": round(fog_gbs, 1),
                          "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(fog_gbs / HBM_PEAK_GBS, 4),
-                         "traffic": read_traffic("hf_fog_apply_kernel"), "algorithmic_bytes": fog_bytes},
+                         "traffic": read_traffic("hf_append_fog_kernel"), "algorithmic_bytes": fog_bytes},
             "cpu_baseline": {"value": round(cpu_ms, 2), "unit": "ms per step", "cores": cores, "kind": "port",
                              "sample": "2 decode steps of the reference's torch.cat / fog op sequence"}}
 
@@ -753,8 +761,8 @@ def pmc_run(dev) -> None:
     """A short fixed sequence of launches for hardware-counter passes
     (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE): a 1 GiB device copy of
     known size (the calibration kernel), then one decode, one remap, one
-    gather + evict pipeline, one recall-inject, one index query, one HF fog
-    pass and one chunked prefill of the bench workloads."""
+    gather + evict pipeline, one recall-inject, one index query, one HF
+    append + fog launch and one chunked prefill of the bench workloads."""
     import torch
 
     src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
@@ -777,9 +785,11 @@ def pmc_run(dev) -> None:
     bench_index_query(dev, reps=1)
     from kessie_amd import ops
 
-    v = torch.randn(1, 8, 8192, 128, device=dev).bfloat16()
-    ops.hf_fog_apply(v, 0.5, 0.5, out=torch.empty_like(v))
-    del v
+    v = torch.randn(1, 8, 8192 + 64, 128, device=dev).bfloat16()
+    k = torch.randn_like(v)
+    tok = torch.randn(1, 8, 1, 128, device=dev).bfloat16()
+    ops.hf_append_fog(k, v, 0, 8191, tok, tok, torch.empty(1, 8, 8192, 128, dtype=v.dtype, device=dev), 0.5, 0.5)
+    del v, k
     torch.cuda.empty_cache()
     bench_prefill(dev, reps=1)
     torch.cuda.synchronize()

@@ -358,6 +358,28 @@ int kessie_hf_fog_apply(const void* v, int64_t v_batch_stride,
                         int seq_len, int head_dim, double fog_alpha,
                         double fog_start, int dtype, void* stream);
 
+/* KeSSieCache.update for one layer in one launch (kessie_exp3.py:427-445:
+ * the torch.cat append of key/value_states, then the fog step): new_k/new_v
+ * [B][H][t_new][D] are written into the K/V arenas at window positions
+ * n_old .. n_old+t_new-1 (k_arena/v_arena point at the window start and share
+ * the arena strides), and, when vfog is non-null, vfog[b][h][t] =
+ * dtype(fp32(V[t]) * w[t]) over all n_old + t_new window tokens with the
+ * weights of kessie_hf_fog_weights_fill (V[t] read from the arena for
+ * t < n_old and from new_v otherwise).  Strides in elements, head_dim
+ * contiguous, 16-byte aligned rows (else KESSIE_ERR_UNSUPPORTED, nothing
+ * launched). */
+int kessie_hf_append_fog(void* k_arena, void* v_arena, int64_t arena_batch_stride,
+                         int64_t arena_head_stride, int64_t arena_tok_stride,
+                         const void* new_k, int64_t k_batch_stride,
+                         int64_t k_head_stride, int64_t k_tok_stride,
+                         const void* new_v, int64_t v_batch_stride,
+                         int64_t v_head_stride, int64_t v_tok_stride,
+                         void* vfog, int64_t vfog_batch_stride,
+                         int64_t vfog_head_stride, int64_t vfog_tok_stride,
+                         int batch, int num_heads, int n_old, int t_new,
+                         int head_dim, double fog_alpha, double fog_start,
+                         int dtype, void* stream);
+
 /* =========================================================================
  * Semantic index query
  * ========================================================================= */

@@ -77,6 +77,8 @@ SIGNATURES = {
     "kessie_probe_copy": (_I, [_P, _P, _I64, _P]),
     "kessie_probe_page_rmw": (_I, [_P, _I64, _I64, _I, _I, _P, _I, _I, _P]),
     "kessie_hf_fog_weights_fill": (_I, [_P, _I, _D, _D, _P]),
+    "kessie_hf_append_fog": (_I, [_P, _P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64, _I64, _I64,
+                                  _P, _I64, _I64, _I64, _I, _I, _I, _I, _I, _D, _D, _I, _P]),
     # v + 3 strides, out + 3 strides, B, H, N, D, fog_alpha, fog_start, dtype, stream
     "kessie_hf_fog_apply": (_I, [_P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _I, _I, _I, _I, _D, _D, _I, _P]),
     "kessie_index_query_workspace_bytes": (_SZ, [_I, _I]),

@@ -148,6 +148,62 @@ __global__ __launch_bounds__(kThreads) void hf_fog_apply_kernel(const T* __restr
   *reinterpret_cast<V8*>(out + b * o_bs + h * o_hs + t * o_ts + c * N) = y;
 }
 
+// Append + fog of one KeSSieCache layer in one pass: window tokens [0, n_old)
+// come from the V arena; tokens [n_old, n_old + t_new) come from new_v, and
+// those threads also write new_k / new_v into the arenas at window positions
+// n_old.. .  V' (when vfog is set) = dtype(fp32(V) * w[t]) over all
+// n_old + t_new tokens; without vfog only the new tokens are written.
+template <typename T>
+struct AppendFogArgs {
+  T* k_arena;  // window start of the K arena
+  T* v_arena;  // window start of the V arena (same strides)
+  int64_t a_bs, a_hs, a_ts;
+  const T* new_k;
+  int64_t k_bs, k_hs, k_ts;
+  const T* new_v;
+  int64_t v_bs, v_hs, v_ts;
+  T* vfog;
+  int64_t o_bs, o_hs, o_ts;
+  int H, n_old, t_new, D;
+  int fc;
+  float inv_den, alpha;
+  int form;
+};
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void hf_append_fog_kernel(AppendFogArgs<T> a) {
+#pragma clang fp contract(off)
+  constexpr int N = 16 / (int)sizeof(T);
+  typedef T V8 __attribute__((ext_vector_type(16 / sizeof(T))));
+  const int chunks = a.D / N;
+  const int first = a.vfog ? 0 : a.n_old;
+  const int n = a.n_old + a.t_new - first;
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= (int64_t)n * chunks) return;  // blockIdx.y: one (batch, head) row
+  const int c = (int)(i % chunks);
+  const int t = first + (int)(i / chunks);
+  const int bh = blockIdx.y;
+  const int b = bh / a.H, h = bh - b * a.H;
+  const int64_t ao = b * a.a_bs + h * a.a_hs + (int64_t)t * a.a_ts + c * N;
+  V8 x;
+  if (t >= a.n_old) {
+    const int tn = t - a.n_old;
+    x = *reinterpret_cast<const V8*>(a.new_v + b * a.v_bs + h * a.v_hs + (int64_t)tn * a.v_ts + c * N);
+    const V8 kx = *reinterpret_cast<const V8*>(a.new_k + b * a.k_bs + h * a.k_hs + (int64_t)tn * a.k_ts + c * N);
+    *reinterpret_cast<V8*>(a.k_arena + ao) = kx;
+    *reinterpret_cast<V8*>(a.v_arena + ao) = x;
+  } else {
+    x = *reinterpret_cast<const V8*>(a.v_arena + ao);
+  }
+  if (a.vfog) {
+    const float w = hf_fog_weight(t, a.fc, a.inv_den, a.alpha, a.form);
+    V8 y;
+#pragma unroll
+    for (int e = 0; e < N; ++e) y[e] = round_to<T>(to_f32(x[e]) * w);
+    *reinterpret_cast<V8*>(a.vfog + b * a.o_bs + h * a.o_hs + (int64_t)t * a.o_ts + c * N) = y;
+  }
+}
+
 struct HfFog {
   int fc;
   float inv_den;
@@ -382,4 +438,55 @@ extern "C" int kessie_hf_fog_apply(const void* v, int64_t v_bs, int64_t v_hs, in
       return KESSIE_ERR_UNSUPPORTED;
   }
   return check_launch("hf fog apply");
+}
+
+template <typename T>
+int hf_append_fog_launch(AppendFogArgs<T> a, int BH, hipStream_t s) {
+  constexpr int N = 16 / (int)sizeof(T);
+  const int n = a.vfog ? a.n_old + a.t_new : a.t_new;
+  const int64_t items = (int64_t)n * (a.D / N);
+  const int64_t gx = (items + kThreads - 1) / kThreads;
+  KESSIE_REQUIRE(gx <= 0x7fffffff && BH <= 65535, KESSIE_ERR_UNSUPPORTED, "hf append fog: too large");
+  hipLaunchKernelGGL(hf_append_fog_kernel<T>, dim3((unsigned)gx, (unsigned)BH), dim3(kThreads), 0, s, a);
+  return check_launch("hf append fog");
+}
+
+extern "C" int kessie_hf_append_fog(void* k_arena, void* v_arena, int64_t a_bs, int64_t a_hs, int64_t a_ts,
+                                    const void* new_k, int64_t k_bs, int64_t k_hs, int64_t k_ts, const void* new_v,
+                                    int64_t v_bs, int64_t v_hs, int64_t v_ts, void* vfog, int64_t o_bs, int64_t o_hs,
+                                    int64_t o_ts, int batch, int num_heads, int n_old, int t_new, int head_dim,
+                                    double fog_alpha, double fog_start, int dtype, void* stream) {
+  clear_error();
+  KESSIE_REQUIRE(batch >= 0 && num_heads > 0 && n_old >= 0 && t_new >= 0 && head_dim > 0, KESSIE_ERR_INVALID,
+                 "hf append fog: B=%d H=%d n_old=%d t_new=%d D=%d", batch, num_heads, n_old, t_new, head_dim);
+  KESSIE_REQUIRE((int64_t)n_old + t_new <= 0x7fffffff, KESSIE_ERR_INVALID, "hf append fog: window too long");
+  if (batch == 0 || (t_new == 0 && (vfog == nullptr || n_old == 0))) return KESSIE_OK;
+  KESSIE_REQUIRE(k_arena && v_arena && (t_new == 0 || (new_k && new_v)), KESSIE_ERR_INVALID,
+                 "hf append fog: null pointer");
+  const int esz = dtype_size(dtype);
+  KESSIE_REQUIRE(esz > 0, KESSIE_ERR_UNSUPPORTED, "hf append fog: dtype %d", dtype);
+  const int N = 16 / esz;
+  const bool rows16 = head_dim % N == 0 && aligned16(k_arena) && aligned16(v_arena) && a_bs % N == 0 &&
+                      a_hs % N == 0 && a_ts % N == 0 &&
+                      (t_new == 0 || (aligned16(new_k) && aligned16(new_v) && k_bs % N == 0 && k_hs % N == 0 &&
+                                      k_ts % N == 0 && v_bs % N == 0 && v_hs % N == 0 && v_ts % N == 0)) &&
+                      (vfog == nullptr || (aligned16(vfog) && o_bs % N == 0 && o_hs % N == 0 && o_ts % N == 0));
+  KESSIE_REQUIRE(rows16, KESSIE_ERR_UNSUPPORTED, "hf append fog: rows must be 16-byte aligned multiples of 16 bytes");
+  const HfFog f = hf_fog_params(n_old + t_new, fog_alpha, fog_start);
+  const hipStream_t s = as_stream(stream);
+  const int BH = batch * num_heads;
+#define KESSIE_AF_ARGS(T)                                                                                        \
+  AppendFogArgs<T>{static_cast<T*>(k_arena), static_cast<T*>(v_arena), a_bs, a_hs, a_ts,                       \
+                   static_cast<const T*>(new_k), k_bs, k_hs, k_ts, static_cast<const T*>(new_v), v_bs, v_hs, v_ts, \
+                   static_cast<T*>(vfog), o_bs, o_hs, o_ts, num_heads, n_old, t_new, head_dim, f.fc, f.inv_den,  \
+                   f.alpha, f.form}
+  switch (dtype) {
+    case KESSIE_DTYPE_BF16: return hf_append_fog_launch<bf16_t>(KESSIE_AF_ARGS(bf16_t), BH, s);
+    case KESSIE_DTYPE_F16: return hf_append_fog_launch<f16_t>(KESSIE_AF_ARGS(f16_t), BH, s);
+    case KESSIE_DTYPE_F32: return hf_append_fog_launch<float>(KESSIE_AF_ARGS(float), BH, s);
+    default:
+      set_error(KESSIE_ERR_UNSUPPORTED, "hf append fog: dtype %d", dtype);
+      return KESSIE_ERR_UNSUPPORTED;
+  }
+#undef KESSIE_AF_ARGS
 }

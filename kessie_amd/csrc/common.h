@@ -78,5 +78,6 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
 __host__ __device__ __forceinline__ int div_up(int a, int b) { return (a + b - 1) / b; }
+__host__ __device__ __forceinline__ int64_t div_up(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 }  // namespace kessie

@@ -195,21 +195,31 @@ class KeSSieCache:
             L.v = torch.empty_like(L.k)
             L.off = L.n = 0
         self._reserve_tail(L, t)
-        end = L.off + L.n
-        L.k[:, :, end:end + t].copy_(key_states)
-        L.v[:, :, end:end + t].copy_(value_states)
-        L.n += t
+        n_old, n = L.n, L.n + t
+        cc = max(1, int(n * self.fog_start))
+        fog_on = self.fog_alpha > 0 and n - cc > 0
+        vf = None
+        if fog_on:
+            if L.vfog is None or L.vfog.shape[2] < n:
+                L.vfog = torch.empty(b, h, max(n, 2 * self.window_size + 256), d, dtype=L.v.dtype,
+                                     device=L.v.device)
+            vf = L.vfog[:, :, :n]
+        # One launch appends the new tokens and writes the fogged window.
+        fused = ops.hf_append_fog(L.k, L.v, L.off, n_old, key_states, value_states, vf, self.fog_alpha,
+                                  self.fog_start)
+        if not fused:
+            end = L.off + n_old
+            L.k[:, :, end:end + t].copy_(key_states)
+            L.v[:, :, end:end + t].copy_(value_states)
+        L.n = n
         if layer_idx == 0:
             self.seen_tokens = self.window_start + L.n
             self._seen_tokens = self.seen_tokens
         k, v = L.views()
-        cc = max(1, int(L.n * self.fog_start))
-        if self.fog_alpha <= 0 or L.n - cc <= 0:
+        if not fog_on:
             return k, v
-        if L.vfog is None or L.vfog.shape[2] < L.n:
-            L.vfog = torch.empty(b, h, max(L.n, 2 * self.window_size + 256), d, dtype=L.v.dtype, device=L.v.device)
-        vf = L.vfog[:, :, :L.n]
-        ops.hf_fog_apply(v, self.fog_alpha, self.fog_start, out=vf)
+        if not fused:
+            ops.hf_fog_apply(v, self.fog_alpha, self.fog_start, out=vf)
         return k, vf
 
     def evict_if_needed(self):

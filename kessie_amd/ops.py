@@ -582,6 +582,43 @@ def hf_fog_weights(seq_len: int, fog_alpha: float, fog_start: float, device=None
     return out[:seq_len]
 
 
+def hf_append_fog(k_arena: torch.Tensor, v_arena: torch.Tensor, off: int, n_old: int, new_k: torch.Tensor,
+                  new_v: torch.Tensor, vfog: Optional[torch.Tensor], fog_alpha: float, fog_start: float,
+                  stream=None) -> bool:
+    """One KeSSieCache layer update in one launch: new_k/new_v [B, H, T, D] go
+    to arena positions off+n_old .. off+n_old+T-1, and, if ``vfog`` (a
+    [B, H, n_old+T, D] view) is given, it receives the fog-weighted V of the
+    whole window.  Returns False, having done nothing, when a row is not a
+    16-byte aligned multiple of 16 bytes (the caller then copies and calls
+    hf_fog_apply)."""
+    b, h, t, d = new_k.shape
+    if (k_arena.dim() != 4 or k_arena.shape != v_arena.shape or k_arena.stride() != v_arena.stride()
+            or new_v.shape != new_k.shape or k_arena.dtype != new_k.dtype or new_v.dtype != new_k.dtype
+            or k_arena.shape[0] != b or k_arena.shape[1] != h or k_arena.shape[3] != d
+            or off + n_old + t > k_arena.shape[2] or k_arena.stride(3) != 1 or new_k.stride(3) != 1
+            or new_v.stride(3) != 1):
+        raise ValueError("hf_append_fog: arena / new state shapes do not match")
+    if vfog is not None and (vfog.shape != (b, h, n_old + t, d) or vfog.dtype != new_k.dtype or vfog.stride(3) != 1):
+        raise ValueError("hf_append_fog: vfog must be [B, H, n_old+T, D] of the cache dtype")
+    es = k_arena.element_size()
+    kp = k_arena.data_ptr() + off * k_arena.stride(2) * es
+    vp = v_arena.data_ptr() + off * v_arena.stride(2) * es
+    lib = _lib.load()
+    st = lib.kessie_hf_append_fog(
+        C.c_void_p(kp), C.c_void_p(vp), k_arena.stride(0), k_arena.stride(1), k_arena.stride(2),
+        _ptr(new_k), new_k.stride(0), new_k.stride(1), new_k.stride(2),
+        _ptr(new_v), new_v.stride(0), new_v.stride(1), new_v.stride(2),
+        _ptr(vfog),
+        vfog.stride(0) if vfog is not None else 0, vfog.stride(1) if vfog is not None else 0,
+        vfog.stride(2) if vfog is not None else 0,
+        b, h, n_old, t, d, float(fog_alpha), float(fog_start), dtype_code(new_k.dtype),
+        _stream_ptr(stream, k_arena.device))
+    if st == _lib.ERR_UNSUPPORTED:
+        return False
+    _lib.check("kessie_hf_append_fog", st)
+    return True
+
+
 def hf_fog_apply(v: torch.Tensor, fog_alpha: float, fog_start: float, out: Optional[torch.Tensor] = None,
                  stream=None) -> torch.Tensor:
     """out = dtype(fp32(v) * w[t]) for v [B, H, N, D] (head_dim contiguous) with

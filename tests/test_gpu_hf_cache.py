@@ -41,6 +41,63 @@ def test_hf_fog_apply(dev, dtype):
     assert torch.equal(out, hf_fogged_v(v, 0.5, 0.5))
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("n_old,t_new", [(250, 1), (250, 37), (0, 40), (5000, 1)])
+def test_hf_append_fog(dev, dtype, n_old, t_new):
+    """The fused append + fog launch: arena rows after the append equal the
+    new states, untouched rows keep their bytes, and the fogged window equals
+    the oracle's fog over the concatenated V."""
+    from kessie_amd import ops
+
+    b, h, d, off, cap = 2, 4, 64, 9, n_old + t_new + 40
+    k_ar = randn((b, h, cap, d), dtype, dev, 1)
+    v_ar = randn((b, h, cap, d), dtype, dev, 2)
+    k0, v0 = k_ar.clone(), v_ar.clone()
+    big = randn((b, h, t_new, d + 8), dtype, dev, 3)
+    new_k = big[..., :d]                                # token stride d+8: still 16-byte rows
+    new_v = randn((b, h, t_new, d), dtype, dev, 4)
+    n = n_old + t_new
+    vfog = torch.empty(b, h, n + 3, d, dtype=dtype, device=dev)[:, :, :n]
+    assert ops.hf_append_fog(k_ar, v_ar, off, n_old, new_k, new_v, vfog, 0.5, 0.5)
+    torch.cuda.synchronize()
+    s = slice(off + n_old, off + n)
+    assert torch.equal(k_ar[:, :, s], new_k) and torch.equal(v_ar[:, :, s], new_v)
+    keep = torch.ones(cap, dtype=torch.bool)
+    keep[s] = False
+    assert torch.equal(k_ar[:, :, keep], k0[:, :, keep]) and torch.equal(v_ar[:, :, keep], v0[:, :, keep])
+    want = hf_fogged_v(torch.cat([v0[:, :, off:off + n_old], new_v], dim=2), 0.5, 0.5)
+    assert torch.equal(vfog, want)
+
+
+def test_hf_append_only_and_unaligned_fallback(dev):
+    """vfog=None appends without a fog pass; rows that are not 16-byte multiples
+    are refused without writing (the cache then takes its copy path)."""
+    from kessie_amd import ops
+    from kessie_amd.hf_cache import KeSSieCache
+
+    k_ar = torch.zeros(1, 2, 64, 32, dtype=torch.bfloat16, device=dev)
+    v_ar = torch.zeros_like(k_ar)
+    nk, nv = randn((1, 2, 3, 32), torch.bfloat16, dev, 5), randn((1, 2, 3, 32), torch.bfloat16, dev, 6)
+    assert ops.hf_append_fog(k_ar, v_ar, 4, 10, nk, nv, None, 0.5, 0.5)
+    torch.cuda.synchronize()
+    assert torch.equal(k_ar[:, :, 14:17], nk) and torch.equal(v_ar[:, :, 14:17], nv)
+    assert torch.count_nonzero(k_ar[:, :, :14]) == 0 and torch.count_nonzero(k_ar[:, :, 17:]) == 0
+    odd = randn((1, 2, 3, 33), torch.bfloat16, dev, 7)[..., :32]   # token stride 33 elements
+    before = k_ar.clone()
+    assert not ops.hf_append_fog(k_ar, v_ar, 0, 0, odd, nv, None, 0.5, 0.5)
+    torch.cuda.synchronize()
+    assert torch.equal(k_ar, before)
+    # The cache falls back to copies + the fog kernel and stays exact.
+    cache, model = KeSSieCache(window_size=16), HFCacheModel(window_size=16)
+    for step in range(3):
+        big_k = randn((1, 2, 5, 33), torch.bfloat16, dev, 20 + step)[..., :32]
+        big_v = randn((1, 2, 5, 33), torch.bfloat16, dev, 40 + step)[..., :32]
+        k, v = cache.update(big_k, big_v, 0)
+        mk, mv = model.update(big_k, big_v, 0)
+        torch.cuda.synchronize()
+        assert torch.equal(k, mk) and torch.equal(v, mv)
+
+
 def _check_layer(cache, model, li):
     k, v = cache[li]
     assert torch.equal(k, model.key_cache[li]) and torch.equal(v, model.value_cache[li])
