@@ -126,8 +126,12 @@ __global__ __launch_bounds__(kThreads) void scan_counts_kernel(const int* counts
   if (threadIdx.x == 0 && total) *total = carry;
 }
 
+// Writes the ids satisfying the predicate in element order; when clear_valid
+// (clear_alloc) is set, each listed page also gets valid = 0 (allocated = 0):
+// only the thread that evaluated a page's predicate touches its flags.
 __global__ __launch_bounds__(kThreads) void compact_write_kernel(PredArgs a, int n, const int* block_offsets,
-                                                                 int32_t* out) {
+                                                                 int32_t* out, int8_t* clear_valid,
+                                                                 int8_t* clear_alloc) {
   __shared__ int sm[kWaves + 1];
   const int base = blockIdx.x * kChunk + threadIdx.x * kItems;
   unsigned flags = 0;
@@ -143,46 +147,56 @@ __global__ __launch_bounds__(kThreads) void compact_write_kernel(PredArgs a, int
   int total;
   int pos = block_exclusive_scan(c, &total, sm) + block_offsets[blockIdx.x];
 #pragma unroll
-  for (int e = 0; e < kItems; ++e)
-    if (flags & (1u << e)) out[pos++] = base + e;
-}
-
-// Marks the listed pages: valid=0 (and allocated=0 when given).
-__global__ __launch_bounds__(kThreads) void mark_evicted_kernel(const int32_t* list, const int32_t* count,
-                                                                int8_t* valid, int8_t* allocated, int num_pages) {
-  const int n = *count;
-  for (int i = blockIdx.x * kThreads + threadIdx.x; i < n; i += gridDim.x * kThreads) {
-    const int id = list[i];
-    if (id < 0 || id >= num_pages) continue;
-    valid[id] = 0;
-    if (allocated) allocated[id] = 0;
+  for (int e = 0; e < kItems; ++e) {
+    if (!(flags & (1u << e))) continue;
+    out[pos++] = base + e;
+    if (clear_valid) clear_valid[base + e] = 0;
+    if (clear_alloc) clear_alloc[base + e] = 0;
   }
 }
 
 // ---------------------------------------------------------------------------
-// Radix select (one workgroup): the key of rank k-1 among valid pages.
-// Keys are 64-bit (ordered score << 32 | page id), so they are unique and the
-// k smallest form exactly the set the total order (score, id) puts first.
-//   pass A  streams every page: counts the valid ones and histograms the top
-//           12 bits of the ordered score (4096 bins);
-//   pass B  streams again and copies the keys of the bucket holding rank k-1
-//           into LDS (up to kSelCap of them);
-//   then    the low 20 score bits (two 10-bit passes) and, when several
-//           candidates share that score, the page id (11+11+10 bits) are
-//           resolved on the LDS copy.
-// A bucket larger than kSelCap (heavily tied scores) takes the fallback: eight
-// byte-wide passes that each stream the pages again.  Streaming loads are
-// issued kSelBatch at a time per thread.  Histogram atomics only count.
+// Radix select: the key of rank k-1 among valid pages.  Keys are 64-bit
+// (ordered score << 32 | page id), so they are unique and the k smallest form
+// exactly the set the total order (score, id) puts first.  Five launches, no
+// host round trip:
+//   clear     zero the global 4096-bin histogram and counters (a fill kernel:
+//             graph-capture safe);
+//   hist      many workgroups histogram the top 12 bits of the ordered score
+//             of valid pages in LDS and add them to the global histogram;
+//   bucket    one workgroup derives k from the valid count and picks the bin
+//             holding rank k-1 and the rank inside it;
+//   collect   many workgroups append that bin's keys (low 20 score bits, page
+//             id) to a candidate list, one atomic per workgroup tile;
+//   resolve   one workgroup resolves the low 20 bits (two 10-bit passes) and,
+//             when several candidates share that score, the page id (11+11+10
+//             bits) on the candidates -- copied to LDS when they fit, read in
+//             place otherwise (heavily tied scores).
+// Histogram and list atomics only count; the result does not depend on their
+// order.  (Folding bucket and resolve into the last workgroup of hist and
+// collect measured slower: 46 us against 26 us for 65,536 pages.)
 // ---------------------------------------------------------------------------
 constexpr int kSelThreads = 1024;
 constexpr int kSelWaves = kSelThreads / 64;
-constexpr int kSelBatch = 32;
-constexpr int kSelCap = 12288;  // candidate keys held in LDS
+constexpr int kSelCap = 12288;   // candidate keys held in LDS
+constexpr int kSelBins = 4096;
+constexpr int kSelPer = 4;       // keys per thread per hist/collect tile
+constexpr int kSelTile = kSelThreads * kSelPer;
+constexpr int kSelMaxGrid = 1024;
 
 struct SelectOut {
   unsigned long long key_thr;  // largest evicted key
   int k;                       // number evicted
   int n_valid;
+};
+
+struct SelScratch {
+  int hist[kSelBins];
+  int n_valid;
+  int ncand;
+  int k;      // keys to evict (0: nothing to resolve)
+  int rank;   // rank of key k-1 inside bin `top`
+  uint32_t top;
 };
 
 __device__ __forceinline__ uint32_t ordered_score(float s) {
@@ -209,6 +223,7 @@ __device__ __forceinline__ int sel_block_scan(int v, int* sm) {
       sm[w] = acc;
       acc += t;
     }
+    sm[kSelWaves] = acc;
   }
   __syncthreads();
   const int res = x - v + sm[wave];
@@ -241,76 +256,54 @@ __device__ __forceinline__ void sel_pick(const int* bins, int nb, int rank, int*
   __syncthreads();
 }
 
-// Wave 0: the digit of a 256-bin histogram whose range holds `rank`.
-__device__ __forceinline__ void pick_digit256(const int* tot, int rank, int* s_digit, int* s_rank) {
-  const int lane = threadIdx.x;
-  const int c0 = tot[4 * lane], c1 = tot[4 * lane + 1], c2 = tot[4 * lane + 2], c3 = tot[4 * lane + 3];
-  const int sum = c0 + c1 + c2 + c3;
-  int incl = sum;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int y = __shfl_up(incl, o, 64);
-    if (lane >= o) incl += y;
-  }
-  const int excl = incl - sum;
-  if (rank >= excl && rank < incl) {
-    int r = rank - excl, d = 4 * lane;
-    if (r >= c0) {
-      r -= c0;
-      ++d;
-      if (r >= c1) {
-        r -= c1;
-        ++d;
-        if (r >= c2) {
-          r -= c2;
-          ++d;
-        }
-      }
-    }
-    *s_digit = d;
-    *s_rank = r;
+__global__ __launch_bounds__(kThreads) void sel_clear_kernel(SelScratch* ss) {
+  for (int e = threadIdx.x; e < kSelBins; e += kThreads) ss->hist[e] = 0;
+  if (threadIdx.x == 0) {
+    ss->n_valid = 0;
+    ss->ncand = 0;
+    ss->k = 0;
+    ss->rank = 0;
+    ss->top = 0;
   }
 }
 
-__global__ __launch_bounds__(kSelThreads) void radix_select_kernel(const float* __restrict__ scores,
-                                                                   const int8_t* __restrict__ valid, int n,
-                                                                   int k_evict, float evict_fraction,
-                                                                   SelectOut* out) {
-  __shared__ int hist[4096];
-  __shared__ uint32_t cand_s[kSelCap];  // low 20 bits of the ordered score
-  __shared__ uint32_t cand_i[kSelCap];  // page id
-  __shared__ int sm[kSelWaves + 1];
-  __shared__ int s_digit, s_rank, s_nvalid, s_ncand, s_id;
-  const int tid = threadIdx.x;
-
-  // Pass A.
-  for (int e = tid; e < 4096; e += kSelThreads) hist[e] = 0;
-  if (tid == 0) {
-    s_nvalid = 0;
-    s_ncand = 0;
-  }
+__global__ __launch_bounds__(kSelThreads) void sel_hist_kernel(const float* __restrict__ scores,
+                                                               const int8_t* __restrict__ valid, int n,
+                                                               SelScratch* ss) {
+  __shared__ int hist[kSelBins];
+  for (int e = threadIdx.x; e < kSelBins; e += kSelThreads) hist[e] = 0;
   __syncthreads();
   int c = 0;
-  for (int b0 = 0; b0 < n; b0 += kSelBatch * kSelThreads) {
-    float sc[kSelBatch];
-    int8_t vv[kSelBatch];
+  for (int64_t t0 = (int64_t)blockIdx.x * kSelTile; t0 < n; t0 += (int64_t)gridDim.x * kSelTile) {
+    float sc[kSelPer];
+    int8_t vv[kSelPer];
 #pragma unroll
-    for (int j = 0; j < kSelBatch; ++j) {
-      const int i = b0 + j * kSelThreads + tid;
+    for (int j = 0; j < kSelPer; ++j) {
+      const int64_t i = t0 + j * kSelThreads + threadIdx.x;
       vv[j] = i < n ? valid[i] : (int8_t)0;
       sc[j] = i < n ? scores[i] : 0.0f;
     }
 #pragma unroll
-    for (int j = 0; j < kSelBatch; ++j) {
+    for (int j = 0; j < kSelPer; ++j) {
       if (vv[j] != 1) continue;
       ++c;
       atomicAdd(&hist[ordered_score(sc[j]) >> 20], 1);
     }
   }
   for (int o = 32; o >= 1; o >>= 1) c += __shfl_xor(c, o, 64);
-  if ((tid & 63) == 0) atomicAdd(&s_nvalid, c);
+  if ((threadIdx.x & 63) == 0 && c) atomicAdd(&ss->n_valid, c);
   __syncthreads();
-  const int n_valid = s_nvalid;
+  for (int e = threadIdx.x; e < kSelBins; e += kSelThreads)
+    if (hist[e]) atomicAdd(&ss->hist[e], hist[e]);
+}
+
+__global__ __launch_bounds__(kSelThreads) void sel_bucket_kernel(SelScratch* ss, int k_evict, float evict_fraction,
+                                                                 SelectOut* out) {
+  __shared__ int hist[kSelBins];
+  __shared__ int sm[kSelWaves + 1];
+  __shared__ int s_digit, s_rank;
+  for (int e = threadIdx.x; e < kSelBins; e += kSelThreads) hist[e] = ss->hist[e];
+  const int n_valid = ss->n_valid;
   long long k;
   if (k_evict >= 0) {
     k = min(k_evict, n_valid);
@@ -319,151 +312,133 @@ __global__ __launch_bounds__(kSelThreads) void radix_select_kernel(const float* 
     if (k < 0) k = 0;
     if (k > n_valid) k = n_valid;
   }
+  __syncthreads();
   if (k == 0) {
-    if (tid == 0) {
+    if (threadIdx.x == 0) {
       out->key_thr = 0;
       out->k = 0;
       out->n_valid = n_valid;
+      ss->k = 0;
     }
     return;
   }
-  int rank = (int)k - 1;
-  sel_pick(hist, 4096, rank, sm, &s_digit, &s_rank);
-  const uint32_t top = (uint32_t)s_digit;
-  rank = s_rank;
-  const int bucket = hist[top];
-  __syncthreads();
-
-  uint32_t score = 0, idp = 0;
-  if (bucket <= kSelCap) {
-    // Pass B: the bucket's keys into LDS (slot order is irrelevant: only
-    // counts are taken from here on).
-    for (int b0 = 0; b0 < n; b0 += kSelBatch * kSelThreads) {
-      float sc[kSelBatch];
-      int8_t vv[kSelBatch];
-#pragma unroll
-      for (int j = 0; j < kSelBatch; ++j) {
-        const int i = b0 + j * kSelThreads + tid;
-        vv[j] = i < n ? valid[i] : (int8_t)0;
-        sc[j] = i < n ? scores[i] : 0.0f;
-      }
-#pragma unroll
-      for (int j = 0; j < kSelBatch; ++j) {
-        if (vv[j] != 1) continue;
-        const uint32_t ks = ordered_score(sc[j]);
-        if ((ks >> 20) != top) continue;
-        const int pos = atomicAdd(&s_ncand, 1);
-        cand_s[pos] = ks & 0xFFFFFu;
-        cand_i[pos] = (uint32_t)(b0 + j * kSelThreads + tid);
-      }
-    }
-    __syncthreads();
-    const int nc = s_ncand;
-    uint32_t low = 0;
-    int ties = 0;
-    for (int pass = 0; pass < 2; ++pass) {
-      const int sh = 10 - 10 * pass;
-      for (int e = tid; e < 1024; e += kSelThreads) hist[e] = 0;
-      __syncthreads();
-      for (int q = tid; q < nc; q += kSelThreads) {
-        const uint32_t v = cand_s[q];
-        if (pass == 0 || (v >> 10) == low) atomicAdd(&hist[(v >> sh) & 1023u], 1);
-      }
-      __syncthreads();
-      sel_pick(hist, 1024, rank, sm, &s_digit, &s_rank);
-      low = (low << 10) | (uint32_t)s_digit;
-      rank = s_rank;
-      ties = hist[s_digit];
-      __syncthreads();
-    }
-    score = (top << 20) | low;
-    if (ties == 1) {
-      for (int q = tid; q < nc; q += kSelThreads)
-        if (cand_s[q] == low) s_id = (int)cand_i[q];
-      __syncthreads();
-      idp = (uint32_t)s_id;
-    } else {
-      for (int pass = 0; pass < 3; ++pass) {
-        const int width = pass < 2 ? 11 : 10;
-        const int sh = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
-        for (int e = tid; e < 2048; e += kSelThreads) hist[e] = 0;
-        __syncthreads();
-        for (int q = tid; q < nc; q += kSelThreads) {
-          if (cand_s[q] != low) continue;
-          const uint32_t id = cand_i[q];
-          if (pass == 0 || (id >> (sh + width)) == idp) atomicAdd(&hist[(id >> sh) & ((1u << width) - 1u)], 1);
-        }
-        __syncthreads();
-        sel_pick(hist, 2048, rank, sm, &s_digit, &s_rank);
-        idp = (idp << width) | (uint32_t)s_digit;
-        rank = s_rank;
-        __syncthreads();
-      }
-    }
-  } else {
-    // Fallback: byte-wide passes streaming the pages each time; passes 0-3
-    // resolve the score, 4-7 the id.  hist[] serves as 16 per-wave 256-bin
-    // histograms here.
-    const int wave = tid >> 6;
-    uint32_t pre_s = 0, pre_i = 0;
-    rank = (int)k - 1;
-    for (int pass = 0; pass < 8; ++pass) {
-      const bool id_pass = pass >= 4;
-      const int sh = 24 - 8 * (pass & 3);
-      for (int e = tid; e < 4096; e += kSelThreads) hist[e] = 0;
-      __syncthreads();
-      for (int b0 = 0; b0 < n; b0 += kSelBatch * kSelThreads) {
-        float sc[kSelBatch];
-        int8_t vv[kSelBatch];
-#pragma unroll
-        for (int j = 0; j < kSelBatch; ++j) {
-          const int i = b0 + j * kSelThreads + tid;
-          vv[j] = i < n ? valid[i] : (int8_t)0;
-          sc[j] = i < n ? scores[i] : 0.0f;
-        }
-#pragma unroll
-        for (int j = 0; j < kSelBatch; ++j) {
-          if (vv[j] != 1) continue;
-          const uint32_t ks = ordered_score(sc[j]);
-          const uint32_t id = (uint32_t)(b0 + j * kSelThreads + tid);
-          bool match;
-          uint32_t digit;
-          if (!id_pass) {
-            match = (pass == 0) || ((ks >> (sh + 8)) == pre_s);
-            digit = (ks >> sh) & 255u;
-          } else {
-            match = (ks == pre_s) && (pass == 4 || (id >> (sh + 8)) == pre_i);
-            digit = (id >> sh) & 255u;
-          }
-          if (match) atomicAdd(&hist[wave * 256 + digit], 1);
-        }
-      }
-      __syncthreads();
-      // Reduce the 16 per-wave histograms into cand_s[0..256) (unused here).
-      if (tid < 256) {
-        int sum = 0;
-#pragma unroll
-        for (int w = 0; w < kSelWaves; ++w) sum += hist[w * 256 + tid];
-        cand_s[tid] = (uint32_t)sum;
-      }
-      __syncthreads();
-      if (tid < 64) pick_digit256(reinterpret_cast<const int*>(cand_s), rank, &s_digit, &s_rank);
-      __syncthreads();
-      if (!id_pass)
-        pre_s = (pre_s << 8) | (uint32_t)s_digit;
-      else
-        pre_i = (pre_i << 8) | (uint32_t)s_digit;
-      rank = s_rank;
-      __syncthreads();
-    }
-    score = pre_s;
-    idp = pre_i;
-  }
-  if (tid == 0) {
-    out->key_thr = ((unsigned long long)score << 32) | idp;
+  sel_pick(hist, kSelBins, (int)k - 1, sm, &s_digit, &s_rank);
+  if (threadIdx.x == 0) {
+    ss->k = (int)k;
+    ss->top = (uint32_t)s_digit;
+    ss->rank = s_rank;
     out->k = (int)k;
     out->n_valid = n_valid;
   }
+}
+
+__global__ __launch_bounds__(kSelThreads) void sel_collect_kernel(const float* __restrict__ scores,
+                                                                  const int8_t* __restrict__ valid, int n,
+                                                                  SelScratch* ss, uint32_t* __restrict__ cand_s,
+                                                                  uint32_t* __restrict__ cand_i) {
+  __shared__ int sm[kSelWaves + 1];
+  __shared__ int s_base;
+  if (ss->k == 0) return;  // written by the previous launch; uniform
+  const int tid = threadIdx.x;
+  const uint32_t top = ss->top;
+  for (int64_t t0 = (int64_t)blockIdx.x * kSelTile; t0 < n; t0 += (int64_t)gridDim.x * kSelTile) {
+    uint32_t ks[kSelPer];
+    int cnt = 0, mbits = 0;
+#pragma unroll
+    for (int j = 0; j < kSelPer; ++j) {
+      const int64_t i = t0 + j * kSelThreads + tid;
+      ks[j] = 0;
+      if (i < n && valid[i] == 1) {
+        ks[j] = ordered_score(scores[i]);
+        if ((ks[j] >> 20) == top) {
+          mbits |= 1 << j;
+          ++cnt;
+        }
+      }
+    }
+    int pos = sel_block_scan(cnt, sm);
+    if (tid == 0 && sm[kSelWaves] > 0) s_base = atomicAdd(&ss->ncand, sm[kSelWaves]);
+    __syncthreads();
+    pos += s_base;
+#pragma unroll
+    for (int j = 0; j < kSelPer; ++j) {
+      if (!((mbits >> j) & 1)) continue;
+      cand_s[pos] = ks[j] & 0xFFFFFu;
+      cand_i[pos] = (uint32_t)(t0 + j * kSelThreads + tid);
+      ++pos;
+    }
+    __syncthreads();  // s_base and sm are reused by the next tile
+  }
+}
+
+__global__ __launch_bounds__(kSelThreads) void sel_resolve_kernel(const SelScratch* ss, const uint32_t* g_cand_s,
+                                                                  const uint32_t* g_cand_i, SelectOut* out) {
+  __shared__ int hist[2048];
+  __shared__ uint32_t lds_s[kSelCap];  // low 20 bits of the ordered score
+  __shared__ uint32_t lds_i[kSelCap];  // page id
+  __shared__ int sm[kSelWaves + 1];
+  __shared__ int s_digit, s_rank, s_id;
+  if (ss->k == 0) return;
+  const int tid = threadIdx.x;
+  const int nc = ss->ncand;
+  const uint32_t top = ss->top;
+  int rank = ss->rank;
+  const uint32_t* cs = g_cand_s;
+  const uint32_t* ci = g_cand_i;
+  if (nc <= kSelCap) {
+    for (int q = tid; q < nc; q += kSelThreads) {
+      lds_s[q] = g_cand_s[q];
+      lds_i[q] = g_cand_i[q];
+    }
+    cs = lds_s;
+    ci = lds_i;
+  }
+  __syncthreads();
+  auto cand_score = [&](int q) { return cs[q]; };
+  auto cand_id = [&](int q) { return ci[q]; };
+  uint32_t low = 0;
+  int ties = 0;
+  for (int pass = 0; pass < 2; ++pass) {
+    const int sh = 10 - 10 * pass;
+    for (int e = tid; e < 1024; e += kSelThreads) hist[e] = 0;
+    __syncthreads();
+    for (int q = tid; q < nc; q += kSelThreads) {
+      const uint32_t v = cand_score(q);
+      if (pass == 0 || (v >> 10) == low) atomicAdd(&hist[(v >> sh) & 1023u], 1);
+    }
+    __syncthreads();
+    sel_pick(hist, 1024, rank, sm, &s_digit, &s_rank);
+    low = (low << 10) | (uint32_t)s_digit;
+    rank = s_rank;
+    ties = hist[s_digit];
+    __syncthreads();
+  }
+  const uint32_t score = (top << 20) | low;
+  uint32_t idp = 0;
+  if (ties == 1) {
+    for (int q = tid; q < nc; q += kSelThreads)
+      if (cand_score(q) == low) s_id = (int)cand_id(q);
+    __syncthreads();
+    idp = (uint32_t)s_id;
+  } else {
+    for (int pass = 0; pass < 3; ++pass) {
+      const int width = pass < 2 ? 11 : 10;
+      const int sh = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
+      for (int e = tid; e < 2048; e += kSelThreads) hist[e] = 0;
+      __syncthreads();
+      for (int q = tid; q < nc; q += kSelThreads) {
+        if (cand_score(q) != low) continue;
+        const uint32_t id = cand_id(q);
+        if (pass == 0 || (id >> (sh + width)) == idp) atomicAdd(&hist[(id >> sh) & ((1u << width) - 1u)], 1);
+      }
+      __syncthreads();
+      sel_pick(hist, 2048, rank, sm, &s_digit, &s_rank);
+      idp = (idp << width) | (uint32_t)s_digit;
+      rank = s_rank;
+      __syncthreads();
+    }
+  }
+  if (tid == 0) out->key_thr = ((unsigned long long)score << 32) | idp;
 }
 
 // ---------------------------------------------------------------------------
@@ -753,14 +728,21 @@ struct Workspace {
   int* counts;
   int* offsets;
   int* rows;  // per-row offsets (table compaction)
+  SelScratch* ss;
+  uint32_t* cand_s;  // select candidates (n each)
+  uint32_t* cand_i;
 };
+
+constexpr size_t round256(size_t b) { return (b + 255) / 256 * 256; }
 
 size_t workspace_bytes(int n) {
   const size_t nb = (size_t)num_blocks(n);
   size_t b = 256;                                   // SelectOut + misc
-  b += (nb * sizeof(int) + 255) / 256 * 256;        // counts
-  b += (nb * sizeof(int) + 255) / 256 * 256;        // offsets
-  b += (((size_t)n + 1) * sizeof(int) + 255) / 256 * 256;  // row offsets
+  b += round256(nb * sizeof(int));                  // counts
+  b += round256(nb * sizeof(int));                  // offsets
+  b += round256(((size_t)n + 1) * sizeof(int));     // row offsets
+  b += round256(sizeof(SelScratch));                // select histogram + counters
+  b += 2 * round256((size_t)n * sizeof(uint32_t));  // select candidates
   return b;
 }
 
@@ -771,19 +753,27 @@ Workspace carve(void* ws, int n) {
   w.sel = reinterpret_cast<SelectOut*>(c);
   c += 256;
   w.counts = reinterpret_cast<int*>(c);
-  c += (nb * sizeof(int) + 255) / 256 * 256;
+  c += round256(nb * sizeof(int));
   w.offsets = reinterpret_cast<int*>(c);
-  c += (nb * sizeof(int) + 255) / 256 * 256;
+  c += round256(nb * sizeof(int));
   w.rows = reinterpret_cast<int*>(c);
+  c += round256(((size_t)n + 1) * sizeof(int));
+  w.ss = reinterpret_cast<SelScratch*>(c);
+  c += round256(sizeof(SelScratch));
+  w.cand_s = reinterpret_cast<uint32_t*>(c);
+  c += round256((size_t)n * sizeof(uint32_t));
+  w.cand_i = reinterpret_cast<uint32_t*>(c);
   return w;
 }
 
 // Ordered compaction of page ids satisfying `a` into out[], count to *count.
-int ordered_compact(const PredArgs& a, int n, int32_t* out, int32_t* count, Workspace& w, hipStream_t s) {
+int ordered_compact(const PredArgs& a, int n, int32_t* out, int32_t* count, Workspace& w, hipStream_t s,
+                    int8_t* clear_valid = nullptr, int8_t* clear_alloc = nullptr) {
   const int nb = num_blocks(n);
   hipLaunchKernelGGL(compact_count_kernel, dim3(nb), dim3(kThreads), 0, s, a, n, w.counts);
   hipLaunchKernelGGL(scan_counts_kernel, dim3(1), dim3(kThreads), 0, s, w.counts, nb, w.offsets, count);
-  hipLaunchKernelGGL(compact_write_kernel, dim3(nb), dim3(kThreads), 0, s, a, n, w.offsets, out);
+  hipLaunchKernelGGL(compact_write_kernel, dim3(nb), dim3(kThreads), 0, s, a, n, w.offsets, out, clear_valid,
+                     clear_alloc);
   return check_launch("ordered compaction");
 }
 
@@ -868,11 +858,7 @@ extern "C" int kessie_page_evict_list(int8_t* page_valid, const int32_t* page_po
   hipStream_t s = as_stream(stream);
   Workspace w = carve(workspace, num_pages);
   PredArgs a{kPredFreed, page_valid, page_positions, allocated, evict_before_pos, nullptr, nullptr, nullptr};
-  st = ordered_compact(a, num_pages, freed_list, freed_count, w, s);
-  if (st) return st;
-  hipLaunchKernelGGL(mark_evicted_kernel, dim3(max(1, min(1024, div_up(num_pages, kThreads)))), dim3(kThreads), 0,
-                     s, freed_list, freed_count, page_valid, allocated, num_pages);
-  return check_launch("page evict (mark)");
+  return ordered_compact(a, num_pages, freed_list, freed_count, w, s, page_valid, allocated);
 }
 
 extern "C" int kessie_page_select_evict(const float* scores, int8_t* page_valid, int num_pages, int k_evict,
@@ -887,16 +873,17 @@ extern "C" int kessie_page_select_evict(const float* scores, int8_t* page_valid,
   if (st) return st;
   hipStream_t s = as_stream(stream);
   Workspace w = carve(workspace, num_pages);
-  hipLaunchKernelGGL(radix_select_kernel, dim3(1), dim3(kSelThreads), 0, s, scores, page_valid, num_pages, k_evict,
-                     evict_fraction, w.sel);
+  const int sg = max(1, min(kSelMaxGrid, div_up(num_pages, kSelTile)));
+  hipLaunchKernelGGL(sel_clear_kernel, dim3(1), dim3(kThreads), 0, s, w.ss);
+  hipLaunchKernelGGL(sel_hist_kernel, dim3(sg), dim3(kSelThreads), 0, s, scores, page_valid, num_pages, w.ss);
+  hipLaunchKernelGGL(sel_bucket_kernel, dim3(1), dim3(kSelThreads), 0, s, w.ss, k_evict, evict_fraction, w.sel);
+  hipLaunchKernelGGL(sel_collect_kernel, dim3(sg), dim3(kSelThreads), 0, s, scores, page_valid, num_pages, w.ss,
+                     w.cand_s, w.cand_i);
+  hipLaunchKernelGGL(sel_resolve_kernel, dim3(1), dim3(kSelThreads), 0, s, w.ss, w.cand_s, w.cand_i, w.sel);
   st = check_launch("select evict (radix select)");
   if (st) return st;
   PredArgs a{kPredScoreEvict, page_valid, nullptr, nullptr, 0, scores, &w.sel->key_thr, &w.sel->k};
-  st = ordered_compact(a, num_pages, evict_list, evict_count, w, s);
-  if (st) return st;
-  hipLaunchKernelGGL(mark_evicted_kernel, dim3(max(1, min(1024, div_up(num_pages, kThreads)))), dim3(kThreads), 0,
-                     s, evict_list, evict_count, page_valid, static_cast<int8_t*>(nullptr), num_pages);
-  return check_launch("select evict (mark)");
+  return ordered_compact(a, num_pages, evict_list, evict_count, w, s, page_valid);
 }
 
 extern "C" int kessie_page_compact(const int32_t* tables, const int32_t* lens, const int8_t* page_valid,
