@@ -193,6 +193,28 @@ int kessie_fog_prefill_paged(
     int causal, int dtype, void* workspace, size_t workspace_bytes,
     void* stream);
 
+/* The same chunked prefill for a batch whose sequences have different chunk
+ * lengths, in one launch (the prefill half of a mixed serving batch, which
+ * KeSSieAttentionImpl.forward, kessie_attention.py:278-304, hands to one
+ * attention call): sequence b's queries are rows query_start_loc[b] -
+ * query_start_loc[0] .. query_start_loc[b+1] - query_start_loc[0] - 1 of
+ * q/out ([T][Hq][D] contiguous; query_start_loc int32 [batch+1],
+ * non-decreasing, on the device, e.g. a slice of vLLM's), chunk length C_b = query_start_loc[b+1] -
+ * query_start_loc[b] <= max_query_len, query i of it at ctx_lens[b] - C_b + i.
+ * MFMA shapes only (bf16/fp16, head_dim 128, 16-token pages, GQA 1/2/4/8,
+ * 16-byte aligned rows); other shapes return KESSIE_ERR_UNSUPPORTED without
+ * launching (call kessie_fog_prefill_paged per sequence instead).  No
+ * workspace. */
+int kessie_fog_prefill_varlen(
+    const void* q, const int32_t* query_start_loc, int max_query_len,
+    const void* kv_pool, int num_pages, int64_t page_stride, int64_t tok_stride,
+    int64_t kv_stride, int64_t head_stride, const int32_t* page_table,
+    int64_t table_stride, const int32_t* ctx_lens, const float* fog_vscale,
+    int64_t fog_vscale_bstride, const float* fog_bias, int64_t fog_bias_bstride,
+    void* out, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+    int page_size, int max_ctx, int window, float sm_scale, int causal,
+    int dtype, void* stream);
+
 /* =========================================================================
  * RoPE position remap
  * ========================================================================= */

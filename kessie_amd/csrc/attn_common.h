@@ -36,6 +36,10 @@ struct Params {
   const float* bias;
   int64_t bias_bs;
   int B, C, Hq, Hkv, G, D;
+  // Variable-length prefill (nullptr: every sequence has C queries at
+  // q + b*q_bs): sequence b's queries are tokens q_start[b] - q_start[0] ..
+  // q_start[b+1] - q_start[0] - 1 of q (and of out), C the longest of them.
+  const int32_t* q_start;
   int window, causal;
   float sm_scale;
   int num_splits;

@@ -917,6 +917,67 @@ extern "C" int kessie_fog_prefill_paged(const void* q, const void* kv_pool, int 
   return run_generic(dtype, p, as_stream(stream));
 }
 
+extern "C" int kessie_fog_prefill_varlen(const void* q, const int32_t* query_start_loc, int max_query_len,
+                                         const void* kv_pool, int num_pages, int64_t page_stride, int64_t tok_stride,
+                                         int64_t kv_stride, int64_t head_stride, const int32_t* page_table,
+                                         int64_t table_stride, const int32_t* ctx_lens, const float* fog_vscale,
+                                         int64_t fog_vscale_bstride, const float* fog_bias, int64_t fog_bias_bstride,
+                                         void* out, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                                         int page_size, int max_ctx, int window, float sm_scale, int causal,
+                                         int dtype, void* stream) {
+  using namespace kessie;
+  using namespace kessie::attn;
+  clear_error();
+  Params p{};
+  const int es = dtype_size(dtype);
+  p.q = q;
+  p.q_is = (int64_t)num_q_heads * head_dim;
+  p.q_hs = head_dim;
+  p.out = out;
+  p.o_is = p.q_is;
+  p.o_hs = head_dim;
+  p.k = kv_pool;
+  p.v = kv_pool ? static_cast<const char*>(kv_pool) + kv_stride * es : nullptr;
+  p.num_pages = num_pages;
+  p.page_stride = page_stride;
+  p.tok_stride = tok_stride;
+  p.head_stride = head_stride;
+  p.page_size = page_size;
+  p.page_table = page_table;
+  p.table_stride = table_stride;
+  p.ctx_lens = ctx_lens;
+  p.ctx_const = max_ctx;
+  p.max_ctx = max_ctx;
+  p.vscale = fog_vscale;
+  p.vs_bs = fog_vscale_bstride;
+  p.bias = fog_bias;
+  p.bias_bs = fog_bias_bstride;
+  p.B = batch;
+  p.C = max_query_len;
+  p.q_start = query_start_loc;
+  p.Hq = num_q_heads;
+  p.Hkv = num_kv_heads;
+  p.G = num_kv_heads > 0 ? num_q_heads / num_kv_heads : 0;
+  p.D = head_dim;
+  p.window = window;
+  p.causal = causal ? 1 : 0;
+  p.sm_scale = sm_scale;
+  int st = validate_common(p, dtype);
+  if (st != KESSIE_OK) return st;
+  KESSIE_REQUIRE(max_query_len >= 0, KESSIE_ERR_INVALID, "fog prefill varlen: max_query_len %d", max_query_len);
+  KESSIE_REQUIRE(page_table != nullptr && ctx_lens != nullptr && query_start_loc != nullptr, KESSIE_ERR_INVALID,
+                 "fog prefill varlen: page_table, ctx_lens and query_start_loc are required");
+  KESSIE_REQUIRE(kv_stride >= 0, KESSIE_ERR_INVALID, "fog prefill varlen: kv_stride %lld", (long long)kv_stride);
+  if (batch == 0 || max_query_len == 0) return KESSIE_OK;
+  KESSIE_REQUIRE(prefill_mfma_ok(p, dtype), KESSIE_ERR_UNSUPPORTED,
+                 "fog prefill varlen: shape not taken by the MFMA kernel (bf16/fp16, head_dim 128, 16-token pages, "
+                 "GQA 1/2/4/8, 16-byte aligned rows)");
+  p.num_splits = 1;
+  p.direct_out = 1;
+  p.launch_combine = 0;
+  return prefill_mfma(p, dtype, as_stream(stream));
+}
+
 // Reference launchers (kessie_kernels_v2.hip:716-751, 788-825): dense fp16
 // [B,H,N,D], no GQA, every position a query.  One split, so no workspace.
 static void dense_fp16(const void* Q, const void* K, const void* V, void* O, const void* fog, float sm_scale,

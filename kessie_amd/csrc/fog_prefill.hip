@@ -95,12 +95,20 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
   const int qtile = blockIdx.x / p.Hkv;
   const int b = blockIdx.y;
   const int ctx = seq_ctx(p, b);
+  int C = p.C;  // this sequence's queries, and where they start (uniform)
+  int64_t q_off = (int64_t)b * p.q_bs, o_off = (int64_t)b * p.o_bs;
+  if (p.q_start) {
+    const int s0 = p.q_start[b] - p.q_start[0];
+    C = p.q_start[b + 1] - p.q_start[b];
+    q_off = (int64_t)s0 * p.q_is;
+    o_off = (int64_t)s0 * p.o_is;
+  }
 
   // Rows of the workgroup and the key range they see (uniform).
   const int qi_first = qtile * kPos;
-  const int qi_last = min(p.C, qi_first + kPos) - 1;
-  const int qmin = max(ctx - p.C + qi_first, 0);
-  const int qmax = ctx - p.C + qi_last;
+  const int qi_last = min(C, qi_first + kPos) - 1;
+  const int qmin = max(ctx - C + qi_first, 0);
+  const int qmax = ctx - C + qi_last;
   if (qi_last < qi_first || qmax < 0) return;
   int lo = 0, hi = 0;
   key_range(p, ctx, qmin, qmax, &lo, &hi);
@@ -112,13 +120,13 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
   const int frow = wave * 32 + col;
   const int qi = qi_first + frow / G;
   const int head = g * G + frow % G;
-  const int q_pos = ctx - p.C + qi;
+  const int q_pos = ctx - C + qi;
   const bool row_ok = qi <= qi_last && q_pos >= 0;
 
   // B operand of S^T = K Q^T: d-step s holds d = 16s + 8*half .. +8.
   v8 qv[8];
   {
-    const T* qr = static_cast<const T*>(p.q) + (int64_t)b * p.q_bs + (int64_t)min(qi, qi_last) * p.q_is +
+    const T* qr = static_cast<const T*>(p.q) + q_off + (int64_t)min(qi, qi_last) * p.q_is +
                   (int64_t)head * p.q_hs;
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
@@ -335,7 +343,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
   const float l = l_half + __shfl_xor(l_half, 32);
   if (!row_ok) return;
   const float il = l > 0.0f ? 1.0f / l : 0.0f;
-  T* orow = static_cast<T*>(p.out) + (int64_t)b * p.o_bs + (int64_t)qi * p.o_is + (int64_t)head * p.o_hs;
+  T* orow = static_cast<T*>(p.out) + o_off + (int64_t)qi * p.o_is + (int64_t)head * p.o_hs;
 #pragma unroll
   for (int db = 0; db < 4; ++db)
 #pragma unroll

@@ -455,6 +455,18 @@ class KeSSieAttentionImpl:
                                        lens.index_select(0, idx), kv_len, fog_bias=bias, window=self.window,
                                        sm_scale=self.scale, layout=layout)
                 out.index_copy_(0, rows, o_dec)
+        if len(prefill) > 1 and prefill == list(range(prefill[0], prefill[-1] + 1)):
+            # One launch for the whole run of prefill sequences (their chunk
+            # lengths differ): query_start_loc's slice locates each one.
+            lo, hi = prefill[0], prefill[-1] + 1
+            s0, s1 = qsl[lo], qsl[hi]
+            qs = meta.query_start_loc[lo:hi + 1]
+            if qs.dtype != torch.int32:
+                qs = qs.to(torch.int32)
+            if ops.fog_prefill_varlen(q[s0:s1], qs, max(qsl[i + 1] - qsl[i] for i in prefill), kv_cache,
+                                      table[lo:hi], lens[lo:hi], kv_len, fog_bias=bias, window=self.window,
+                                      causal=True, sm_scale=self.scale, layout=layout, out=out[s0:s1]):
+                prefill = []
         for i in prefill:
             s, e = qsl[i], qsl[i + 1]
             ops.fog_prefill(q[s:e].unsqueeze(0), kv_cache, table[i:i + 1], lens[i:i + 1], kv_len, fog_bias=bias,

@@ -279,6 +279,51 @@ def fog_prefill(q: torch.Tensor, pool: torch.Tensor, page_table: torch.Tensor, c
     return out
 
 
+def fog_prefill_varlen(q: torch.Tensor, query_start_loc: torch.Tensor, max_query_len: int, pool: torch.Tensor,
+                       page_table: torch.Tensor, ctx_lens: torch.Tensor, max_ctx: int,
+                       fog_vscale: Optional[torch.Tensor] = None, fog_bias: Optional[torch.Tensor] = None,
+                       window: int = 0, causal: bool = True, sm_scale: Optional[float] = None,
+                       layout: str = "native", out: Optional[torch.Tensor] = None, stream=None) -> bool:
+    """Chunked prefill of B sequences with different chunk lengths in one
+    launch: q/out [T, Hq, D] packed, sequence b's queries at rows
+    query_start_loc[b] - query_start_loc[0] .. (int32 [B+1] on the device, e.g.
+    a slice of vLLM's query_start_loc), query i of it at ctx_lens[b] - C_b + i.
+    Returns False, having launched nothing, for shapes the MFMA kernel does not
+    take (the caller then runs fog_prefill per sequence)."""
+    pv = pool_view(pool, layout)
+    q = _contig(q, "q")
+    t, hq, d = q.shape
+    b = ctx_lens.numel()
+    if d != pv.head_dim or q.dtype != pool.dtype:
+        raise ValueError("q and pool disagree on head_dim or dtype")
+    if page_table.dtype != torch.int32 or ctx_lens.dtype != torch.int32 or query_start_loc.dtype != torch.int32:
+        raise TypeError("page_table, ctx_lens and query_start_loc must be int32")
+    if query_start_loc.numel() != b + 1 or query_start_loc.stride(0) != 1:
+        raise ValueError("query_start_loc must hold B+1 contiguous entries")
+    if page_table.dim() != 2 or page_table.shape[0] != b or page_table.stride(1) != 1:
+        raise ValueError("page_table must be [B, W] with contiguous rows")
+    if max_ctx > page_table.shape[1] * pv.page_size:
+        raise ValueError(f"max_ctx={max_ctx} exceeds the page table's {page_table.shape[1]} pages")
+    if out is None:
+        out = torch.empty_like(q)
+    if out.shape != q.shape or out.dtype != q.dtype or not out.is_contiguous():
+        raise ValueError("out must be a contiguous [T, Hq, D] tensor of q's dtype")
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(d)
+    vs, vs_bs = _fog_arg(fog_vscale, b, "fog_vscale", max_ctx)
+    bi, bi_bs = _fog_arg(fog_bias, b, "fog_bias", max_ctx)
+    lib = _lib.load()
+    st = lib.kessie_fog_prefill_varlen(
+        _ptr(q), _ptr(query_start_loc), int(max_query_len), C.c_void_p(pv.k_ptr), pv.num_pages, pv.page_stride,
+        pv.tok_stride, pv.kv_stride, pv.head_stride, _ptr(page_table), page_table.stride(0), _ptr(ctx_lens),
+        _ptr(vs), vs_bs, _ptr(bi), bi_bs, _ptr(out), b, hq, pv.num_kv_heads, d, pv.page_size, int(max_ctx),
+        int(window), float(sm_scale), 1 if causal else 0, dtype_code(q.dtype), _stream_ptr(stream, q.device))
+    if st == _lib.ERR_UNSUPPORTED:
+        return False
+    _lib.check("kessie_fog_prefill_varlen", st)
+    return True
+
+
 # ---------------------------------------------------------------------------
 # RoPE remap
 # ---------------------------------------------------------------------------

@@ -135,3 +135,57 @@ def test_prefill_1m_context_sampled(dev):
     rows = torch.tensor([0, 1, 777, 1500, 2046, 2047])
     ref = paged_prefill_blockwise(q.cpu(), pool, table.cpu(), lens.cpu(), rows, fog.cpu(), block_pages=4096)
     _check(out[:, rows], ref, torch.bfloat16)
+
+
+@pytest.mark.parametrize("fog", ["vscale", "bias", "none"])
+@pytest.mark.parametrize("window", [0, 50])
+def test_prefill_varlen_matches_per_sequence(dev, fog, window):
+    """One varlen launch over sequences with different chunk lengths (incl. a
+    one-token chunk and an empty one) equals the per-sequence launches bit for
+    bit, and the oracle within tolerance; the query_start_loc slice may start
+    at a non-zero offset."""
+    from kessie_amd import ops
+
+    chunks, ctxs = [37, 1, 300, 0, 129], [900, 64, 300, 50, 4000]
+    b, hq, hkv, d = len(chunks), 32, 8, 128
+    _, pool, table, lens = _case(dev, b, 1, ctxs, hq, hkv, torch.bfloat16, seed=11)
+    starts = [5]
+    for c in chunks:
+        starts.append(starts[-1] + c)
+    qsl = torch.tensor(starts, dtype=torch.int32, device=dev)
+    q_all = torch.randn(starts[-1], hq, d, generator=gen(dev, 12), device=dev).to(torch.bfloat16)
+    q = q_all[5:]
+    mx = max(ctxs)
+    vs = bias = None
+    if fog == "vscale":
+        vs = torch.rand(b, mx, generator=gen(dev, 13), device=dev)
+    elif fog == "bias":
+        bias = fog_bias(mx, 0.5, 0.5, {3, 17, 200}, 0.1).to(dev)
+    out = torch.full_like(q, float("nan"))
+    assert ops.fog_prefill_varlen(q, qsl, max(chunks), pool, table, lens, mx, fog_vscale=vs, fog_bias=bias,
+                                  window=window, out=out)
+    torch.cuda.synchronize()
+    for i, c in enumerate(chunks):
+        if c == 0:
+            continue
+        s = starts[i] - 5
+        one = ops.fog_prefill(q[s:s + c].unsqueeze(0).contiguous(), pool, table[i:i + 1], lens[i:i + 1], mx,
+                              fog_vscale=None if vs is None else vs[i:i + 1], fog_bias=bias, window=window)
+        torch.cuda.synchronize()
+        assert torch.equal(out[s:s + c], one[0]), f"sequence {i}"
+        ref = paged_prefill_ref(q[s:s + c].unsqueeze(0).cpu(), pool.cpu(), table[i:i + 1].cpu(),
+                                lens[i:i + 1].cpu(), None if vs is None else vs[i].cpu(),
+                                None if bias is None else bias.cpu(), window)
+        _check(one, ref, torch.bfloat16)
+
+
+def test_prefill_varlen_unsupported_shape_launches_nothing(dev):
+    from kessie_amd import ops
+
+    _, pool, table, lens = _case(dev, 2, 1, [40, 40], 32, 8, torch.float32, seed=14)
+    qsl = torch.tensor([0, 3, 8], dtype=torch.int32, device=dev)
+    q = torch.randn(8, 32, 128, device=dev)
+    out = torch.full_like(q, 7.0)
+    assert not ops.fog_prefill_varlen(q, qsl, 5, pool, table, lens, 40, out=out)
+    torch.cuda.synchronize()
+    assert torch.all(out == 7.0)
