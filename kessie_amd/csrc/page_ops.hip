@@ -516,18 +516,28 @@ __global__ __launch_bounds__(kThreads) void threshold_evict_kernel(int8_t* valid
 // page slot, one non-temporal 16-byte load and store per lane: a 64 KiB page is
 // spread over 16 workgroups.  (Measured on 49,152 random 64 KiB pages: 0.99 ms
 // against 1.17-1.21 ms for one workgroup per page at 1-8 chunks per lane.)
+// The grid covers the slot capacity n while only *count_dev slots are live;
+// slots are taken from kGatherRegions interleaved regions of [0, n), so the
+// workgroups of dead slots (the tail of the capacity) are spread through the
+// dispatch order instead of forming a tail of their own (49,152 live of 65,536:
+// 1.03 ms against 1.07 ms; all live: within 0.5 %).
 // ---------------------------------------------------------------------------
 constexpr int kGatherThreads = 256;
+constexpr int kGatherRegions = 32;
 
 __global__ __launch_bounds__(kGatherThreads) void gather_kernel(const u32x4* __restrict__ src, int64_t page_vecs,
-                                                                int tiles_per_page, const int32_t* __restrict__ idx,
+                                                                int tiles_per_page, int per_region,
+                                                                const int32_t* __restrict__ idx,
                                                                 const int32_t* __restrict__ count_dev, int n,
                                                                 int num_pages, u32x4* __restrict__ dst) {
-  const int cnt = count_dev ? min(n, *count_dev) : n;
-  const int i = blockIdx.x / tiles_per_page;
-  if (i >= cnt) return;
+  const int j = blockIdx.x / tiles_per_page;
+  const int i = (j % kGatherRegions) * per_region + j / kGatherRegions;  // slot
+  if (i >= n) return;
+  // The slot's page id and the device count are independent loads, issued
+  // together: the data load then waits for one round trip, not two.
   const int pid = idx[i];
-  if (pid < 0 || pid >= num_pages) return;
+  const int cnt = count_dev ? min(n, *count_dev) : n;
+  if (i >= cnt || pid < 0 || pid >= num_pages) return;
   const int64_t v = (int64_t)(blockIdx.x % tiles_per_page) * kGatherThreads + threadIdx.x;
   if (v < page_vecs)
     __builtin_nontemporal_store(__builtin_nontemporal_load(src + (int64_t)pid * page_vecs + v),
@@ -934,12 +944,14 @@ extern "C" int kessie_page_gather(const void* src_pool, int64_t page_bytes, cons
                  "page gather: page_bytes and pointers must be 16-byte multiples/aligned");
   const int64_t page_vecs = page_bytes / 16;
   const int64_t tiles = div_up(page_vecs, (int64_t)kGatherThreads);
-  KESSIE_REQUIRE(tiles * n < (1LL << 31), KESSIE_ERR_UNSUPPORTED, "page gather: %d pages of %lld bytes is too large",
-                 n, (long long)page_bytes);
+  const int per_region = div_up(n, kGatherRegions);
+  const int64_t grid = tiles * per_region * kGatherRegions;
+  KESSIE_REQUIRE(grid < (1LL << 31), KESSIE_ERR_UNSUPPORTED, "page gather: %d pages of %lld bytes is too large", n,
+                 (long long)page_bytes);
   const u32x4* s = static_cast<const u32x4*>(src_pool);
   u32x4* d = static_cast<u32x4*>(dst);
-  hipLaunchKernelGGL(gather_kernel, dim3((unsigned)(tiles * n)), dim3(kGatherThreads), 0, as_stream(stream), s,
-                     page_vecs, (int)tiles, idx, count_dev, n, num_pages, d);
+  hipLaunchKernelGGL(gather_kernel, dim3((unsigned)grid), dim3(kGatherThreads), 0, as_stream(stream), s, page_vecs,
+                     (int)tiles, per_region, idx, count_dev, n, num_pages, d);
   return check_launch("page gather");
 }
 
