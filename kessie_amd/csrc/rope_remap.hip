@@ -22,7 +22,7 @@ namespace kessie {
 namespace {
 
 constexpr int kRemapThreads = 256;
-constexpr int kRemapTile = 16;    // tokens per workgroup
+constexpr int kRemapTile = 4;     // tokens per workgroup (8 KiB of K at 8 heads x 128 bf16)
 constexpr int kVecMaxHalf = 128;  // vectorised kernel: head_dim <= 256
 
 // Byte-free addressing helper: element offset of token t's K row, or -1 when
@@ -63,7 +63,11 @@ struct Vec16<float> {
 // rows and head starts.  The K chunks of a round are loaded into registers
 // before the cos/sin phase, so HBM latency overlaps the trigonometry; the
 // workgroup barrier that publishes cos/sin keeps those loads ahead of it.
-constexpr int kRemapItems = 4;  // chunk pairs per thread per round
+// One chunk pair (two 16-byte loads) per thread per round: the read-modify-
+// write pattern is fastest with many small workgroups (measured, 65,536 bf16
+// tokens: 4 tokens per workgroup 56.6 us; 8: 58.3; 16 tokens with 4 pairs per
+// thread: 61.3; 2: 58.7).
+constexpr int kRemapItems = 1;  // chunk pairs per thread per round
 
 // kHalf / kHeads / kPage > 0 fix head_dim/2, the head count and the page size
 // at compile time (the index arithmetic then has no runtime divisions); 0
