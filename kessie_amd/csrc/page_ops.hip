@@ -547,7 +547,6 @@ __global__ __launch_bounds__(kGatherThreads) void gather_kernel(const u32x4* __r
 // ---------------------------------------------------------------------------
 // Insert (optionally remapping K)
 // ---------------------------------------------------------------------------
-constexpr int kInsTile = 8;  // tokens per workgroup
 constexpr int kInsMaxHalf = 128;
 
 template <typename T>
@@ -628,103 +627,108 @@ __global__ __launch_bounds__(kThreads) void insert_scalar_kernel(InsertArgs a) {
   }
 }
 
-// Vectorised insert: 16-byte chunks, one (token, head, chunk pair) per item.
-// Each thread issues the non-temporal loads of its first kInsEarly items before
-// the tile's cos/sin are evaluated into LDS, so the trigonometry runs under the
-// load latency; items past kInsEarly x kThreads (large H x D) load as they go.
-// (Measured, 65,536 bf16 tokens, 8 heads x 128, remap on: 105 us against 112 us
-// for 16-token tiles with plain loads/stores issued after the cos/sin phase.)
-constexpr int kInsEarly = 2;
-
-template <typename T>
+// Vectorised insert: one token per workgroup.  Its H x half/N K chunk pairs
+// (two 16-byte loads, rotated when remapping) and its H x D/N V chunks (one
+// load) are separate items, one per lane (looping past 256 for large H x D);
+// each lane issues its first item's non-temporal loads before the token's
+// cos/sin are evaluated into LDS, so the trigonometry hides under the load
+// latency.  (Measured, 65,536 bf16 tokens, 8 heads x 128, remap on: 93 us --
+// the rate of a plain scatter of the same bytes into random pages -- against
+// 103-106 us for 4-16-token workgroups with K and V pairs in one item.)
+// kH / kChunks / kPage > 0 fix the head count, the chunk pairs per head and
+// the page size at compile time (no runtime divisions in the index math, which
+// with one item per lane would cost more than the copy); 0 reads them from the
+// arguments.
+template <typename T, int kH, int kChunks, int kPage>
 __global__ __launch_bounds__(kThreads) void insert_vec_kernel(InsertArgs a) {
 #pragma clang fp contract(off)
   typedef typename Vec16<T>::type V;
   constexpr int N = Vec16<T>::N;
-  __shared__ float2 cs[kInsTile * kInsMaxHalf];
-  const int half = a.D / 2;
+  __shared__ float2 cs[kInsMaxHalf];
+  const int H = kH > 0 ? kH : a.H;
+  const int chunks = kChunks > 0 ? kChunks : a.D / 2 / N;  // chunk pairs per head
+  const int page_size = kPage > 0 ? kPage : a.page_size;
+  const int half = chunks * N;
+  const int D = 2 * half;
   const bool remap = a.inv_freq != nullptr;
-  const int t0 = blockIdx.x * kInsTile;
-  const int ntok = min(kInsTile, a.T - t0);
+  const int t = blockIdx.x;
+  const int kp = H * chunks;              // K pair items
+  const int items = kp + 2 * kp;          // + V chunk items (H x D/N)
+  const int nthr = blockDim.x;
+  const int phys = a.target_pages[t / page_size];
+  const bool ok = phys >= 0 && phys < a.num_pages;  // uniform
   T* pool = static_cast<T*>(a.pool);
   const T* nk = static_cast<const T*>(a.new_k);
   const T* nv = static_cast<const T*>(a.new_v);
-  const int chunks = half / N;             // chunk pairs per head
-  const int per_tok = a.H * chunks;
-  const int total = ntok * per_tok;
+  const int64_t dst_row = (int64_t)phys * a.page_stride + (int64_t)(t % page_size) * a.tok_stride;
 
-  auto load = [&](int i, V& k1, V& k2, V& v1, V& v2) {
-    const int tt = i / per_tok;
-    const int r = i - tt * per_tok;
-    const int h = r / chunks, c = r - h * chunks;
-    const int64_t src = ((int64_t)(t0 + tt) * a.H + h) * a.D + c * N;
-    k1 = __builtin_nontemporal_load(reinterpret_cast<const V*>(nk + src));
-    k2 = __builtin_nontemporal_load(reinterpret_cast<const V*>(nk + src + half));
-    v1 = __builtin_nontemporal_load(reinterpret_cast<const V*>(nv + src));
-    v2 = __builtin_nontemporal_load(reinterpret_cast<const V*>(nv + src + half));
+  auto load = [&](int i, V& x1, V& x2) {
+    if (i < kp) {
+      const int h = i / chunks, c = i - h * chunks;
+      const int64_t src = ((int64_t)t * H + h) * D + c * N;
+      x1 = __builtin_nontemporal_load(reinterpret_cast<const V*>(nk + src));
+      x2 = __builtin_nontemporal_load(reinterpret_cast<const V*>(nk + src + half));
+    } else {
+      const int q = i - kp;
+      const int h = q / (2 * chunks), c = q - h * 2 * chunks;
+      x1 = __builtin_nontemporal_load(reinterpret_cast<const V*>(nv + ((int64_t)t * H + h) * D + c * N));
+    }
   };
-  auto store = [&](int i, const V& k1, const V& k2, const V& v1, const V& v2) {
-    const int tt = i / per_tok;
-    const int r = i - tt * per_tok;
-    const int h = r / chunks, c = r - h * chunks;
-    const int t = t0 + tt;
-    const int phys = a.target_pages[t / a.page_size];
-    if (phys < 0 || phys >= a.num_pages) return;
-    const int64_t dst = (int64_t)phys * a.page_stride + (int64_t)(t % a.page_size) * a.tok_stride +
-                        (int64_t)h * a.head_stride + c * N;
-    V y1 = k1, y2 = k2;
-    if (remap) {
-      const float2* csr = cs + tt * half + c * N;
+  auto store = [&](int i, const V& x1, const V& x2) {
+    if (i < kp) {
+      const int h = i / chunks, c = i - h * chunks;
+      V y1 = x1, y2 = x2;
+      if (remap) {
+        const float2* csr = cs + c * N;
 #pragma unroll
-      for (int e = 0; e < N; ++e) {
-        const float2 q = csr[e];
-        const float x1 = to_f32(k1[e]);
-        const float x2 = to_f32(k2[e]);
-        const float u1 = x1 * q.x;
-        const float u2 = x2 * q.y;
-        const float w1 = x1 * q.y;
-        const float w2 = x2 * q.x;
-        y1[e] = from_f32<T>(u1 - u2);
-        y2[e] = from_f32<T>(w1 + w2);
+        for (int e = 0; e < N; ++e) {
+          const float2 q = csr[e];
+          const float v1 = to_f32(x1[e]);
+          const float v2 = to_f32(x2[e]);
+          const float u1 = v1 * q.x;
+          const float u2 = v2 * q.y;
+          const float w1 = v1 * q.y;
+          const float w2 = v2 * q.x;
+          y1[e] = from_f32<T>(u1 - u2);
+          y2[e] = from_f32<T>(w1 + w2);
+        }
       }
-    }
-    __builtin_nontemporal_store(y1, reinterpret_cast<V*>(pool + dst));
-    __builtin_nontemporal_store(y2, reinterpret_cast<V*>(pool + dst + half));
-    __builtin_nontemporal_store(v1, reinterpret_cast<V*>(pool + dst + a.kv_stride));
-    __builtin_nontemporal_store(v2, reinterpret_cast<V*>(pool + dst + a.kv_stride + half));
-    if (t % a.page_size == 0 && h == 0 && c == 0) {
-      a.valid[phys] = 1;
-      a.positions[phys] = a.conv_pos + t;
+      T* d = pool + dst_row + (int64_t)h * a.head_stride + c * N;
+      __builtin_nontemporal_store(y1, reinterpret_cast<V*>(d));
+      __builtin_nontemporal_store(y2, reinterpret_cast<V*>(d + half));
+    } else {
+      const int q = i - kp;
+      const int h = q / (2 * chunks), c = q - h * 2 * chunks;
+      T* d = pool + dst_row + a.kv_stride + (int64_t)h * a.head_stride + c * N;
+      __builtin_nontemporal_store(x1, reinterpret_cast<V*>(d));
     }
   };
 
-  V k1[kInsEarly], k2[kInsEarly], v1[kInsEarly], v2[kInsEarly];
-#pragma unroll
-  for (int u = 0; u < kInsEarly; ++u) {
-    const int i = threadIdx.x + u * kThreads;
-    if (i < total) load(i, k1[u], k2[u], v1[u], v2[u]);
-  }
+  // The staging rows are always in bounds: load them without waiting for the
+  // page id (a load that waited on it would add a round trip per token).
+  V x1, x2;
+  const int i0 = threadIdx.x;
+  if (i0 < items) load(i0, x1, x2);
   if (remap) {
-    for (int i = threadIdx.x; i < ntok * half; i += kThreads) {
-      const int tt = i / half, j = i - tt * half;
-      const int t = t0 + tt;
-      const float delta = (float)(a.tgt_pos[t] - a.orig_pos[t]);
+    const float delta = (float)(a.tgt_pos[t] - a.orig_pos[t]);
+    for (int j = threadIdx.x; j < half; j += nthr) {
       const float ang = delta * a.inv_freq[j];
-      float s, c;
-      sincosf(ang, &s, &c);
-      cs[i] = make_float2(c, s);
+      float sn, cn;
+      sincosf(ang, &sn, &cn);
+      cs[j] = make_float2(cn, sn);
     }
     __syncthreads();
   }
-#pragma unroll
-  for (int u = 0; u < kInsEarly; ++u) {
-    const int i = threadIdx.x + u * kThreads;
-    if (i < total) store(i, k1[u], k2[u], v1[u], v2[u]);
+  if (!ok) return;
+  if (i0 < items) store(i0, x1, x2);
+  for (int i = i0 + nthr; i < items; i += nthr) {
+    V y1, y2;
+    load(i, y1, y2);
+    store(i, y1, y2);
   }
-  for (int i = threadIdx.x + kInsEarly * kThreads; i < total; i += kThreads) {
-    V x1, x2, y1, y2;
-    load(i, x1, x2, y1, y2);
-    store(i, x1, x2, y1, y2);
+  if (threadIdx.x == 0 && t % page_size == 0) {
+    a.valid[phys] = 1;
+    a.positions[phys] = a.conv_pos + t;
   }
 }
 
@@ -803,7 +807,11 @@ int launch_insert(InsertArgs& a, hipStream_t s) {
                       aligned16(a.new_k) && aligned16(a.new_v) && a.page_stride % N == 0 &&
                       a.tok_stride % N == 0 && a.head_stride % N == 0 && a.kv_stride % N == 0;
   if (vec_ok) {
-    hipLaunchKernelGGL(insert_vec_kernel<T>, dim3(div_up(a.T, kInsTile)), dim3(kThreads), 0, s, a);
+    const int chunks = half / N;
+    if (a.H == 8 && chunks == 8 && a.page_size == 16)  // 8 kv heads x 128, 16-token pages
+      hipLaunchKernelGGL((insert_vec_kernel<T, 8, 8, 16>), dim3(a.T), dim3(3 * 8 * 8), 0, s, a);
+    else
+      hipLaunchKernelGGL((insert_vec_kernel<T, 0, 0, 0>), dim3(a.T), dim3(kThreads), 0, s, a);
   } else {
     const int64_t total = (int64_t)a.T * a.H * a.D;
     const int64_t grid = (total + kThreads - 1) / kThreads;
