@@ -12,7 +12,7 @@
 //
 // Kernels:
 //   decode_mfma   bf16/f16, head_dim 128, 16-token pages.  One workgroup =
-//                 one (sequence, split) x 8 kv heads, one wave per kv head; a
+//                 one (sequence, split) x 2 kv heads, one wave per kv head; a
 //                 wave streams its kv head's 256-byte K and V rows of every
 //                 page in its split with 16-byte loads (register prefetch of
 //                 PREF pages); QK^T and PV both on MFMA (P in the input
@@ -264,8 +264,8 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(Params p) {
 // ---------------------------------------------------------------------------
 // MFMA decode (bf16 / f16, head_dim 128, 16-token pages)
 //
-// One workgroup = (split of one sequence's pages) x 8 kv heads, one wave per
-// kv head, no workgroup barriers.  Per page a wave:
+// One workgroup = (split of one sequence's pages) x kDecWaves kv heads, one
+// wave per kv head, no workgroup barriers.  Per page a wave:
 //   * loads its kv head's K rows (16 tokens x 256 B) straight into the A
 //     operand layout of MFMA 16x16x32 (lane = token l%16, 16 bytes of d), and
 //     its V rows with 16-byte loads (lane group q = tokens 4q..4q+3, chunk
