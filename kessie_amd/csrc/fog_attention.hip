@@ -221,44 +221,88 @@ __global__ __launch_bounds__(kGenThreads) void attn_generic_kernel(Params p) {
 // ---------------------------------------------------------------------------
 // Split combine
 // ---------------------------------------------------------------------------
-constexpr int kCombineThreads = 128;
+constexpr int kCombineThreads = 256;
 constexpr int kMaxSplits = 256;
 
+// Workgroup (row, y) merges d in [y*D/Y, (y+1)*D/Y) of one row (Y =
+// gridDim.y, 1 unless rows are few).  With an even chunk its 256 lanes are
+// (split group, float2 column) pairs: each sums every groups-th split of its
+// column, and the groups meet in LDS.  (One thread per d looping over every
+// split was latency-bound: 25 us for one 128K sequence's 32 rows x 256 splits,
+// against 89 us for the whole partials kernel.)
 template <typename T>
 __global__ __launch_bounds__(kCombineThreads) void combine_kernel(Params p) {
   __shared__ float e_s[kMaxSplits];
+  __shared__ float2 part[kCombineThreads];
   __shared__ float inv_l;
   const int64_t row = blockIdx.x;  // (b*C + i)*Hq + h
   const int S = p.num_splits;
+  const int D = p.D;
   const int h = (int)(row % p.Hq);
   const int64_t bi = row / p.Hq;
   const int i = (int)(bi % p.C);
   const int b = (int)(bi / p.C);
+  const int tid = threadIdx.x, lane = tid & 63;
   const float* m = p.ws_m + row * S;
   const float* l = p.ws_l + row * S;
-  if (threadIdx.x < 64) {
+  if (tid < 64) {
     float mx = kNegInf;
-    for (int s = threadIdx.x; s < S; s += 64) mx = fmaxf(mx, m[s]);
+    for (int s = lane; s < S; s += 64) mx = fmaxf(mx, m[s]);
 #pragma unroll
     for (int w = 32; w >= 1; w >>= 1) mx = fmaxf(mx, __shfl_xor(mx, w, 64));
     float sum = 0.0f;
-    for (int s = threadIdx.x; s < S; s += 64) {
+    for (int s = lane; s < S; s += 64) {
       const float e = (m[s] == kNegInf) ? 0.0f : expf(m[s] - mx);
       e_s[s] = e;
       sum += e * l[s];
     }
 #pragma unroll
     for (int w = 32; w >= 1; w >>= 1) sum += __shfl_xor(sum, w, 64);
-    if (threadIdx.x == 0) inv_l = sum > 0.0f ? 1.0f / sum : 0.0f;
+    if (lane == 0) inv_l = sum > 0.0f ? 1.0f / sum : 0.0f;
   }
   __syncthreads();
   const float il = inv_l;
-  const float* o = p.ws_o + row * S * p.D;
-  for (int d = threadIdx.x; d < p.D; d += kCombineThreads) {
-    float acc = 0.0f;
-    for (int s = 0; s < S; ++s) acc += e_s[s] * o[(int64_t)s * p.D + d];
-    store_out<T>(p, b, i, h, d, acc * il);
+  const int chunk = D / gridDim.y;
+  const int d0 = blockIdx.y * chunk;
+  const float* o = p.ws_o + row * S * D + d0;
+  if ((chunk & 1) == 0 && kCombineThreads % (chunk / 2) == 0) {
+    const int cols = chunk / 2;                // float2 columns
+    const int groups = kCombineThreads / cols;
+    const int col = tid % cols, grp = tid / cols;
+    float ax = 0.0f, ay = 0.0f;
+#pragma unroll 4
+    for (int s = grp; s < S; s += groups) {
+      const float e = e_s[s];
+      const float2 v = *reinterpret_cast<const float2*>(o + (int64_t)s * D + 2 * col);
+      ax += e * v.x;
+      ay += e * v.y;
+    }
+    part[tid] = make_float2(ax, ay);
+    __syncthreads();
+    if (tid < cols) {
+      float2 acc = part[tid];
+      for (int g = 1; g < groups; ++g) {
+        acc.x += part[g * cols + tid].x;
+        acc.y += part[g * cols + tid].y;
+      }
+      store_out<T>(p, b, i, h, d0 + 2 * tid, acc.x * il);
+      store_out<T>(p, b, i, h, d0 + 2 * tid + 1, acc.y * il);
+    }
+  } else {
+    for (int d = tid; d < chunk; d += kCombineThreads) {
+      float acc = 0.0f;
+      for (int s = 0; s < S; ++s) acc += e_s[s] * o[(int64_t)s * D + d];
+      store_out<T>(p, b, i, h, d0 + d, acc * il);
+    }
   }
+}
+
+// Workgroups per row of the combine: split head_dim into up to four even
+// chunks when the rows alone would leave the chip mostly idle.
+inline int combine_dsplit(int64_t rows, int D) {
+  int y = 1;
+  while (y < 4 && rows * y < 256 && D % (4 * y) == 0) y *= 2;  // the chunk D/y stays even
+  return y;
 }
 
 // ---------------------------------------------------------------------------
@@ -590,7 +634,8 @@ int launch_generic(Params& p, hipStream_t stream) {
   if (check_launch("fog attention (generic)") != KESSIE_OK) return KESSIE_ERR_HIP;
   if (!p.direct_out && p.launch_combine) {
     const int64_t rows = (int64_t)p.B * p.C * p.Hq;
-    hipLaunchKernelGGL(combine_kernel<T>, dim3((unsigned)rows), dim3(kCombineThreads), 0, stream, p);
+    hipLaunchKernelGGL(combine_kernel<T>, dim3((unsigned)rows, combine_dsplit(rows, p.D)), dim3(kCombineThreads),
+                       0, stream, p);
     return check_launch("fog attention (combine)");
   }
   return KESSIE_OK;
@@ -614,7 +659,8 @@ int launch_decode_mfma(Params& p, hipStream_t stream) {
   if (check_launch("fog decode (mfma)") != KESSIE_OK) return KESSIE_ERR_HIP;
   if (!p.direct_out && p.launch_combine) {
     const int64_t rows = (int64_t)p.B * p.Hq;
-    hipLaunchKernelGGL(combine_kernel<T>, dim3((unsigned)rows), dim3(kCombineThreads), 0, stream, p);
+    hipLaunchKernelGGL(combine_kernel<T>, dim3((unsigned)rows, combine_dsplit(rows, p.D)), dim3(kCombineThreads),
+                       0, stream, p);
     return check_launch("fog decode (combine)");
   }
   return KESSIE_OK;
@@ -823,13 +869,16 @@ extern "C" int kessie_fog_decode_combine(const void* workspace, size_t workspace
   hipStream_t s = as_stream(stream);
   switch (dtype) {
     case KESSIE_DTYPE_F32:
-      hipLaunchKernelGGL(combine_kernel<float>, dim3((unsigned)rows), dim3(kCombineThreads), 0, s, p);
+      hipLaunchKernelGGL(combine_kernel<float>, dim3((unsigned)rows, combine_dsplit(rows, p.D)),
+                         dim3(kCombineThreads), 0, s, p);
       break;
     case KESSIE_DTYPE_BF16:
-      hipLaunchKernelGGL(combine_kernel<bf16_t>, dim3((unsigned)rows), dim3(kCombineThreads), 0, s, p);
+      hipLaunchKernelGGL(combine_kernel<bf16_t>, dim3((unsigned)rows, combine_dsplit(rows, p.D)),
+                         dim3(kCombineThreads), 0, s, p);
       break;
     default:
-      hipLaunchKernelGGL(combine_kernel<f16_t>, dim3((unsigned)rows), dim3(kCombineThreads), 0, s, p);
+      hipLaunchKernelGGL(combine_kernel<f16_t>, dim3((unsigned)rows, combine_dsplit(rows, p.D)),
+                         dim3(kCombineThreads), 0, s, p);
       break;
   }
   return check_launch("fog decode combine");
