@@ -169,7 +169,10 @@ int kessie_fog_decode_combine(const void* workspace, size_t workspace_bytes,
                               int num_kv_heads, int head_dim, int max_ctx,
                               int page_size, int dtype, void* stream);
 
-/* Bytes of workspace kessie_fog_prefill_paged needs (host call). */
+/* Bytes of workspace kessie_fog_prefill_paged needs (host call).  Zero when
+ * one pass per query tile fills the device; a small chunk on a long context
+ * splits the key range (S from the CU count and KESSIE_PREFILL_SPLITS) and
+ * needs room for the per-split partials. */
 size_t kessie_fog_prefill_workspace_bytes(int batch, int num_q_tokens,
                                           int num_q_heads, int num_kv_heads,
                                           int head_dim, int max_ctx,

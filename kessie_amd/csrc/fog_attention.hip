@@ -607,6 +607,22 @@ int decode_splits(int B, int Hkv, int max_ctx, int page_size) {
   return max(s, 1);
 }
 
+// Key splits of the MFMA prefill: enough workgroups for one per CU (one fits a
+// CU at a time: 106.5 KiB of LDS), at least 8 key tiles (512 keys) per split.
+// A 2,048-query chunk at GQA 4 and 8 kv heads already has 256 workgroups: no
+// split.  KESSIE_PREFILL_SPLITS > 0 forces the count.
+int prefill_mfma_splits(int B, int C, int Hkv, int G, int max_ctx) {
+  const int forced = env_int("KESSIE_PREFILL_SPLITS", 0);  // 0: sized to fill the chip
+  if (forced > 0) return min(forced, kMaxSplits);
+  const int per_wg = 256 / max(G, 1);  // query positions per workgroup
+  const int units = B * Hkv * div_up(max(C, 1), per_wg);
+  const int tiles = div_up(max(max_ctx, 1), 64);
+  int s = div_up(device_cus(), max(units, 1));
+  s = min(s, max(1, tiles / 8));
+  s = min(s, kMaxSplits);
+  return max(s, 1);
+}
+
 int prefill_splits(int B, int C, int Hkv, int G, int max_ctx, int page_size) {
   const int target = env_int("KESSIE_PREFILL_WGS", 1024);
   const int units = B * Hkv * div_up(C * G, kGenRT);
@@ -888,8 +904,9 @@ extern "C" size_t kessie_fog_prefill_workspace_bytes(int batch, int num_q_tokens
                                                      int head_dim, int max_ctx, int page_size, int dtype) {
   (void)dtype;
   if (batch <= 0 || num_q_tokens <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0) return 0;
-  const int S = kessie::attn::prefill_splits(batch, num_q_tokens, num_kv_heads, num_q_heads / num_kv_heads,
-                                             max_ctx, page_size);
+  const int G = num_q_heads / num_kv_heads;
+  const int S = max(kessie::attn::prefill_splits(batch, num_q_tokens, num_kv_heads, G, max_ctx, page_size),
+                    kessie::attn::prefill_mfma_splits(batch, num_q_tokens, num_kv_heads, G, max_ctx));
   return kessie::attn::partial_bytes((int64_t)batch * num_q_tokens * num_q_heads, S, head_dim);
 }
 
@@ -946,11 +963,29 @@ extern "C" int kessie_fog_prefill_paged(const void* q, const void* kv_pool, int 
                  "fog prefill: page_table and ctx_lens are required");
   KESSIE_REQUIRE(kv_stride >= 0, KESSIE_ERR_INVALID, "fog prefill: kv_stride %lld", (long long)kv_stride);
   if (batch == 0) return KESSIE_OK;
-  if (prefill_mfma_ok(p, dtype)) {  // MFMA kernel: one pass over the keys, no workspace
-    p.num_splits = 1;
-    p.direct_out = 1;
+  if (prefill_mfma_ok(p, dtype)) {
+    // MFMA kernel: one pass over the keys; split-K (partials + combine) when
+    // the chunk alone would leave the chip idle.
+    p.num_splits = prefill_mfma_splits(batch, num_q_tokens, num_kv_heads, p.G, max_ctx);
+    p.direct_out = p.num_splits == 1 ? 1 : 0;
     p.launch_combine = 0;
-    return prefill_mfma(p, dtype, as_stream(stream));
+    const int64_t rows = (int64_t)batch * num_q_tokens * num_q_heads;
+    if (!p.direct_out) {
+      const size_t need = partial_bytes(rows, p.num_splits, head_dim);
+      KESSIE_REQUIRE(workspace != nullptr && workspace_bytes >= need, KESSIE_ERR_WORKSPACE,
+                     "fog prefill: workspace of %zu bytes needed, got %zu", need, workspace_bytes);
+      KESSIE_REQUIRE(aligned16(workspace), KESSIE_ERR_INVALID, "fog prefill: workspace not 16-byte aligned");
+      carve_workspace(p, workspace, rows);
+    }
+    st = prefill_mfma(p, dtype, as_stream(stream));
+    if (st != KESSIE_OK || p.direct_out) return st;
+    const hipStream_t s = as_stream(stream);
+    const dim3 cgrid((unsigned)rows, combine_dsplit(rows, p.D));
+    if (dtype == KESSIE_DTYPE_BF16)
+      hipLaunchKernelGGL(combine_kernel<bf16_t>, cgrid, dim3(kCombineThreads), 0, s, p);
+    else
+      hipLaunchKernelGGL(combine_kernel<f16_t>, cgrid, dim3(kCombineThreads), 0, s, p);
+    return check_launch("fog prefill (combine)");
   }
   p.num_splits = prefill_splits(batch, num_q_tokens, num_kv_heads, p.G, max_ctx, page_size);
   p.direct_out = p.num_splits == 1 ? 1 : 0;

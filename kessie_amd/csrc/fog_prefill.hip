@@ -43,6 +43,7 @@ constexpr int kKStage = kPfKT * kKRow;  // elements per K stage
 constexpr int kVStage = 128 * kVRowW;   // words per V^T stage
 constexpr size_t kPfLdsBytes = (size_t)kPfStages * (kKStage * 2 + kVStage * 4 + 2 * kPfKT * 4);
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
@@ -77,7 +78,7 @@ __device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirs
 
 __device__ __forceinline__ bool page_ok(int pid, int num_pages) { return pid >= 0 && pid < num_pages; }
 
-template <typename T, int G, bool kBias, bool kVs>
+template <typename T, int G, bool kBias, bool kVs, bool kSplit>
 __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
   typedef typename Mma32<T>::v8 v8;
   typedef typename Mma32<T>::v4 v4;
@@ -109,11 +110,23 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
   const int qi_last = min(C, qi_first + kPos) - 1;
   const int qmin = max(ctx - C + qi_first, 0);
   const int qmax = ctx - C + qi_last;
-  if (qi_last < qi_first || qmax < 0) return;
+  if (qi_last < qi_first) return;
+  // Rows before position 0 (a chunk longer than its context) see no keys:
+  // they still run, with no tiles, and store zeros (or empty partials).
   int lo = 0, hi = 0;
-  key_range(p, ctx, qmin, qmax, &lo, &hi);
-  const int t_begin = (lo / kPfKT) * kPfKT;
-  const int n_tiles = hi > t_begin ? div_up(hi - t_begin, kPfKT) : 0;
+  if (qmax >= 0) key_range(p, ctx, qmin, qmax, &lo, &hi);
+  const int tile_lo = lo / kPfKT;
+  int n_tiles = hi > tile_lo * kPfKT ? div_up(hi - tile_lo * kPfKT, kPfKT) : 0;
+  // Split-K: workgroup z takes its share of the key tiles (possibly none:
+  // it still writes an empty partial for its rows).
+  const int S = kSplit ? (int)gridDim.z : 1, split = kSplit ? (int)blockIdx.z : 0;
+  int first = 0;
+  if (kSplit) {
+    const int per = div_up(n_tiles, S);
+    first = min(n_tiles, split * per);
+    n_tiles = min(n_tiles, first + per) - first;
+  }
+  const int t_begin = (tile_lo + first) * kPfKT;
   const int n_tab = div_up(hi, 16);  // table entries that may be read
 
   // This lane's query row.
@@ -342,6 +355,23 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
   // Lane (col, half) holds row frow at d = 32*db + 8*(v/4) + 4*half + (v%4).
   const float l = l_half + __shfl_xor(l_half, 32);
   if (!row_ok) return;
+  if (kSplit) {
+    // Split partial: unnormalised O, the running max in natural-log units
+    // (the softmax here is base 2) and the sum, merged by the combine kernel.
+    const int64_t r = row_id(p, b, qi, head) * S + split;
+    float* dst = p.ws_o + r * 128 + 4 * half;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int vq = 0; vq < 4; ++vq)
+        *reinterpret_cast<f32x4*>(dst + 32 * db + 8 * vq) =
+            f32x4{oacc[db][4 * vq], oacc[db][4 * vq + 1], oacc[db][4 * vq + 2], oacc[db][4 * vq + 3]};
+    if (half == 0) {
+      p.ws_m[r] = m_run == kNegInf ? kNegInf : m_run * kLn2;
+      p.ws_l[r] = l;
+    }
+    return;
+  }
   const float il = l > 0.0f ? 1.0f / l : 0.0f;
   T* orow = static_cast<T*>(p.out) + o_off + (int64_t)qi * p.o_is + (int64_t)head * p.o_hs;
 #pragma unroll
@@ -355,12 +385,12 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
     }
 }
 
-template <typename T, int G, bool kBias, bool kVs>
+template <typename T, int G, bool kBias, bool kVs, bool kSplit>
 int launch_one(const Params& p, dim3 grid, hipStream_t stream) {
   static bool lds_set[64] = {};  // per instance and device
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-  const void* fn = reinterpret_cast<const void*>(prefill_mfma_kernel<T, G, kBias, kVs>);
+  const void* fn = reinterpret_cast<const void*>(prefill_mfma_kernel<T, G, kBias, kVs, kSplit>);
   if (!lds_set[dev]) {
     if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPfLdsBytes) != hipSuccess) {
       set_error(KESSIE_ERR_HIP, "fog prefill (mfma): %zu bytes of LDS unavailable", kPfLdsBytes);
@@ -368,25 +398,35 @@ int launch_one(const Params& p, dim3 grid, hipStream_t stream) {
     }
     lds_set[dev] = true;
   }
-  hipLaunchKernelGGL((prefill_mfma_kernel<T, G, kBias, kVs>), grid, dim3(kPfThreads), kPfLdsBytes, stream, p);
+  hipLaunchKernelGGL((prefill_mfma_kernel<T, G, kBias, kVs, kSplit>), grid, dim3(kPfThreads), kPfLdsBytes, stream, p);
   return check_launch("fog prefill (mfma)");
 }
 
-template <typename T, int G>
+template <typename T, int G, bool kSplit>
 int launch_fog(const Params& p, dim3 grid, hipStream_t stream) {
-  if (p.bias) return p.vscale ? launch_one<T, G, true, true>(p, grid, stream) : launch_one<T, G, true, false>(p, grid, stream);
-  return p.vscale ? launch_one<T, G, false, true>(p, grid, stream) : launch_one<T, G, false, false>(p, grid, stream);
+  if (p.bias)
+    return p.vscale ? launch_one<T, G, true, true, kSplit>(p, grid, stream)
+                    : launch_one<T, G, true, false, kSplit>(p, grid, stream);
+  return p.vscale ? launch_one<T, G, false, true, kSplit>(p, grid, stream)
+                  : launch_one<T, G, false, false, kSplit>(p, grid, stream);
+}
+
+// The split instances are separate: the unsplit loop keeps the register
+// allocation it was tuned with (the shared form cost the V-fog instance 6%).
+template <typename T, int G>
+int launch_split(const Params& p, dim3 grid, hipStream_t stream) {
+  return p.direct_out ? launch_fog<T, G, false>(p, grid, stream) : launch_fog<T, G, true>(p, grid, stream);
 }
 
 template <typename T>
 int launch_prefill(Params& p, hipStream_t stream) {
   const int kpos = kPfRows / p.G;
-  dim3 grid(div_up(p.C, kpos) * p.Hkv, p.B);
+  dim3 grid(div_up(p.C, kpos) * p.Hkv, p.B, max(p.num_splits, 1));
   switch (p.G) {
-    case 1: return launch_fog<T, 1>(p, grid, stream);
-    case 2: return launch_fog<T, 2>(p, grid, stream);
-    case 4: return launch_fog<T, 4>(p, grid, stream);
-    case 8: return launch_fog<T, 8>(p, grid, stream);
+    case 1: return launch_split<T, 1>(p, grid, stream);
+    case 2: return launch_split<T, 2>(p, grid, stream);
+    case 4: return launch_split<T, 4>(p, grid, stream);
+    case 8: return launch_split<T, 8>(p, grid, stream);
     default:
       set_error(KESSIE_ERR_UNSUPPORTED, "fog prefill (mfma): GQA ratio %d", p.G);
       return KESSIE_ERR_UNSUPPORTED;

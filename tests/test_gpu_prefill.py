@@ -139,12 +139,15 @@ def test_prefill_1m_context_sampled(dev):
 
 @pytest.mark.parametrize("fog", ["vscale", "bias", "none"])
 @pytest.mark.parametrize("window", [0, 50])
-def test_prefill_varlen_matches_per_sequence(dev, fog, window):
+def test_prefill_varlen_matches_per_sequence(dev, fog, window, monkeypatch):
     """One varlen launch over sequences with different chunk lengths (incl. a
     one-token chunk and an empty one) equals the per-sequence launches bit for
     bit, and the oracle within tolerance; the query_start_loc slice may start
-    at a non-zero offset."""
+    at a non-zero offset.  The per-sequence launches are held to one key split
+    (the varlen launch never splits), which makes the summation orders equal."""
     from kessie_amd import ops
+
+    monkeypatch.setenv("KESSIE_PREFILL_SPLITS", "1")
 
     chunks, ctxs = [37, 1, 300, 0, 129], [900, 64, 300, 50, 4000]
     b, hq, hkv, d = len(chunks), 32, 8, 128
@@ -189,3 +192,30 @@ def test_prefill_varlen_unsupported_shape_launches_nothing(dev):
     assert not ops.fog_prefill_varlen(q, qsl, 5, pool, table, lens, 40, out=out)
     torch.cuda.synchronize()
     assert torch.all(out == 7.0)
+
+
+@pytest.mark.parametrize("c,ctx,fog,window,force", [(300, 20000, "vscale", 0, 0), (512, 40000, "bias", 0, 0),
+                                                    (64, 9000, "none", 0, 0), (200, 30000, "vscale", 5000, 0),
+                                                    (100, 3000, "vscale", 0, 64), (700, 2000, "bias", 300, 5)])
+def test_prefill_split_k(dev, c, ctx, fog, window, force, monkeypatch):
+    """A small chunk on a long context takes the MFMA kernel's split-K path
+    (partials + combine): checked against the blockwise oracle on sampled rows,
+    including the chunk's first and last rows.  Forced counts cover splits that
+    get no key tile (64 splits of 47 tiles; a window leaves most splits empty)."""
+    from kessie_amd import _lib, ops
+
+    if force:
+        monkeypatch.setenv("KESSIE_PREFILL_SPLITS", str(force))
+    assert _lib.load().kessie_fog_prefill_workspace_bytes(1, c, 32, 8, 128, ctx, 16, 1) > 0
+    q, pool, table, lens = _case(dev, 1, c, [ctx], 32, 8, torch.bfloat16, seed=c)
+    vs = build_fog_weights(ctx).to(dev) if fog == "vscale" else None
+    bias = fog_bias(ctx, 0.5, 0.5, {3, 17, ctx - 2}, 0.1).to(dev) if fog == "bias" else None
+    out = ops.fog_prefill(q, pool, table, lens, ctx, fog_vscale=vs, fog_bias=bias, window=window)
+    torch.cuda.synchronize()
+    rows = torch.unique(torch.tensor([0, 1, c // 3, c // 2, c - 2, c - 1]))
+    if bias is None:
+        ref = paged_prefill_blockwise(q.cpu(), pool, table, lens.cpu(), rows,
+                                      fog_vscale=None if vs is None else vs.cpu(), window=window)
+    else:
+        ref = paged_prefill_ref(q.cpu(), pool.cpu(), table.cpu(), lens.cpu(), None, bias.cpu(), window, rows=rows)
+    _check(out[:, rows.long()], ref, torch.bfloat16)
