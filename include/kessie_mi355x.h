@@ -169,10 +169,11 @@ int kessie_fog_decode_combine(const void* workspace, size_t workspace_bytes,
                               int num_kv_heads, int head_dim, int max_ctx,
                               int page_size, int dtype, void* stream);
 
-/* Bytes of workspace kessie_fog_prefill_paged needs (host call).  Zero when
- * one pass per query tile fills the device; a small chunk on a long context
- * splits the key range (S from the CU count and KESSIE_PREFILL_SPLITS) and
- * needs room for the per-split partials. */
+/* Bytes of workspace kessie_fog_prefill_paged may need (host call): room for
+ * per-split partials at the larger of the two kernels' split counts.  The
+ * MFMA kernel touches it only when a small chunk on a long context splits
+ * the key range (S from the CU count, or KESSIE_PREFILL_SPLITS); the generic
+ * kernel always uses it. */
 size_t kessie_fog_prefill_workspace_bytes(int batch, int num_q_tokens,
                                           int num_q_heads, int num_kv_heads,
                                           int head_dim, int max_ctx,
