@@ -207,8 +207,10 @@ int kessie_fog_prefill_paged(
  * query_start_loc[b] <= max_query_len, query i of it at ctx_lens[b] - C_b + i.
  * MFMA shapes only (bf16/fp16, head_dim 128, 16-token pages, GQA 1/2/4/8,
  * 16-byte aligned rows); other shapes return KESSIE_ERR_UNSUPPORTED without
- * launching (call kessie_fog_prefill_paged per sequence instead).  No
- * workspace. */
+ * launching (call kessie_fog_prefill_paged per sequence instead).  The
+ * workspace is sized by kessie_fog_prefill_workspace_bytes(batch,
+ * max_query_len, ...) and used only when the chunks are too few to fill the
+ * device (split-K). */
 int kessie_fog_prefill_varlen(
     const void* q, const int32_t* query_start_loc, int max_query_len,
     const void* kv_pool, int num_pages, int64_t page_stride, int64_t tok_stride,
@@ -217,7 +219,7 @@ int kessie_fog_prefill_varlen(
     int64_t fog_vscale_bstride, const float* fog_bias, int64_t fog_bias_bstride,
     void* out, int batch, int num_q_heads, int num_kv_heads, int head_dim,
     int page_size, int max_ctx, int window, float sm_scale, int causal,
-    int dtype, void* stream);
+    int dtype, void* workspace, size_t workspace_bytes, void* stream);
 
 /* =========================================================================
  * RoPE position remap

@@ -59,7 +59,7 @@ SIGNATURES = {
         _P, _I, _I, _I, _I, _I, _I, _I, _I, _F, _I, _I, _P, _SZ, _P]),
     "kessie_fog_prefill_varlen": (_I, [
         _P, _P, _I, _P, _I, _I64, _I64, _I64, _I64, _P, _I64, _P, _P, _I64, _P, _I64,
-        _P, _I, _I, _I, _I, _I, _I, _I, _F, _I, _I, _P]),
+        _P, _I, _I, _I, _I, _I, _I, _I, _F, _I, _I, _P, _SZ, _P]),
     # rope remap
     "kessie_rope_remap_paged": (_I, [_P, _I64, _I64, _I64, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     # page management

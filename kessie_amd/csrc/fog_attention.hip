@@ -240,8 +240,14 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(Params p) {
   const int D = p.D;
   const int h = (int)(row % p.Hq);
   const int64_t bi = row / p.Hq;
-  const int i = (int)(bi % p.C);
-  const int b = (int)(bi / p.C);
+  int i = (int)(bi % p.C);
+  int b = (int)(bi / p.C);
+  if (p.q_start) {  // varlen prefill: rows past the chunk have no partials
+    const int s0 = p.q_start[b] - p.q_start[0];
+    if (i >= p.q_start[b + 1] - p.q_start[b]) return;  // uniform, before any barrier
+    i += s0;
+    b = 0;
+  }
   const int tid = threadIdx.x, lane = tid & 63;
   const float* m = p.ws_m + row * S;
   const float* l = p.ws_l + row * S;
@@ -910,6 +916,36 @@ extern "C" size_t kessie_fog_prefill_workspace_bytes(int batch, int num_q_tokens
   return kessie::attn::partial_bytes((int64_t)batch * num_q_tokens * num_q_heads, S, head_dim);
 }
 
+// MFMA prefill for p.B sequences of up to p.C queries: one pass over the keys;
+// split-K (partials + combine) when the chunks alone would leave CUs idle.
+// Partial rows are (b*C + i)*Hq + h; with q_start the combine skips rows past a
+// sequence's chunk and writes the rest at its packed offset.
+static int run_prefill_mfma(kessie::attn::Params& p, int dtype, void* workspace, size_t workspace_bytes,
+                            void* stream) {
+  using namespace kessie;
+  using namespace kessie::attn;
+  p.num_splits = prefill_mfma_splits(p.B, p.C, p.Hkv, p.G, p.max_ctx);
+  p.direct_out = p.num_splits == 1 ? 1 : 0;
+  p.launch_combine = 0;
+  const int64_t rows = (int64_t)p.B * p.C * p.Hq;
+  if (!p.direct_out) {
+    const size_t need = partial_bytes(rows, p.num_splits, p.D);
+    KESSIE_REQUIRE(workspace != nullptr && workspace_bytes >= need, KESSIE_ERR_WORKSPACE,
+                   "fog prefill: workspace of %zu bytes needed, got %zu", need, workspace_bytes);
+    KESSIE_REQUIRE(aligned16(workspace), KESSIE_ERR_INVALID, "fog prefill: workspace not 16-byte aligned");
+    carve_workspace(p, workspace, rows);
+  }
+  const hipStream_t s = as_stream(stream);
+  const int st = prefill_mfma(p, dtype, s);
+  if (st != KESSIE_OK || p.direct_out) return st;
+  const dim3 cgrid((unsigned)rows, combine_dsplit(rows, p.D));
+  if (dtype == KESSIE_DTYPE_BF16)
+    hipLaunchKernelGGL(combine_kernel<bf16_t>, cgrid, dim3(kCombineThreads), 0, s, p);
+  else
+    hipLaunchKernelGGL(combine_kernel<f16_t>, cgrid, dim3(kCombineThreads), 0, s, p);
+  return check_launch("fog prefill (combine)");
+}
+
 extern "C" int kessie_fog_prefill_paged(const void* q, const void* kv_pool, int num_pages, int64_t page_stride,
                                         int64_t tok_stride, int64_t kv_stride, int64_t head_stride,
                                         const int32_t* page_table, int64_t table_stride, const int32_t* ctx_lens,
@@ -963,30 +999,7 @@ extern "C" int kessie_fog_prefill_paged(const void* q, const void* kv_pool, int 
                  "fog prefill: page_table and ctx_lens are required");
   KESSIE_REQUIRE(kv_stride >= 0, KESSIE_ERR_INVALID, "fog prefill: kv_stride %lld", (long long)kv_stride);
   if (batch == 0) return KESSIE_OK;
-  if (prefill_mfma_ok(p, dtype)) {
-    // MFMA kernel: one pass over the keys; split-K (partials + combine) when
-    // the chunk alone would leave the chip idle.
-    p.num_splits = prefill_mfma_splits(batch, num_q_tokens, num_kv_heads, p.G, max_ctx);
-    p.direct_out = p.num_splits == 1 ? 1 : 0;
-    p.launch_combine = 0;
-    const int64_t rows = (int64_t)batch * num_q_tokens * num_q_heads;
-    if (!p.direct_out) {
-      const size_t need = partial_bytes(rows, p.num_splits, head_dim);
-      KESSIE_REQUIRE(workspace != nullptr && workspace_bytes >= need, KESSIE_ERR_WORKSPACE,
-                     "fog prefill: workspace of %zu bytes needed, got %zu", need, workspace_bytes);
-      KESSIE_REQUIRE(aligned16(workspace), KESSIE_ERR_INVALID, "fog prefill: workspace not 16-byte aligned");
-      carve_workspace(p, workspace, rows);
-    }
-    st = prefill_mfma(p, dtype, as_stream(stream));
-    if (st != KESSIE_OK || p.direct_out) return st;
-    const hipStream_t s = as_stream(stream);
-    const dim3 cgrid((unsigned)rows, combine_dsplit(rows, p.D));
-    if (dtype == KESSIE_DTYPE_BF16)
-      hipLaunchKernelGGL(combine_kernel<bf16_t>, cgrid, dim3(kCombineThreads), 0, s, p);
-    else
-      hipLaunchKernelGGL(combine_kernel<f16_t>, cgrid, dim3(kCombineThreads), 0, s, p);
-    return check_launch("fog prefill (combine)");
-  }
+  if (prefill_mfma_ok(p, dtype)) return run_prefill_mfma(p, dtype, workspace, workspace_bytes, stream);
   p.num_splits = prefill_splits(batch, num_q_tokens, num_kv_heads, p.G, max_ctx, page_size);
   p.direct_out = p.num_splits == 1 ? 1 : 0;
   p.launch_combine = 1;
@@ -1008,7 +1021,7 @@ extern "C" int kessie_fog_prefill_varlen(const void* q, const int32_t* query_sta
                                          int64_t fog_vscale_bstride, const float* fog_bias, int64_t fog_bias_bstride,
                                          void* out, int batch, int num_q_heads, int num_kv_heads, int head_dim,
                                          int page_size, int max_ctx, int window, float sm_scale, int causal,
-                                         int dtype, void* stream) {
+                                         int dtype, void* workspace, size_t workspace_bytes, void* stream) {
   using namespace kessie;
   using namespace kessie::attn;
   clear_error();
@@ -1056,10 +1069,7 @@ extern "C" int kessie_fog_prefill_varlen(const void* q, const int32_t* query_sta
   KESSIE_REQUIRE(prefill_mfma_ok(p, dtype), KESSIE_ERR_UNSUPPORTED,
                  "fog prefill varlen: shape not taken by the MFMA kernel (bf16/fp16, head_dim 128, 16-token pages, "
                  "GQA 1/2/4/8, 16-byte aligned rows)");
-  p.num_splits = 1;
-  p.direct_out = 1;
-  p.launch_combine = 0;
-  return prefill_mfma(p, dtype, as_stream(stream));
+  return run_prefill_mfma(p, dtype, workspace, workspace_bytes, stream);
 }
 
 // Reference launchers (kessie_kernels_v2.hip:716-751, 788-825): dense fp16

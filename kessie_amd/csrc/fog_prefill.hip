@@ -93,8 +93,35 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
   const int wave = uniform(tid >> 6);
   const int col = lane & 31, half = lane >> 5;
   const int g = blockIdx.x % p.Hkv;
-  const int qtile = blockIdx.x / p.Hkv;
-  const int b = blockIdx.y;
+  int qtile = blockIdx.x / p.Hkv;
+  int b = blockIdx.y;
+  if (p.q_start) {
+    // Varlen: x / Hkv numbers the live (sequence, query tile) pairs in order,
+    // so the grid's surplus workgroups all sit at its end and exit at once
+    // (left among the live ones, they unbalanced the placement of those).
+    // Each wave scans query_start_loc 64 sequences at a time.
+    int found = -1, before = 0;
+    for (int b0 = 0; b0 < p.B; b0 += 64) {
+      const int bb = b0 + lane;
+      const int nt = bb < p.B ? div_up(p.q_start[bb + 1] - p.q_start[bb], kPos) : 0;
+      int inc = nt;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(inc, o, 64);
+        if (lane >= o) inc += y;
+      }
+      const int total = __builtin_amdgcn_readlane(inc, 63);
+      if (qtile < before + total) {
+        const int l = __ffsll((unsigned long long)__ballot(before + inc > qtile)) - 1;
+        found = b0 + l;
+        qtile -= before + __builtin_amdgcn_readlane(inc - nt, l);
+        break;
+      }
+      before += total;
+    }
+    if (found < 0) return;
+    b = found;
+  }
   const int ctx = seq_ctx(p, b);
   int C = p.C;  // this sequence's queries, and where they start (uniform)
   int64_t q_off = (int64_t)b * p.q_bs, o_off = (int64_t)b * p.o_bs;
@@ -421,7 +448,8 @@ int launch_split(const Params& p, dim3 grid, hipStream_t stream) {
 template <typename T>
 int launch_prefill(Params& p, hipStream_t stream) {
   const int kpos = kPfRows / p.G;
-  dim3 grid(div_up(p.C, kpos) * p.Hkv, p.B, max(p.num_splits, 1));
+  // Varlen: the live (sequence, query tile) pairs are numbered along x.
+  dim3 grid(div_up(p.C, kpos) * p.Hkv * (p.q_start ? p.B : 1), p.q_start ? 1 : p.B, max(p.num_splits, 1));
   switch (p.G) {
     case 1: return launch_split<T, 1>(p, grid, stream);
     case 2: return launch_split<T, 2>(p, grid, stream);

@@ -283,13 +283,16 @@ def fog_prefill_varlen(q: torch.Tensor, query_start_loc: torch.Tensor, max_query
                        page_table: torch.Tensor, ctx_lens: torch.Tensor, max_ctx: int,
                        fog_vscale: Optional[torch.Tensor] = None, fog_bias: Optional[torch.Tensor] = None,
                        window: int = 0, causal: bool = True, sm_scale: Optional[float] = None,
-                       layout: str = "native", out: Optional[torch.Tensor] = None, stream=None) -> bool:
+                       layout: str = "native", out: Optional[torch.Tensor] = None,
+                       ws: Optional[torch.Tensor] = None, stream=None) -> bool:
     """Chunked prefill of B sequences with different chunk lengths in one
     launch: q/out [T, Hq, D] packed, sequence b's queries at rows
     query_start_loc[b] - query_start_loc[0] .. (int32 [B+1] on the device, e.g.
     a slice of vLLM's query_start_loc), query i of it at ctx_lens[b] - C_b + i.
     Returns False, having launched nothing, for shapes the MFMA kernel does not
-    take (the caller then runs fog_prefill per sequence)."""
+    take (the caller then runs fog_prefill per sequence).  ws: split-K
+    workspace (a cached one when None), used when the chunks are too few to
+    fill the device."""
     pv = pool_view(pool, layout)
     q = _contig(q, "q")
     t, hq, d = q.shape
@@ -313,11 +316,17 @@ def fog_prefill_varlen(q: torch.Tensor, query_start_loc: torch.Tensor, max_query
     vs, vs_bs = _fog_arg(fog_vscale, b, "fog_vscale", max_ctx)
     bi, bi_bs = _fog_arg(fog_bias, b, "fog_bias", max_ctx)
     lib = _lib.load()
+    dt = dtype_code(q.dtype)
+    if ws is None:
+        need = lib.kessie_fog_prefill_workspace_bytes(b, int(max_query_len), hq, pv.num_kv_heads, d, max_ctx,
+                                                      pv.page_size, dt)
+        ws = workspace(need, q.device, "attn")
+    wsz = 0 if ws is None else ws.numel() * ws.element_size()
     st = lib.kessie_fog_prefill_varlen(
         _ptr(q), _ptr(query_start_loc), int(max_query_len), C.c_void_p(pv.k_ptr), pv.num_pages, pv.page_stride,
         pv.tok_stride, pv.kv_stride, pv.head_stride, _ptr(page_table), page_table.stride(0), _ptr(ctx_lens),
         _ptr(vs), vs_bs, _ptr(bi), bi_bs, _ptr(out), b, hq, pv.num_kv_heads, d, pv.page_size, int(max_ctx),
-        int(window), float(sm_scale), 1 if causal else 0, dtype_code(q.dtype), _stream_ptr(stream, q.device))
+        int(window), float(sm_scale), 1 if causal else 0, dt, _ptr(ws), wsz, _stream_ptr(stream, q.device))
     if st == _lib.ERR_UNSUPPORTED:
         return False
     _lib.check("kessie_fog_prefill_varlen", st)

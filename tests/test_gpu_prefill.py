@@ -219,3 +219,70 @@ def test_prefill_split_k(dev, c, ctx, fog, window, force, monkeypatch):
     else:
         ref = paged_prefill_ref(q.cpu(), pool.cpu(), table.cpu(), lens.cpu(), None, bias.cpu(), window, rows=rows)
     _check(out[:, rows.long()], ref, torch.bfloat16)
+
+
+@pytest.mark.parametrize("chunks,ctxs,force", [([200, 150], [30000, 20000], 0),
+                                               ([37, 1, 300, 0, 129], [900, 64, 300, 50, 4000], 16)])
+def test_prefill_varlen_split_k(dev, chunks, ctxs, force, monkeypatch):
+    """Varlen launches that split the key range (two short chunks on long
+    contexts: sized split; ragged chunks incl. an empty one: forced 16 splits,
+    most of them empty) match the oracle, every packed row written."""
+    from kessie_amd import ops
+
+    if force:
+        monkeypatch.setenv("KESSIE_PREFILL_SPLITS", str(force))
+    b, hq, hkv, d = len(chunks), 32, 8, 128
+    _, pool, table, lens = _case(dev, b, 1, ctxs, hq, hkv, torch.bfloat16, seed=21)
+    starts = [0]
+    for c in chunks:
+        starts.append(starts[-1] + c)
+    qsl = torch.tensor(starts, dtype=torch.int32, device=dev)
+    q = torch.randn(starts[-1], hq, d, generator=gen(dev, 22), device=dev).to(torch.bfloat16)
+    mx = max(ctxs)
+    vs = torch.rand(b, mx, generator=gen(dev, 23), device=dev)
+    out = torch.full_like(q, float("nan"))
+    assert ops.fog_prefill_varlen(q, qsl, max(chunks), pool, table, lens, mx, fog_vscale=vs, out=out)
+    torch.cuda.synchronize()
+    assert not torch.isnan(out).any()
+    for i, c in enumerate(chunks):
+        if c == 0:
+            continue
+        s = starts[i]
+        rows = torch.unique(torch.tensor([0, c // 2, c - 1]))
+        qq = q[s:s + c].unsqueeze(0).cpu()
+        if ctxs[i] > 8192:
+            ref = paged_prefill_blockwise(qq, pool, table[i:i + 1].cpu(), lens[i:i + 1].cpu(), rows,
+                                          fog_vscale=vs[i].cpu())
+        else:
+            ref = paged_prefill_ref(qq, pool.cpu(), table[i:i + 1].cpu(), lens[i:i + 1].cpu(), vs[i].cpu(), None, 0,
+                                    rows=rows)
+        _check(out[s:s + c][rows.long()].unsqueeze(0), ref, torch.bfloat16)
+
+
+def test_prefill_varlen_many_sequences(dev):
+    """70 sequences (the tile numbering scans query_start_loc 64 at a time),
+    chunk lengths 0..80 with empty ones, every row against the oracle."""
+    from kessie_amd import ops
+
+    g = torch.Generator().manual_seed(31)
+    b, hq, hkv, d = 70, 16, 8, 128
+    chunks = torch.randint(0, 81, (b,), generator=g).tolist()
+    chunks[3] = chunks[64] = 0
+    ctxs = [c + int(x) for c, x in zip(chunks, torch.randint(1, 400, (b,), generator=g))]
+    _, pool, table, lens = _case(dev, b, 1, ctxs, hq, hkv, torch.bfloat16, seed=32)
+    starts = [0]
+    for c in chunks:
+        starts.append(starts[-1] + c)
+    qsl = torch.tensor(starts, dtype=torch.int32, device=dev)
+    q = torch.randn(starts[-1], hq, d, generator=gen(dev, 33), device=dev).to(torch.bfloat16)
+    out = torch.full_like(q, float("nan"))
+    assert ops.fog_prefill_varlen(q, qsl, max(chunks), pool, table, lens, max(ctxs), out=out)
+    torch.cuda.synchronize()
+    assert not torch.isnan(out).any()
+    pool_c, table_c, lens_c, out_c, q_c = pool.cpu(), table.cpu(), lens.cpu(), out.cpu(), q.cpu()
+    for i, c in enumerate(chunks):
+        if c == 0:
+            continue
+        s = starts[i]
+        ref = paged_prefill_ref(q_c[s:s + c].unsqueeze(0), pool_c, table_c[i:i + 1], lens_c[i:i + 1])
+        _check(out_c[s:s + c].unsqueeze(0), ref, torch.bfloat16)
