@@ -76,6 +76,32 @@ __device__ __forceinline__ uint32_t bits16(T x) {
 
 __device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// Two floats rounded to nearest-even and packed into one operand dword (one
+// v_cvt_pk per pair, where element-wise stores left shuffles behind).
+template <typename T>
+__device__ __forceinline__ uint32_t pack2(float a, float b);
+template <>
+__device__ __forceinline__ uint32_t pack2<bf16_t>(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, bf16x2));
+}
+template <>
+__device__ __forceinline__ uint32_t pack2<f16_t>(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, f16x2));
+}
+
+// max(a, b, c) in one instruction.  fmaxf on MFMA results first quiets each
+// input (one extra v_max per score); scores hold no signalling NaN, so the
+// raw instruction gives the same result.
+__device__ __forceinline__ float max3(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
 __device__ __forceinline__ bool page_ok(int pid, int num_pages) { return pid >= 0 && pid < num_pages; }
 
 template <typename T, int G, bool kBias, bool kVs, bool kSplit>
@@ -309,7 +335,6 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
     const float* fwt = fws + st_cur * kPfKT + 8 * half;
     const float* fbt = fbs + st_cur * kPfKT + 8 * half;
     // Base-2 logits y = x * c2 (+ bias * log2 e); the tile max of y.
-    float mloc = kNegInf;
     if (!interior) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
@@ -328,26 +353,36 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) sc[kb][v] = fmaf(sc[kb][v], c2, fbt[32 * kb + 16 * (v >> 3) + (v & 7)]);
     }
+    float ma = kNegInf, mb = kNegInf;  // two chains of max3
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int v = 0; v < 16; v += 2) mloc = fmaxf(mloc, fmaxf(sc[kb][v], sc[kb][v + 1]));
+      for (int v = 0; v < 16; v += 4) {
+        ma = max3(ma, sc[kb][v], sc[kb][v + 1]);
+        mb = max3(mb, sc[kb][v + 2], sc[kb][v + 3]);
+      }
+    float mloc = fmaxf(ma, mb);
     mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
     if (!kBias) mloc *= c2;  // without a bias, y = x * c2 and c2 > 0
     const float mnew = fmaxf(m_run, mloc);
     const float muse = mnew == kNegInf ? 0.0f : mnew;
     const float alpha = mnew == kNegInf ? 1.0f : __builtin_amdgcn_exp2f(m_run - mnew);
     float psum = 0.0f;
-    v8 pb[4];
+    u32x4 pb[4];  // p as the PV B operand, two keys per dword
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const float y = sc[kb][v];
-        float pr = __builtin_amdgcn_exp2f(kBias ? y - muse : fmaf(y, c2, -muse));
-        psum += pr;
-        if (kVs) pr *= fwt[32 * kb + 16 * (v >> 3) + (v & 7)];
-        pb[2 * kb + (v >> 3)][v & 7] = static_cast<T>(pr);
+      for (int v = 0; v < 16; v += 2) {
+        const float y0 = sc[kb][v], y1 = sc[kb][v + 1];
+        float p0 = __builtin_amdgcn_exp2f(kBias ? y0 - muse : fmaf(y0, c2, -muse));
+        float p1 = __builtin_amdgcn_exp2f(kBias ? y1 - muse : fmaf(y1, c2, -muse));
+        psum += p0;
+        psum += p1;
+        if (kVs) {
+          p0 *= fwt[32 * kb + 16 * (v >> 3) + (v & 7)];
+          p1 *= fwt[32 * kb + 16 * (v >> 3) + (v & 7) + 1];
+        }
+        pb[2 * kb + (v >> 3)][(v & 7) >> 1] = pack2<T>(p0, p1);
       }
     if (!qk_first) qk(st_nxt, sn);
     l_half = l_half * alpha + psum;
@@ -363,7 +398,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
         const v8 a = *reinterpret_cast<const v8*>(vr + 32 * db * kVRowW + 8 * (s ^ db));
-        oacc[db] = Mma32<T>::mma(a, pb[s], oacc[db]);
+        oacc[db] = Mma32<T>::mma(a, __builtin_bit_cast(v8, pb[s]), oacc[db]);
       }
 
     if (more) store(st_new);
