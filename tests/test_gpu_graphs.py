@@ -107,3 +107,25 @@ def test_graph_remap(dev):
         ops.rope_remap_paged(ref, orig, tgt, 500000.0, page_list=plist)
         torch.cuda.synchronize()
         assert torch.equal(pool, ref), f"replay {i}"
+
+
+def test_graph_prefill_split(dev):
+    """A small chunk on a long context (key range split, partials + combine)
+    captured once and replayed with new queries."""
+    from kessie_amd import ops
+
+    ctx, c = 20000, 128
+    q, pool, table, lens = decode_case(1, 32, 8, 128, ctx, 16, torch.bfloat16, dev, seed=11)
+    q = randn((1, c, 32, 128), torch.bfloat16, dev, 12)
+    vs = torch.rand(ctx, generator=torch.Generator(device=dev).manual_seed(13), device=dev)
+    out = torch.empty_like(q)
+    g = _capture(lambda: ops.fog_prefill(q, pool, table, lens, ctx, fog_vscale=vs, out=out))
+    for i in range(3):
+        q.copy_(randn(q.shape, torch.bfloat16, dev, 200 + i))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got = out.clone()
+        want = ops.fog_prefill(q, pool, table, lens, ctx, fog_vscale=vs)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"replay {i}"

@@ -286,3 +286,27 @@ def test_prefill_varlen_many_sequences(dev):
         s = starts[i]
         ref = paged_prefill_ref(q_c[s:s + c].unsqueeze(0), pool_c, table_c[i:i + 1], lens_c[i:i + 1])
         _check(out_c[s:s + c].unsqueeze(0), ref, torch.bfloat16)
+
+
+@pytest.mark.parametrize("hq,dtype,fog,causal,window", [(8, torch.bfloat16, "vscale", True, 0),
+                                                        (16, torch.float16, "bias", True, 300),
+                                                        (64, torch.bfloat16, "both", True, 0),
+                                                        (32, torch.float16, "none", False, 0)])
+def test_prefill_split_k_forced_shapes(dev, hq, dtype, fog, causal, window, monkeypatch):
+    """Three forced key splits for every GQA ratio and fog mode, fp16 and bf16,
+    ragged contexts, a window and the non-causal form: all rows against the
+    oracle."""
+    from kessie_amd import ops
+
+    monkeypatch.setenv("KESSIE_PREFILL_SPLITS", "3")
+    ctxs = [2000, 1337]
+    q, pool, table, lens = _case(dev, 2, 150, ctxs, hq, 8, dtype, seed=hq)
+    vs = torch.rand(2, 2000, generator=gen(dev, 41), device=dev) if fog in ("vscale", "both") else None
+    bias = fog_bias(2000, 0.5, 0.5, {5, 700, 1999}, 0.1).to(dev) if fog in ("bias", "both") else None
+    out = ops.fog_prefill(q, pool, table, lens, 2000, fog_vscale=vs, fog_bias=bias, window=window, causal=causal)
+    torch.cuda.synchronize()
+    for b in range(2):
+        ref = paged_prefill_ref(q[b:b + 1].cpu(), pool.cpu(), table[b:b + 1].cpu(), lens[b:b + 1].cpu(),
+                                None if vs is None else vs[b].cpu(), None if bias is None else bias.cpu(), window,
+                                causal=causal)
+        _check(out[b:b + 1], ref, dtype)
