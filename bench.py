@@ -425,6 +425,56 @@ def bench_prefill(dev, reps=3, c=2048, L=1 << 20, hq=32, hkv=8, d=128, cpu=False
                          "traffic": read_traffic("prefill_mfma_kernel"), "algorithmic_flops": flops}}
 
 
+def bench_dense(dev, reps=3, b=1, h=32, n=8192, d=128, cpu=False, cpu_heads=4):
+    """The reference's dense launcher launch_kessie_fused_fog_attn through
+    KeSSieKernels.fused_fog_attention: fp16 [B, H, N, D] with every position a
+    query, causal, V rows scaled by fog weights.  D=128 and N a multiple of 16
+    run on the MFMA prefill kernel with table-less pages."""
+    import torch
+
+    from kessie_amd.kessie_hip_ctypes import KeSSieKernels
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(3)
+    q, k, v = (torch.randn(b, h, n, d, generator=g, device=dev).half() for _ in range(3))
+    cf = n // 2
+    w = torch.ones(n, dtype=torch.float32, device=dev)
+    w[:cf] = (torch.arange(cf, dtype=torch.float32, device=dev) / max(cf - 1, 1)).pow(0.5)
+    kk = KeSSieKernels()
+    s = torch.cuda.current_stream()
+    kk.fused_fog_attention(q, k, v, w, stream=s)
+    torch.cuda.synchronize()
+    e0, e1 = events(reps), events(reps)
+    backlog()
+    for i in range(reps):
+        e0[i].record()
+        kk.fused_fog_attention(q, k, v, w, stream=s)
+        e1[i].record()
+    torch.cuda.synchronize()
+    ms = sum(a.elapsed_time(b_) for a, b_ in zip(e0, e1)) / reps
+    flops = b * h * 4 * d * (n * (n + 1) // 2)
+    tf = flops / (ms * 1e-3) / 1e12
+    res_cpu = None
+    if cpu:
+        from oracle.attention import fused_fog_attention_ref
+
+        cores = _cpu_threads()
+        qc, kc, vc = (x[:1, :cpu_heads].float().cpu() for x in (q, k, v))
+        wc = w.cpu()
+        t = time.perf_counter()
+        fused_fog_attention_ref(qc, kc, vc, wc)
+        sec = time.perf_counter() - t
+        flops_s = cpu_heads * 4 * d * (n * (n + 1) // 2)
+        res_cpu = {"value": round(flops_s / sec / 1e12, 4), "unit": "TFLOP/s", "cores": cores, "kind": "port",
+                   "sample": f"{cpu_heads} of the {h} heads (fp32 dense oracle: scores, causal mask, softmax, "
+                             f"@ V*w), one timed call", "seconds": round(sec, 2)}
+    return {"workload": f"dense fused fog attention fp16 (reference launcher), B={b} H={h} N={n:,} D={d}, causal",
+            "ms": round(ms, 3), "tflops": round(tf, 1), "cpu_baseline": res_cpu,
+            "roofline": {"bound": "mfma", "kernel": "prefill_mfma_kernel (table-less pages)", "achieved": round(tf, 1),
+                         "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 4),
+                         "traffic": None, "algorithmic_flops": flops}}
+
+
 def bench_decode_fp32(dev, reps=20, cpu=False):
     """Fog decode on the reference CPU path's shape, fp32: B=1, 32q/8kv, D=128,
     4,096-token context in 16-token pages."""
@@ -802,6 +852,7 @@ SECONDARY = {
     "gather": bench_gather_evict,
     "fp32": bench_decode_fp32,
     "prefill": bench_prefill,
+    "dense": bench_dense,
     "fog_bias": bench_fog_bias,
     "recall": bench_recall_inject,
     "index": bench_index_query,
@@ -905,6 +956,9 @@ def main():
         torch.cuda.empty_cache()
         log("secondary: chunked prefill 2048 x 1M")
         sec["prefill_1m"] = bench_prefill(dev, cpu=not args.no_cpu)
+        torch.cuda.empty_cache()
+        log("secondary: dense fused fog attention (reference launcher)")
+        sec["dense_fused_fog_8k"] = bench_dense(dev, cpu=not args.no_cpu)
         torch.cuda.empty_cache()
         log("secondary: fog bias producer")
         sec["fog_bias_131k"] = bench_fog_bias(dev)

@@ -40,6 +40,10 @@ struct Params {
   // q + b*q_bs): sequence b's queries are tokens q_start[b] - q_start[0] ..
   // q_start[b+1] - q_start[0] - 1 of q (and of out), C the longest of them.
   const int32_t* q_start;
+  // Table-less 16-token pages (page_table == nullptr, MFMA prefill only):
+  // page j of sequence b is page b * dense_ppb + j, as in a dense [B][H][N][D]
+  // tensor with page_stride = 16 * D and head_stride = N * D.
+  int dense_ppb;
   int window, causal;
   float sm_scale;
   int num_splits;

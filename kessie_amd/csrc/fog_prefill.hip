@@ -104,7 +104,7 @@ __device__ __forceinline__ float max3(float a, float b, float c) {
 
 __device__ __forceinline__ bool page_ok(int pid, int num_pages) { return pid >= 0 && pid < num_pages; }
 
-template <typename T, int G, bool kBias, bool kVs, bool kSplit>
+template <typename T, int G, bool kBias, bool kVs, bool kSplit, bool kDense>
 __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
   typedef typename Mma32<T>::v8 v8;
   typedef typename Mma32<T>::v4 v4;
@@ -211,7 +211,8 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
   const int kc = tid & 15, kr = tid >> 4;
   const T* kbase = static_cast<const T*>(p.k) + (int64_t)g * p.head_stride + 8 * kc;
   const T* vbase = static_cast<const T*>(p.v) + (int64_t)g * p.head_stride + 8 * kc;
-  const int32_t* table = p.page_table + (int64_t)b * p.table_stride;
+  const int32_t* table = kDense ? nullptr : p.page_table + (int64_t)b * p.table_stride;
+  const int dense0 = kDense ? b * p.dense_ppb : 0;  // table-less pages: sequence b's first
   const int kslot = wave >> 2, vslot = wave >> 1;
 
   // Page ids of a tile (4 uniform values; -1 past the end).
@@ -219,7 +220,8 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
     const int pg0 = (t_begin + tile * kPfKT) >> 4;
     i32x4 ids;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) ids[j] = (tile < n_tiles && pg0 + j < n_tab) ? table[pg0 + j] : -1;
+    for (int j = 0; j < 4; ++j)
+      ids[j] = (tile < n_tiles && pg0 + j < n_tab) ? (kDense ? dense0 + pg0 + j : table[pg0 + j]) : -1;
     return ids;
   };
   auto valid_mask = [&](i32x4 ids) {
@@ -447,12 +449,12 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
     }
 }
 
-template <typename T, int G, bool kBias, bool kVs, bool kSplit>
+template <typename T, int G, bool kBias, bool kVs, bool kSplit, bool kDense = false>
 int launch_one(const Params& p, dim3 grid, hipStream_t stream) {
   static bool lds_set[64] = {};  // per instance and device
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-  const void* fn = reinterpret_cast<const void*>(prefill_mfma_kernel<T, G, kBias, kVs, kSplit>);
+  const void* fn = reinterpret_cast<const void*>(prefill_mfma_kernel<T, G, kBias, kVs, kSplit, kDense>);
   if (!lds_set[dev]) {
     if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPfLdsBytes) != hipSuccess) {
       set_error(KESSIE_ERR_HIP, "fog prefill (mfma): %zu bytes of LDS unavailable", kPfLdsBytes);
@@ -460,7 +462,7 @@ int launch_one(const Params& p, dim3 grid, hipStream_t stream) {
     }
     lds_set[dev] = true;
   }
-  hipLaunchKernelGGL((prefill_mfma_kernel<T, G, kBias, kVs, kSplit>), grid, dim3(kPfThreads), kPfLdsBytes, stream, p);
+  hipLaunchKernelGGL((prefill_mfma_kernel<T, G, kBias, kVs, kSplit, kDense>), grid, dim3(kPfThreads), kPfLdsBytes, stream, p);
   return check_launch("fog prefill (mfma)");
 }
 
@@ -485,6 +487,9 @@ int launch_prefill(Params& p, hipStream_t stream) {
   const int kpos = kPfRows / p.G;
   // Varlen: the live (sequence, query tile) pairs are numbered along x.
   dim3 grid(div_up(p.C, kpos) * p.Hkv * (p.q_start ? p.B : 1), p.q_start ? 1 : p.B, max(p.num_splits, 1));
+  if (p.page_table == nullptr)  // table-less pages (dense launchers): G 1, no bias, one split
+    return p.vscale ? launch_one<T, 1, false, true, false, true>(p, grid, stream)
+                    : launch_one<T, 1, false, false, false, true>(p, grid, stream);
   switch (p.G) {
     case 1: return launch_split<T, 1>(p, grid, stream);
     case 2: return launch_split<T, 2>(p, grid, stream);
@@ -501,7 +506,9 @@ int launch_prefill(Params& p, hipStream_t stream) {
 bool prefill_mfma_ok(const Params& p, int dtype) {
   if (env_int("KESSIE_FORCE_GENERIC", 0)) return false;
   if (dtype != KESSIE_DTYPE_BF16 && dtype != KESSIE_DTYPE_F16) return false;
-  if (p.D != 128 || p.page_size != 16 || p.page_table == nullptr) return false;
+  if (p.D != 128 || p.page_size != 16) return false;
+  // Table-less pages: instantiated for the dense launchers' form only.
+  if (p.page_table == nullptr && (p.dense_ppb <= 0 || p.G != 1 || p.bias || p.num_splits > 1)) return false;
   if (!(p.G == 1 || p.G == 2 || p.G == 4 || p.G == 8)) return false;
   if (!(p.sm_scale > 0.0f)) return false;
   if (!aligned16(p.q) || !aligned16(p.k) || !aligned16(p.v) || !aligned16(p.out)) return false;
