@@ -204,7 +204,9 @@ int kessie_fog_prefill_paged(
  * query_start_loc[0] .. query_start_loc[b+1] - query_start_loc[0] - 1 of
  * q/out ([T][Hq][D] contiguous; query_start_loc int32 [batch+1],
  * non-decreasing, on the device, e.g. a slice of vLLM's), chunk length C_b = query_start_loc[b+1] -
- * query_start_loc[b] <= max_query_len, query i of it at ctx_lens[b] - C_b + i.
+ * query_start_loc[b] <= max_query_len, query i of it at ctx_lens[b] - C_b + i
+ * (a longer chunk is read as its first max_query_len queries at positions
+ * ctx_lens[b] - max_query_len + i; its other rows are not written).
  * MFMA shapes only (bf16/fp16, head_dim 128, 16-token pages, GQA 1/2/4/8,
  * 16-byte aligned rows); other shapes return KESSIE_ERR_UNSUPPORTED without
  * launching (call kessie_fog_prefill_paged per sequence instead).  The

@@ -244,7 +244,7 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(Params p) {
   int b = (int)(bi / p.C);
   if (p.q_start) {  // varlen prefill: rows past the chunk have no partials
     const int s0 = p.q_start[b] - p.q_start[0];
-    if (i >= p.q_start[b + 1] - p.q_start[b]) return;  // uniform, before any barrier
+    if (i >= p.q_start[b + 1] - p.q_start[b]) return;  // uniform, before any barrier (i < max_query_len)
     i += s0;
     b = 0;
   }

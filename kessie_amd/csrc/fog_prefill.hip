@@ -134,7 +134,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
     int found = -1, before = 0;
     for (int b0 = 0; b0 < p.B; b0 += 64) {
       const int bb = b0 + lane;
-      const int nt = bb < p.B ? div_up(p.q_start[bb + 1] - p.q_start[bb], kPos) : 0;
+      const int nt = bb < p.B ? div_up(min(max(p.q_start[bb + 1] - p.q_start[bb], 0), p.C), kPos) : 0;
       int inc = nt;
 #pragma unroll
       for (int o = 1; o < 64; o <<= 1) {
@@ -158,7 +158,9 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
   int64_t q_off = (int64_t)b * p.q_bs, o_off = (int64_t)b * p.o_bs;
   if (p.q_start) {
     const int s0 = p.q_start[b] - p.q_start[0];
-    C = p.q_start[b + 1] - p.q_start[b];
+    // Chunks are clamped to [0, max_query_len]: partial rows (split) are
+    // indexed by it, so a longer chunk must not reach past them.
+    C = min(max(p.q_start[b + 1] - p.q_start[b], 0), p.C);
     q_off = (int64_t)s0 * p.q_is;
     o_off = (int64_t)s0 * p.o_is;
   }

@@ -310,3 +310,26 @@ def test_prefill_split_k_forced_shapes(dev, hq, dtype, fog, causal, window, monk
                                 None if vs is None else vs[b].cpu(), None if bias is None else bias.cpu(), window,
                                 causal=causal)
         _check(out[b:b + 1], ref, dtype)
+
+
+def test_prefill_varlen_chunk_longer_than_max_query_len(dev, monkeypatch):
+    """A chunk longer than max_query_len is read as its first max_query_len
+    queries at the last max_query_len positions of its context (the rest of
+    its rows untouched) and the other sequences are unaffected, also when the
+    key range is split: partial rows are indexed by max_query_len and must not
+    overrun the workspace."""
+    from kessie_amd import ops
+
+    monkeypatch.setenv("KESSIE_PREFILL_SPLITS", "4")
+    chunks, ctxs, mq = [300, 50], [3000, 2000], 200
+    _, pool, table, lens = _case(dev, 2, 1, ctxs, 32, 8, torch.bfloat16, seed=51)
+    qsl = torch.tensor([0, 300, 350], dtype=torch.int32, device=dev)
+    q = torch.randn(350, 32, 128, generator=gen(dev, 52), device=dev).to(torch.bfloat16)
+    out = torch.full_like(q, float("nan"))
+    assert ops.fog_prefill_varlen(q, qsl, mq, pool, table, lens, 3000, out=out)
+    torch.cuda.synchronize()
+    assert torch.isnan(out[mq:300]).all()
+    ref0 = paged_prefill_ref(q[:mq].unsqueeze(0).cpu(), pool.cpu(), table[:1].cpu(), lens[:1].cpu())
+    _check(out[:mq].unsqueeze(0), ref0, torch.bfloat16)
+    ref1 = paged_prefill_ref(q[300:].unsqueeze(0).cpu(), pool.cpu(), table[1:].cpu(), lens[1:].cpu())
+    _check(out[300:].unsqueeze(0), ref1, torch.bfloat16)
