@@ -222,7 +222,7 @@ __global__ __launch_bounds__(kGenThreads) void attn_generic_kernel(Params p) {
 // Split combine
 // ---------------------------------------------------------------------------
 constexpr int kCombineThreads = 256;
-constexpr int kMaxSplits = 256;
+constexpr int kMaxSplits = 512;
 
 // Workgroup (row, y) merges d in [y*D/Y, (y+1)*D/Y) of one row (Y =
 // gridDim.y, 1 unless rows are few).  With an even chunk its 256 lanes are
@@ -303,11 +303,11 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(Params p) {
   }
 }
 
-// Workgroups per row of the combine: split head_dim into up to four even
+// Workgroups per row of the combine: split head_dim into up to eight even
 // chunks when the rows alone would leave the chip mostly idle.
 inline int combine_dsplit(int64_t rows, int D) {
   int y = 1;
-  while (y < 4 && rows * y < 256 && D % (4 * y) == 0) y *= 2;  // the chunk D/y stays even
+  while (y < 8 && rows * y < 256 && D % (4 * y) == 0) y *= 2;  // the chunk D/y stays even
   return y;
 }
 
