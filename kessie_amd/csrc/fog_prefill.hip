@@ -182,9 +182,11 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
   const int S = kSplit ? (int)gridDim.z : 1, split = kSplit ? (int)blockIdx.z : 0;
   int first = 0;
   if (kSplit) {
-    const int per = div_up(n_tiles, S);
-    first = min(n_tiles, split * per);
-    n_tiles = min(n_tiles, first + per) - first;
+    // (The division runs on the vector unit; readfirstlane returns the
+    // uniform bounds to scalar registers.)
+    const int per = __builtin_amdgcn_readfirstlane(div_up(n_tiles, S));
+    first = __builtin_amdgcn_readfirstlane(min(n_tiles, split * per));
+    n_tiles = __builtin_amdgcn_readfirstlane(min(n_tiles, first + per) - first);
   }
   const int t_begin = (tile_lo + first) * kPfKT;
   const int n_tab = div_up(hi, 16);  // table entries that may be read
