@@ -26,6 +26,15 @@
 // Grid index x = qtile * Hkv + g, so with 8 kv heads (and the hardware's
 // round-robin of workgroups over the 8 XCDs) every workgroup of kv head g
 // sits on one XCD and the query tiles of that head share its keys in L2.
+//
+// Variants (template and Params):
+//   kSplit   grid z splits each query tile's key tiles; every split stores
+//            unnormalised partials (O, max, sum) merged by the combine kernel
+//            -- used when the chunks alone would leave CUs idle;
+//   q_start  varlen batch: x / Hkv numbers the live (sequence, query tile)
+//            pairs, each chunk's queries packed at query_start_loc;
+//   kDense   table-less pages (page b * dense_ppb + j) for the reference's
+//            dense [B][H][N][D] launchers, query tiles longest first.
 #include "attn_common.h"
 
 namespace kessie {

@@ -245,7 +245,10 @@ def fog_prefill(q: torch.Tensor, pool: torch.Tensor, page_table: torch.Tensor, c
                 sm_scale: Optional[float] = None, layout: str = "native",
                 out: Optional[torch.Tensor] = None, ws: Optional[torch.Tensor] = None,
                 stream=None) -> torch.Tensor:
-    """Chunked prefill: q [B, C, Hq, D]; query i of sequence b sits at ctx_lens[b]-C+i."""
+    """Chunked prefill: q [B, C, Hq, D]; query i of sequence b sits at ctx_lens[b]-C+i.
+
+    ws: workspace for split partials (a cached one when None); the MFMA kernel
+    uses it only when the chunk is too small to fill the device."""
     pv = pool_view(pool, layout)
     q = _contig(q, "q")
     b, c, hq, d = q.shape
