@@ -424,12 +424,15 @@ class KeSSieAttentionImpl:
             output = torch.empty(query.shape[0], hq * d, dtype=query.dtype, device=query.device)
         out = output[:n_tok].view(n_tok, hq, d)
         layout = _kv_layout(kv_cache)
+        # One stream lookup per call (each torch.cuda.current_stream costs a
+        # few microseconds of host time, which short contexts notice).
+        sp = torch.cuda.current_stream(query.device).cuda_stream
 
         # New K/V rows into the cache (skipped for layers that share a cache).
         if key is not None and value is not None:
             ops.kv_cache_write(kv_cache, key[:n_tok].reshape(n_tok, self.num_kv_heads, d),
                                value[:n_tok].reshape(n_tok, self.num_kv_heads, d), meta.slot_mapping[:n_tok],
-                               layout=layout)
+                               layout=layout, stream=sp)
 
         kv_len = int(meta.max_seq_len)
         bias = None
@@ -447,13 +450,13 @@ class KeSSieAttentionImpl:
                 q_dec = q[qsl[lo]:qsl[lo] + (hi - lo)]
                 ops.fog_decode(q_dec, kv_cache, table[lo:hi], lens[lo:hi], kv_len, fog_bias=bias,
                                window=self.window, sm_scale=self.scale, layout=layout,
-                               out=out[qsl[lo]:qsl[lo] + (hi - lo)])
+                               out=out[qsl[lo]:qsl[lo] + (hi - lo)], stream=sp)
             else:
                 idx = torch.tensor(decode, device=q.device)
                 rows = torch.tensor([qsl[i] for i in decode], device=q.device)
                 o_dec = ops.fog_decode(q.index_select(0, rows).contiguous(), kv_cache, table.index_select(0, idx),
                                        lens.index_select(0, idx), kv_len, fog_bias=bias, window=self.window,
-                                       sm_scale=self.scale, layout=layout)
+                                       sm_scale=self.scale, layout=layout, stream=sp)
                 out.index_copy_(0, rows, o_dec)
         if len(prefill) > 1 and prefill == list(range(prefill[0], prefill[-1] + 1)):
             # One launch for the whole run of prefill sequences (their chunk
@@ -465,11 +468,12 @@ class KeSSieAttentionImpl:
                 qs = qs.to(torch.int32)
             if ops.fog_prefill_varlen(q[s0:s1], qs, max(qsl[i + 1] - qsl[i] for i in prefill), kv_cache,
                                       table[lo:hi], lens[lo:hi], kv_len, fog_bias=bias, window=self.window,
-                                      causal=True, sm_scale=self.scale, layout=layout, out=out[s0:s1]):
+                                      causal=True, sm_scale=self.scale, layout=layout, out=out[s0:s1],
+                                      stream=sp):
                 prefill = []
         for i in prefill:
             s, e = qsl[i], qsl[i + 1]
             ops.fog_prefill(q[s:e].unsqueeze(0), kv_cache, table[i:i + 1], lens[i:i + 1], kv_len, fog_bias=bias,
                             window=self.window, causal=True, sm_scale=self.scale, layout=layout,
-                            out=out[s:e].unsqueeze(0))
+                            out=out[s:e].unsqueeze(0), stream=sp)
         return output

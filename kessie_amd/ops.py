@@ -51,12 +51,12 @@ def _contig(t: torch.Tensor, name: str) -> torch.Tensor:
 
 
 def _stream_ptr(stream, device) -> C.c_void_p:
+    if isinstance(stream, int):
+        return C.c_void_p(stream)
     if stream is None:
         stream = torch.cuda.current_stream(device)
     if isinstance(stream, torch.cuda.Stream):
         return C.c_void_p(stream.cuda_stream)
-    if isinstance(stream, int):
-        return C.c_void_p(stream)
     raise TypeError(f"stream must be a torch.cuda.Stream, an int handle or None, got {type(stream)}")
 
 
