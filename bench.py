@@ -428,8 +428,8 @@ def bench_prefill(dev, reps=3, c=2048, L=1 << 20, hq=32, hkv=8, d=128, cpu=False
 def bench_dense(dev, reps=3, b=1, h=32, n=8192, d=128, cpu=False, cpu_heads=4):
     """The reference's dense launcher launch_kessie_fused_fog_attn through
     KeSSieKernels.fused_fog_attention: fp16 [B, H, N, D] with every position a
-    query, causal, V rows scaled by fog weights.  D=128 and N a multiple of 16
-    run on the MFMA prefill kernel with table-less pages."""
+    query, causal, V rows scaled by fog weights.  D=128 with H*N a multiple of
+    16 runs on the MFMA prefill kernel with table-less pages."""
     import torch
 
     from kessie_amd.kessie_hip_ctypes import KeSSieKernels

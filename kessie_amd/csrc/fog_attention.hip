@@ -1127,16 +1127,18 @@ static void dense_fp16(const void* Q, const void* K, const void* V, void* O, con
     set_error(KESSIE_ERR_INVALID, "dense attention: null pointer or window %d", window);
     return;
   }
-  // head_dim 128 in whole 16-token pages: the MFMA prefill kernel, reading the
-  // dense tensors as table-less pages (page b*H*N/16 + j = tokens 16j..16j+15
-  // of every head of sequence b, heads N*D apart).  One key split: these
-  // launchers take no workspace.
-  if (D == 128 && N % 16 == 0 && (int64_t)B * H * (N / 16) <= INT_MAX) {
+  // head_dim 128: the MFMA prefill kernel, reading the dense tensors as
+  // table-less 16-token pages (page b*H*N/16 + j = tokens 16j..16j+15 of every
+  // head of sequence b, heads N*D apart; H*N a multiple of 16 keeps sequences
+  // on whole pages, and the kernel reads no token past N).  One key split:
+  // these launchers take no workspace.
+  const int64_t dense_pages = (int64_t)B * H * N / 16;
+  if (D == 128 && ((int64_t)H * N) % 16 == 0 && dense_pages <= INT_MAX) {
     Params m = p;
     m.page_size = 16;
     m.page_stride = 16 * (int64_t)D;
-    m.num_pages = B * H * (N / 16);
-    m.dense_ppb = H * (N / 16);
+    m.num_pages = (int)dense_pages;
+    m.dense_ppb = (int)(((int64_t)H * N) / 16);
     if (prefill_mfma_ok(m, KESSIE_DTYPE_F16)) {
       prefill_mfma(m, KESSIE_DTYPE_F16, as_stream(stream));  // records any launch error
       return;

@@ -256,7 +256,10 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
       const int pid = uniform(kslot ? ids[2 * r + 1] : ids[2 * r]);
-      if (page_ok(pid, p.num_pages)) {
+      // Dense pages may end inside the last one: tokens past the key range
+      // are not read (past the tensor's end for its last head).
+      const bool kin = !kDense || t0 + 32 * r + kr < hi;
+      if (page_ok(pid, p.num_pages) && kin) {
         kreg[r] = *reinterpret_cast<const v8*>(kbase + (int64_t)pid * p.page_stride + (int64_t)(kr & 15) * p.tok_stride);
       } else {
 #pragma unroll
@@ -267,8 +270,16 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
       const int pid = uniform(vslot & 2 ? (vslot & 1 ? ids[3] : ids[2]) : (vslot & 1 ? ids[1] : ids[0]));
       if (page_ok(pid, p.num_pages)) {
         const T* vp = vbase + (int64_t)pid * p.page_stride + (int64_t)((2 * kr) & 15) * p.tok_stride;
-        vreg[0] = *reinterpret_cast<const v8*>(vp);
-        vreg[1] = *reinterpret_cast<const v8*>(vp + p.tok_stride);
+        if (kDense) {
+          const int vkey = t0 + 16 * vslot + ((2 * kr) & 15);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) vreg[0][e] = vreg[1][e] = static_cast<T>(0.0f);
+          if (vkey < hi) vreg[0] = *reinterpret_cast<const v8*>(vp);
+          if (vkey + 1 < hi) vreg[1] = *reinterpret_cast<const v8*>(vp + p.tok_stride);
+        } else {
+          vreg[0] = *reinterpret_cast<const v8*>(vp);
+          vreg[1] = *reinterpret_cast<const v8*>(vp + p.tok_stride);
+        }
       } else {
 #pragma unroll
         for (int e = 0; e < 8; ++e) vreg[0][e] = vreg[1][e] = static_cast<T>(0.0f);

@@ -1,7 +1,7 @@
 """GPU parity: the reference's dense launchers (launch_kessie_windowed_attn,
 launch_kessie_fused_fog_attn: fp16 [B, H, N, D], every position a query)
 through KeSSieKernels vs the CPU oracle (fp32 on upcast inputs).  head_dim 128
-with N a multiple of 16 runs on the MFMA prefill kernel (table-less pages),
+with H*N a multiple of 16 runs on the MFMA prefill kernel (table-less pages),
 other shapes on the generic kernel.  Tolerance |gpu - ref| <= 2e-2 + 1e-2*|ref|."""
 import pytest
 import torch
@@ -23,7 +23,10 @@ def _qkv(dev, b, h, n, d, seed):
     return [torch.randn(b, h, n, d, generator=gen(dev, seed + i), device=dev).to(torch.float16) for i in range(3)]
 
 
-SHAPES = [(2, 4, 256, 128), (1, 3, 1024, 128), (2, 2, 100, 128), (2, 3, 64, 64), (1, 2, 48, 64)]
+# MFMA route: D = 128 and H*N a multiple of 16 (N itself need not be: the last
+# page of every head ends inside it); the rest run on the generic kernel.
+SHAPES = [(2, 4, 256, 128), (1, 3, 1024, 128), (2, 32, 100, 128), (1, 4, 1000, 128), (3, 16, 37, 128),
+          (2, 2, 100, 128), (2, 3, 64, 64), (1, 2, 48, 64)]
 
 
 @pytest.mark.parametrize("b,h,n,d", SHAPES)
