@@ -129,3 +129,36 @@ def test_graph_prefill_split(dev):
         want = ops.fog_prefill(q, pool, table, lens, ctx, fog_vscale=vs)
         torch.cuda.synchronize()
         assert torch.equal(got, want), f"replay {i}"
+
+
+def test_graph_prefill_varlen_split(dev, monkeypatch):
+    """The serving path's prefill launch (varlen, key range split in two,
+    partials + combine) captured once and replayed with new queries."""
+    from kessie_amd import ops
+
+    monkeypatch.setenv("KESSIE_PREFILL_SPLITS", "2")
+    chunks, ctxs = [96, 1, 200], [5000, 3000, 7000]
+    pages = [(c + 15) // 16 for c in ctxs]
+    pool = paged_pool(sum(pages) + 4, 16, 8, 128, torch.bfloat16, dev, seed=41)
+    perm = randperm(sum(pages) + 4, dev, 42)
+    table = torch.full((3, max(pages)), -1, dtype=torch.int32, device=dev)
+    at = 0
+    for i, n in enumerate(pages):
+        table[i, :n] = perm[at:at + n]
+        at += n
+    lens = torch.tensor(ctxs, dtype=torch.int32, device=dev)
+    qsl = torch.tensor([0, 96, 97, 297], dtype=torch.int32, device=dev)
+    q = randn((297, 32, 128), torch.bfloat16, dev, 43)
+    bias = torch.randn(max(ctxs), generator=torch.Generator(device=dev).manual_seed(44), device=dev) * 0.1
+    out = torch.empty_like(q)
+    g = _capture(lambda: ops.fog_prefill_varlen(q, qsl, 200, pool, table, lens, max(ctxs), fog_bias=bias, out=out))
+    for i in range(3):
+        q.copy_(randn(q.shape, torch.bfloat16, dev, 300 + i))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got = out.clone()
+        want = torch.empty_like(q)
+        ops.fog_prefill_varlen(q, qsl, 200, pool, table, lens, max(ctxs), fog_bias=bias, out=want)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"replay {i}"
