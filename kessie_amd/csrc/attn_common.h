@@ -44,6 +44,9 @@ struct Params {
   // page j of sequence b is page b * dense_ppb + j, as in a dense [B][H][N][D]
   // tensor with page_stride = 16 * D and head_stride = N * D.
   int dense_ppb;
+  // Causal chunk covering most of its context over several grid rounds: the
+  // MFMA prefill dispatches its query tiles longest first (host-set).
+  int reverse_q;
   int window, causal;
   float sm_scale;
   int num_splits;

@@ -927,6 +927,11 @@ static int run_prefill_mfma(kessie::attn::Params& p, int dtype, void* workspace,
   p.num_splits = prefill_mfma_splits(p.B, p.C, p.Hkv, p.G, p.max_ctx);
   p.direct_out = p.num_splits == 1 ? 1 : 0;
   p.launch_combine = 0;
+  // Longest query tiles first when the causal triangle dominates (the chunk is
+  // at least half its context) and the grid takes more than one round: +4-11 %
+  // on fresh prompts; with one round it only costs.
+  const int64_t wgs = (int64_t)div_up(p.C, 256 / p.G) * p.Hkv * p.B;
+  p.reverse_q = p.causal && p.direct_out && !p.q_start && wgs > device_cus() && 2 * (int64_t)p.C >= p.max_ctx;
   const int64_t rows = (int64_t)p.B * p.C * p.Hq;
   if (!p.direct_out) {
     const size_t need = partial_bytes(rows, p.num_splits, p.D);

@@ -33,8 +33,10 @@
 //            -- used when the chunks alone would leave CUs idle;
 //   q_start  varlen batch: x / Hkv numbers the live (sequence, query tile)
 //            pairs, each chunk's queries packed at query_start_loc;
-//   kDense   table-less pages (page b * dense_ppb + j) for the reference's
-//            dense [B][H][N][D] launchers, query tiles longest first.
+//   kMode    0 paged; 1 table-less pages (page b * dense_ppb + j) for the
+//            reference's dense [B][H][N][D] launchers, query tiles longest
+//            first; 2 paged with query tiles longest first (a causal chunk
+//            that is most of its context and takes several grid rounds).
 #include "attn_common.h"
 
 namespace kessie {
@@ -113,8 +115,9 @@ __device__ __forceinline__ float max3(float a, float b, float c) {
 
 __device__ __forceinline__ bool page_ok(int pid, int num_pages) { return pid >= 0 && pid < num_pages; }
 
-template <typename T, int G, bool kBias, bool kVs, bool kSplit, bool kDense>
+template <typename T, int G, bool kBias, bool kVs, bool kSplit, int kMode>
 __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
+  constexpr bool kDense = kMode == 1;
   typedef typename Mma32<T>::v8 v8;
   typedef typename Mma32<T>::v4 v4;
   constexpr int kPos = kPfRows / G;  // query positions per workgroup
@@ -134,7 +137,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
   // dispatching them first keeps the short ones for the tail of the grid
   // (+15-19 %).  Not in the paged instances: there the same two lines cost the
   // long-context shape 1-2 % through code generation.
-  if (kDense && p.causal) qtile = (int)(gridDim.x / p.Hkv) - 1 - qtile;
+  if ((kDense && p.causal) || kMode == 2) qtile = (int)(gridDim.x / p.Hkv) - 1 - qtile;
   if (p.q_start) {
     // Varlen: x / Hkv numbers the live (sequence, query tile) pairs in order,
     // so the grid's surplus workgroups all sit at its end and exit at once
@@ -478,12 +481,12 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
     }
 }
 
-template <typename T, int G, bool kBias, bool kVs, bool kSplit, bool kDense = false>
+template <typename T, int G, bool kBias, bool kVs, bool kSplit, int kMode = 0>
 int launch_one(const Params& p, dim3 grid, hipStream_t stream) {
   static bool lds_set[64] = {};  // per instance and device
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-  const void* fn = reinterpret_cast<const void*>(prefill_mfma_kernel<T, G, kBias, kVs, kSplit, kDense>);
+  const void* fn = reinterpret_cast<const void*>(prefill_mfma_kernel<T, G, kBias, kVs, kSplit, kMode>);
   if (!lds_set[dev]) {
     if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPfLdsBytes) != hipSuccess) {
       set_error(KESSIE_ERR_HIP, "fog prefill (mfma): %zu bytes of LDS unavailable", kPfLdsBytes);
@@ -491,24 +494,26 @@ int launch_one(const Params& p, dim3 grid, hipStream_t stream) {
     }
     lds_set[dev] = true;
   }
-  hipLaunchKernelGGL((prefill_mfma_kernel<T, G, kBias, kVs, kSplit, kDense>), grid, dim3(kPfThreads), kPfLdsBytes, stream, p);
+  hipLaunchKernelGGL((prefill_mfma_kernel<T, G, kBias, kVs, kSplit, kMode>), grid, dim3(kPfThreads), kPfLdsBytes, stream, p);
   return check_launch("fog prefill (mfma)");
 }
 
-template <typename T, int G, bool kSplit>
+template <typename T, int G, bool kSplit, int kMode = 0>
 int launch_fog(const Params& p, dim3 grid, hipStream_t stream) {
   if (p.bias)
-    return p.vscale ? launch_one<T, G, true, true, kSplit>(p, grid, stream)
-                    : launch_one<T, G, true, false, kSplit>(p, grid, stream);
-  return p.vscale ? launch_one<T, G, false, true, kSplit>(p, grid, stream)
-                  : launch_one<T, G, false, false, kSplit>(p, grid, stream);
+    return p.vscale ? launch_one<T, G, true, true, kSplit, kMode>(p, grid, stream)
+                    : launch_one<T, G, true, false, kSplit, kMode>(p, grid, stream);
+  return p.vscale ? launch_one<T, G, false, true, kSplit, kMode>(p, grid, stream)
+                  : launch_one<T, G, false, false, kSplit, kMode>(p, grid, stream);
 }
 
-// The split instances are separate: the unsplit loop keeps the register
-// allocation it was tuned with (the shared form cost the V-fog instance 6%).
+// The split and longest-first instances are separate: the plain loop keeps the
+// register allocation it was tuned with (folding either into it cost the
+// V-fog long-context shape 1-6 %).
 template <typename T, int G>
 int launch_split(const Params& p, dim3 grid, hipStream_t stream) {
-  return p.direct_out ? launch_fog<T, G, false>(p, grid, stream) : launch_fog<T, G, true>(p, grid, stream);
+  if (!p.direct_out) return launch_fog<T, G, true>(p, grid, stream);
+  return p.reverse_q ? launch_fog<T, G, false, 2>(p, grid, stream) : launch_fog<T, G, false>(p, grid, stream);
 }
 
 template <typename T>
@@ -517,8 +522,8 @@ int launch_prefill(Params& p, hipStream_t stream) {
   // Varlen: the live (sequence, query tile) pairs are numbered along x.
   dim3 grid(div_up(p.C, kpos) * p.Hkv * (p.q_start ? p.B : 1), p.q_start ? 1 : p.B, max(p.num_splits, 1));
   if (p.page_table == nullptr)  // table-less pages (dense launchers): G 1, no bias, one split
-    return p.vscale ? launch_one<T, 1, false, true, false, true>(p, grid, stream)
-                    : launch_one<T, 1, false, false, false, true>(p, grid, stream);
+    return p.vscale ? launch_one<T, 1, false, true, false, 1>(p, grid, stream)
+                    : launch_one<T, 1, false, false, false, 1>(p, grid, stream);
   switch (p.G) {
     case 1: return launch_split<T, 1>(p, grid, stream);
     case 2: return launch_split<T, 2>(p, grid, stream);

@@ -333,3 +333,27 @@ def test_prefill_varlen_chunk_longer_than_max_query_len(dev, monkeypatch):
     _check(out[:mq].unsqueeze(0), ref0, torch.bfloat16)
     ref1 = paged_prefill_ref(q[300:].unsqueeze(0).cpu(), pool.cpu(), table[1:].cpu(), lens[1:].cpu())
     _check(out[300:].unsqueeze(0), ref1, torch.bfloat16)
+
+
+def test_prefill_longest_first_dispatch(dev, monkeypatch):
+    """A causal batch whose chunks are most of their contexts and whose grid
+    takes several rounds dispatches query tiles longest first: same arithmetic
+    per tile, so it equals one-sequence launches (one round, plain order, held
+    to one key split) bit for bit, and the oracle on sampled rows."""
+    from kessie_amd import ops
+
+    monkeypatch.setenv("KESSIE_PREFILL_SPLITS", "1")
+    c, ctxs = 1500, [1500, 2000, 2900]
+    q, pool, table, lens = _case(dev, 3, c, ctxs, 32, 8, torch.bfloat16, seed=61)
+    vs = torch.rand(3, 2900, generator=gen(dev, 62), device=dev)
+    out = ops.fog_prefill(q, pool, table, lens, 2900, fog_vscale=vs)
+    torch.cuda.synchronize()
+    rows = torch.tensor([0, 700, 1499])
+    for i in range(3):
+        one = ops.fog_prefill(q[i:i + 1].contiguous(), pool, table[i:i + 1], lens[i:i + 1], 2900,
+                              fog_vscale=vs[i:i + 1])
+        torch.cuda.synchronize()
+        assert torch.equal(out[i:i + 1], one), f"sequence {i}"
+        ref = paged_prefill_ref(q[i:i + 1].cpu(), pool.cpu(), table[i:i + 1].cpu(), lens[i:i + 1].cpu(),
+                                vs[i].cpu(), None, 0, rows=rows)
+        _check(out[i:i + 1, rows], ref, torch.bfloat16)
