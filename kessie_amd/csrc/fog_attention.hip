@@ -702,7 +702,7 @@ bool decode_mfma_ok(const Params& p, int dtype) {
   if (env_int("KESSIE_FORCE_GENERIC", 0)) return false;
   if (dtype != KESSIE_DTYPE_BF16 && dtype != KESSIE_DTYPE_F16) return false;
   if (p.D != 128 || p.page_size != 16 || p.page_table == nullptr) return false;
-  if (!(p.G == 1 || p.G == 2 || p.G == 4 || p.G == 8)) return false;  // G=16 would spill
+  if (!(p.G == 1 || p.G == 2 || p.G == 4 || p.G == 8 || p.G == 16)) return false;
   if (!aligned16(p.q) || !aligned16(p.k) || !aligned16(p.v) || !aligned16(p.out)) return false;
   if (p.page_stride % 8 || p.tok_stride % 8 || p.head_stride % 8 || p.q_bs % 8 || p.q_hs % 8 || p.o_bs % 8 ||
       p.o_hs % 8)
@@ -717,6 +717,7 @@ int run_decode_mfma(Params& p, hipStream_t s) {
     case 2: return launch_decode_mfma<T, 2>(p, s);
     case 4: return launch_decode_mfma<T, 4>(p, s);
     case 8: return launch_decode_mfma<T, 8>(p, s);
+    case 16: return launch_decode_mfma<T, 16>(p, s);
   }
   set_error(KESSIE_ERR_UNSUPPORTED, "fog decode: GQA ratio %d", p.G);
   return KESSIE_ERR_UNSUPPORTED;
@@ -1073,7 +1074,7 @@ extern "C" int kessie_fog_prefill_varlen(const void* q, const int32_t* query_sta
   if (batch == 0 || max_query_len == 0) return KESSIE_OK;
   KESSIE_REQUIRE(prefill_mfma_ok(p, dtype), KESSIE_ERR_UNSUPPORTED,
                  "fog prefill varlen: shape not taken by the MFMA kernel (bf16/fp16, head_dim 128, 16-token pages, "
-                 "GQA 1/2/4/8, 16-byte aligned rows)");
+                 "GQA 1/2/4/8/16, 16-byte aligned rows)");
   return run_prefill_mfma(p, dtype, workspace, workspace_bytes, stream);
 }
 

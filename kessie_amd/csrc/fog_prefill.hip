@@ -1,5 +1,5 @@
 // Chunked-prefill fog attention on MFMA for gfx950 (bf16 / f16, head_dim 128,
-// 16-token pages, GQA ratio G dividing 32, sm_scale > 0).
+// 16-token pages, GQA ratio 1/2/4/8/16, sm_scale > 0).
 //
 // Math: the last C rows of kessie_hip_kernels.py:577-593 over ctx = L + C
 // tokens (query i at position ctx-C+i, causal, window, fog weights scaling V
@@ -529,6 +529,7 @@ int launch_prefill(Params& p, hipStream_t stream) {
     case 2: return launch_split<T, 2>(p, grid, stream);
     case 4: return launch_split<T, 4>(p, grid, stream);
     case 8: return launch_split<T, 8>(p, grid, stream);
+    case 16: return launch_split<T, 16>(p, grid, stream);
     default:
       set_error(KESSIE_ERR_UNSUPPORTED, "fog prefill (mfma): GQA ratio %d", p.G);
       return KESSIE_ERR_UNSUPPORTED;
@@ -543,7 +544,7 @@ bool prefill_mfma_ok(const Params& p, int dtype) {
   if (p.D != 128 || p.page_size != 16) return false;
   // Table-less pages: instantiated for the dense launchers' form only.
   if (p.page_table == nullptr && (p.dense_ppb <= 0 || p.G != 1 || p.bias || p.num_splits > 1)) return false;
-  if (!(p.G == 1 || p.G == 2 || p.G == 4 || p.G == 8)) return false;
+  if (!(p.G == 1 || p.G == 2 || p.G == 4 || p.G == 8 || p.G == 16)) return false;
   if (!(p.sm_scale > 0.0f)) return false;
   if (!aligned16(p.q) || !aligned16(p.k) || !aligned16(p.v) || !aligned16(p.out)) return false;
   if (p.page_stride % 8 || p.tok_stride % 8 || p.head_stride % 8) return false;

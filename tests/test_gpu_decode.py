@@ -53,7 +53,8 @@ def _run(dev, b, hq, hkv, ctx, dtype, fog="vscale", window=0, ctx_lens=None, lay
     return out, ref
 
 
-@pytest.mark.parametrize("hq,hkv", [(32, 8), (8, 8), (16, 8), (64, 8), (8, 1), (12, 3), (32, 4)])
+@pytest.mark.parametrize("hq,hkv", [(32, 8), (8, 8), (16, 8), (64, 8), (8, 1), (12, 3), (32, 4),
+                                     (16, 1), (128, 8)])
 def test_decode_bf16_gqa(dev, hq, hkv):
     out, ref = _run(dev, 2, hq, hkv, 1000, torch.bfloat16)
     _check(out, ref, torch.bfloat16)

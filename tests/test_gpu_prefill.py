@@ -32,7 +32,8 @@ def _case(dev, b, c, ctxs, hq, hkv, dtype, seed=0):
     return q, pool, table, lens
 
 
-@pytest.mark.parametrize("hq,hkv", [(32, 8), (8, 8), (16, 8), (64, 8), (8, 1), (12, 3), (32, 4)])
+@pytest.mark.parametrize("hq,hkv", [(32, 8), (8, 8), (16, 8), (64, 8), (8, 1), (12, 3), (32, 4),
+                                     (16, 1), (128, 8)])
 def test_prefill_bf16_gqa(dev, hq, hkv):
     from kessie_amd import ops
 
