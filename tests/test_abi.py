@@ -87,3 +87,41 @@ def test_ctypes_class_mirrors_reference_surface():
     for name in ("windowed_attention", "fused_fog_attention", "rope_remap", "page_evict", "page_insert",
                  "create_stream", "sync_stream", "_get_stream_ptr", "_ptr"):
         assert callable(getattr(KeSSieKernels, name))
+
+
+def test_prefill_and_decode_argument_errors_without_gpu():
+    """The paged entry points reject bad arguments before any launch: missing
+    query_start_loc / page table (invalid), a shape the MFMA varlen kernel does
+    not take (unsupported), a split prefill without room for its partials
+    (workspace).  Fake 16-byte-aligned addresses stand in for device buffers:
+    none of these paths reads them."""
+    import ctypes as C
+
+    from kessie_amd import _lib
+
+    lib = _lib.load()
+    fake = C.c_void_p(1 << 20)
+    bf16 = _lib.DTYPE_BF16
+    # varlen: query_start_loc missing
+    st = lib.kessie_fog_prefill_varlen(fake, None, 64, fake, 1024, 65536, 4096, 2048, 128, fake, 64, fake,
+                                       None, 0, None, 0, fake, 2, 32, 8, 128, 16, 1024, 0, 0.088, 1, bf16,
+                                       None, 0, None)
+    assert st == _lib.ERR_INVALID
+    # varlen: head_dim 64 is not an MFMA shape
+    st = lib.kessie_fog_prefill_varlen(fake, fake, 64, fake, 1024, 32768, 2048, 1024, 64, fake, 64, fake,
+                                       None, 0, None, 0, fake, 2, 32, 8, 64, 16, 1024, 0, 0.125, 1, bf16,
+                                       None, 0, None)
+    assert st == _lib.ERR_UNSUPPORTED
+    # paged prefill: a 64-query chunk on 64K keys splits the key range and needs a workspace
+    need = lib.kessie_fog_prefill_workspace_bytes(1, 64, 32, 8, 128, 65536, 16, bf16)
+    assert need > 0
+    st = lib.kessie_fog_prefill_paged(fake, fake, 4096, 65536, 4096, 2048, 128, fake, 4096, fake, None, 0,
+                                      None, 0, fake, 1, 64, 32, 8, 128, 16, 65536, 0, 0.088, 1, bf16,
+                                      None, 0, None)
+    assert st == _lib.ERR_WORKSPACE
+    status, msg = _lib.last_error()
+    assert status == _lib.ERR_WORKSPACE and "workspace" in msg
+    # decode: page table missing
+    st = lib.kessie_fog_decode_paged(fake, fake, 4096, 65536, 4096, 2048, 128, None, 4096, fake, None, 0,
+                                     None, 0, fake, 1, 32, 8, 128, 16, 4096, 0, 0.088, bf16, None, 0, None)
+    assert st == _lib.ERR_INVALID
