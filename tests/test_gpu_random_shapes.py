@@ -1,7 +1,7 @@
-"""GPU parity over seeded random shapes: decode and chunked prefill with random
-batch, ragged contexts (including empty ones), chunk lengths, GQA ratio, window,
-fog mode (none / V-scale per batch / bias / both) and dtype, each case against
-the CPU oracle.  The cases are fixed by their seeds (no randomness between
+"""GPU parity over seeded random shapes: decode, chunked prefill and varlen
+prefill with random batch, ragged contexts (including empty ones), chunk
+lengths, GQA ratio, window, fog mode (none / V-scale per batch / bias / both),
+dtype and key split count, each case against the CPU oracle.  The cases are fixed by their seeds (no randomness between
 runs).  Tolerance |gpu - ref| <= 2e-2 + 1e-2*|ref|."""
 import random
 
@@ -88,3 +88,45 @@ def test_random_prefill(dev, seed):
                                 None if vs is None else vs[i].cpu(), None if bias is None else bias.cpu(), window,
                                 causal=causal)
         _check(out[i:i + 1], ref)
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_random_varlen(dev, seed, monkeypatch):
+    from kessie_amd import ops
+
+    rng = random.Random(3000 + seed)
+    b = rng.randint(1, 8)
+    hq, hkv = rng.choice(GQA)
+    dtype = rng.choice([torch.bfloat16, torch.float16])
+    chunks = [rng.choice([0, 1, 16, 63, 64, 65, rng.randint(2, 300)]) for _ in range(b)]
+    if not any(chunks):
+        chunks[0] = 5
+    ctxs = [c + rng.choice([0, 1, rng.randint(2, 3000)]) for c in chunks]
+    ctxs = [max(x, 1) for x in ctxs]
+    mx = max(ctxs)
+    window = rng.choice([0, 0, 1, rng.randint(2, 1500)])
+    splits = rng.choice([None, 1, 3, 8])
+    if splits:
+        monkeypatch.setenv("KESSIE_PREFILL_SPLITS", str(splits))
+    pool, table, lens = _setup(dev, rng, b, ctxs, hkv, dtype, seed)
+    mode, vs, bias = _fog(dev, rng, b, mx, seed)
+    off = rng.randint(0, 7)
+    starts = [off]
+    for c in chunks:
+        starts.append(starts[-1] + c)
+    qsl = torch.tensor(starts, dtype=torch.int32, device=dev)
+    q_all = torch.randn(starts[-1], hq, 128, generator=gen(dev, seed + 9), device=dev).to(dtype)
+    q = q_all[off:]
+    out = torch.full_like(q, float("nan"))
+    assert ops.fog_prefill_varlen(q, qsl, max(chunks), pool, table, lens, mx, fog_vscale=vs, fog_bias=bias,
+                                  window=window, out=out)
+    torch.cuda.synchronize()
+    for i, c in enumerate(chunks):
+        if c == 0:
+            continue
+        s = starts[i] - off
+        ref = paged_prefill_ref(q[s:s + c].unsqueeze(0).cpu(), pool.cpu(), table[i:i + 1].cpu(),
+                                lens[i:i + 1].cpu(), None if vs is None else vs[i].cpu(),
+                                None if bias is None else bias.cpu(), window)
+        _check(out[s:s + c].unsqueeze(0), ref)
+    assert not torch.isnan(out).any()
