@@ -332,7 +332,7 @@ inline int combine_dsplit(int64_t rows, int D) {
 //     moved on that page.
 // ---------------------------------------------------------------------------
 constexpr int kDecWaves = 2;     // kv heads (waves) per decode workgroup
-constexpr int kDecPref = 4;      // pages in flight per wave
+constexpr int kDecPref = 2;      // pages in flight per wave
 constexpr int kDecWgsPerCu = 4;  // 2 waves/SIMD x 4 SIMDs / kDecWaves: one round of the grid
 constexpr int kVRow = 128 + 8;  // LDS row stride of the V and Q tiles (elements)
 
@@ -378,7 +378,7 @@ __device__ __forceinline__ void wave_lds_sync() {
 constexpr int kFogBias = 1, kFogVs = 2;
 
 template <typename T, int G, int PREF, int W, int FOG>
-// Two waves per SIMD (256 VGPRs), which holds four pages of K and V per wave.
+// Two waves per SIMD (256 VGPRs; ~160 used with two pages of K and V in flight).
 __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_mfma_kernel(Params p) {
   typedef typename Mfma<T>::vec8 vec8;
   typedef typename Mfma<T>::vec4 vec4;
@@ -669,9 +669,10 @@ int launch_generic(Params& p, hipStream_t stream) {
 
 template <typename T, int G>
 int launch_decode_mfma(Params& p, hipStream_t stream) {
-  // Two kv heads per workgroup, four pages in flight per wave, two waves per
-  // SIMD (measured at batch 16, 128K context: 1.264 ms against 1.325 ms for 8
-  // heads per workgroup, two pages in flight, four waves per SIMD).
+  // Two kv heads per workgroup, two pages in flight per wave, two waves per
+  // SIMD (measured at batch 16, 128K context: 1.308 ms against 1.314 ms with
+  // four pages in flight -- which also cost one sequence 3-9 % -- and 1.398 ms
+  // with two pages at three waves per SIMD).
   dim3 grid(p.num_splits, p.B, div_up(p.Hkv, kDecWaves));
   const int fog = (p.bias ? kFogBias : 0) | (p.vscale ? kFogVs : 0);
   const dim3 block(kDecWaves * 64);
