@@ -295,8 +295,8 @@ def bench_gather_evict(dev, reps=5, cpu=False):
     gc = torch.zeros(1, dtype=torch.int32, device=dev)
 
     def pipeline(e_sel=None, e_gat=None):
-        ops.page_select_evict(scores, valid, -1, 0.25, ev_list, ev_cnt)
-        ops.page_compact(tables, lens, valid, nt, nl, gi, gc)
+        # Score eviction + table compaction fused (clear + one launch), then the gather.
+        ops.page_evict_compact(scores, valid, tables, lens, -1, 0.25, ev_list, ev_cnt, nt, nl, gi, gc)
         if e_sel is not None:
             e_sel.record()
         ops.page_gather(pool, gi, gc, out=out, n=s * w)
@@ -345,7 +345,8 @@ def bench_gather_evict(dev, reps=5, cpu=False):
         del pool_bytes
     return {
         "cpu_baseline": res_cpu,
-        "workload": "score evict 25% of 65,536 pages + compact 64x1024 tables + gather survivors (bf16 pages)",
+        "workload": "score evict 25% of 65,536 pages + compact 64x1024 tables (fused: 2 launches) + gather "
+                    "survivors (bf16 pages)",
         "pipeline_ms": round(tot, 4),
         "gather_kernel_ms": round(gat, 4),
         "select_compact_ms": round(tot - gat, 4),
@@ -753,20 +754,47 @@ def bench_hf_cache(dev, layers=32, heads=8, d=128, window=4096, prefill=8000, st
                              "sample": "2 decode steps of the reference's torch.cat / fog op sequence"}}
 
 
+def load_probes():
+    """libkessie_probes.so (measurement-only HBM ceiling probes, built beside
+    the product library by kessie_amd.build; declared in include/kessie_probes.h)."""
+    import ctypes as C
+
+    from kessie_amd import build as kbuild
+
+    if not os.path.exists(kbuild.PROBES_LIB_PATH):
+        raise FileNotFoundError(f"{kbuild.PROBES_LIB_PATH} is not built (python -m kessie_amd.build)")
+    lib = C.CDLL(kbuild.PROBES_LIB_PATH)
+    P, I, I64 = C.c_void_p, C.c_int, C.c_int64
+    lib.kessie_probe_stream_read.argtypes = [P, I64, P, P]
+    lib.kessie_probe_copy.argtypes = [P, P, I64, P]
+    lib.kessie_probe_page_rows.argtypes = [P, P, I64, I64, I, I, P, I, I, I, P, P]
+    for fn in (lib.kessie_probe_stream_read, lib.kessie_probe_copy, lib.kessie_probe_page_rows):
+        fn.restype = I
+    return lib
+
+
 def bench_hbm_ceilings(dev, reps=10):
     """Practical HBM ceilings of the hot path's access patterns on this device
-    (kessie_probe_*): a 4 GiB read-only stream (the decode kernel's pattern at
-    its best), a 2 GiB copy (gather, insert), and the remap's pattern -- read
-    and rewrite the 2 KiB K half of every 4 KiB token row of 4,096 random
-    64 KiB pages (4 rotating page sets, so the 256 MB MALL does not serve it)."""
+    (libkessie_probes.so): a 4 GiB read-only stream (the decode kernel's
+    pattern at its best), a 2 GiB copy (gather, insert), and a matrix of page
+    patterns around the RoPE remap's (read and rewrite the 2 KiB K half of
+    every 4 KiB token row of 4,096 random 64 KiB pages, 4 rotating page sets
+    so the 256 MB MALL does not serve it): whole rows instead of half rows,
+    out of place instead of in place, pages in ascending id order, the V half
+    instead of the K half, whole pages copied out of place, and half / whole
+    rows only read; each at 1, 2, 4 and 8 sixteen-byte chunks per thread (8 =
+    one page's K half per workgroup, all read before any write).  GB/s count
+    the bytes read plus the bytes written."""
     import ctypes as C
 
     import torch
 
-    from kessie_amd import _lib
-
-    lib = _lib.load()
+    lib = load_probes()
     s = C.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+    def check(name, st):
+        if st != 0:
+            raise RuntimeError(f"{name} returned {st}")
 
     def timed(fn, n):
         fn(0)
@@ -784,26 +812,52 @@ def bench_hbm_ceilings(dev, reps=10):
     big = torch.empty(4 << 30, dtype=torch.uint8, device=dev)
     big.fill_(1)
     sink = torch.zeros(1, dtype=torch.int32, device=dev)
-    ms = timed(lambda i: _lib.check("kessie_probe_stream_read", lib.kessie_probe_stream_read(
+    ms = timed(lambda i: check("stream_read", lib.kessie_probe_stream_read(
         C.c_void_p(big.data_ptr()), big.numel(), C.c_void_p(sink.data_ptr()), s)), reps)
     out["stream_read_gbs"] = round(big.numel() / (ms * 1e-3) / 1e9, 1)
     half = big.numel() // 2
-    ms = timed(lambda i: _lib.check("kessie_probe_copy", lib.kessie_probe_copy(
+    ms = timed(lambda i: check("copy", lib.kessie_probe_copy(
         C.c_void_p(big.data_ptr() + half), C.c_void_p(big.data_ptr()), half, s)), reps)
     out["copy_gbs"] = round(2 * half / (ms * 1e-3) / 1e9, 1)
     del big
     torch.cuda.empty_cache()
     n_pages, sets = 4096, 4
     pool = torch.zeros(n_pages * sets * 2, 16, 2, 8, 128, dtype=torch.bfloat16, device=dev)
+    dst = torch.zeros_like(pool)
     g = torch.Generator(device=dev)
     g.manual_seed(1)
     lists = [torch.randperm(pool.shape[0], generator=g, device=dev)[:n_pages].to(torch.int32) for _ in range(sets)]
+    sorted_lists = [torch.sort(x)[0].contiguous() for x in lists]
     page_bytes = pool[0].numel() * 2
-    ms = timed(lambda i: _lib.check("kessie_probe_page_rmw", lib.kessie_probe_page_rmw(
-        C.c_void_p(pool.data_ptr()), page_bytes, 4096, 16, 2048, C.c_void_p(lists[i % sets].data_ptr()), n_pages,
-        pool.shape[0], s)), 4 * reps)
-    out["remap_pattern_rmw_gbs"] = round(2 * n_pages * 16 * 2048 / (ms * 1e-3) / 1e9, 1)
-    out["note"] = "bandwidth of the access pattern alone, no arithmetic; spec peak 8000 GB/s"
+    # name -> (byte offset in the page, destination (None: read only), row stride, rows per page,
+    #          bytes per row, page lists)
+    variants = {
+        "remap_pattern_rmw": (0, pool, 4096, 16, 2048, lists),
+        "full_row_rmw": (0, pool, 4096, 16, 4096, lists),
+        "half_row_out_of_place": (0, dst, 4096, 16, 2048, lists),
+        "half_row_rmw_sorted_pages": (0, pool, 4096, 16, 2048, sorted_lists),
+        "v_half_row_rmw": (2048, pool, 4096, 16, 2048, lists),
+        "whole_page_out_of_place": (0, dst, page_bytes, 1, page_bytes, lists),
+        "half_row_read_only": (0, None, 4096, 16, 2048, lists),
+        "full_row_read_only": (0, None, 4096, 16, 4096, lists),
+    }
+    matrix = {}
+    for name, (off, target, stride, rows, row_bytes, pl) in variants.items():
+        moved = (2 if target is not None else 1) * n_pages * rows * row_bytes
+        row = {}
+        for u in (1, 2, 4, 8):
+            ms = timed(lambda i: check("page_rows", lib.kessie_probe_page_rows(
+                C.c_void_p(pool.data_ptr() + off), None if target is None else C.c_void_p(target.data_ptr() + off),
+                page_bytes, stride, rows, row_bytes, C.c_void_p(pl[i % sets].data_ptr()), n_pages, pool.shape[0], u,
+                C.c_void_p(sink.data_ptr()), s)), 4 * reps)
+            row[f"u{u}"] = round(moved / (ms * 1e-3) / 1e9, 1)
+        row["best_gbs"] = max(row.values())
+        matrix[name] = row
+        log(f"ceilings: {name} {row}")
+    out["remap_pattern_rmw_gbs"] = matrix["remap_pattern_rmw"]["best_gbs"]
+    out["page_pattern_matrix_gbs"] = matrix
+    out["note"] = ("bandwidth of the access pattern alone, no arithmetic (bytes read + written per second); "
+                   "spec peak 8000 GB/s")
     return out
 
 

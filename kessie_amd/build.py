@@ -5,7 +5,9 @@
 Each translation unit is compiled to an object with hipcc in parallel, then
 linked into ``kessie_amd/libkessie_mi355x.so``.  The library is what the ctypes
 loader (kessie_amd/kessie_hip_ctypes.py) opens; nothing is JIT-compiled at
-import time.
+import time.  The same call builds the measurement-only companion
+``kessie_amd/probes/libkessie_probes.so`` (HBM ceiling probes that bench.py
+loads; not part of the product library).
 """
 from __future__ import annotations
 
@@ -20,6 +22,8 @@ CSRC = os.path.join(PKG_DIR, "csrc")
 BUILD_DIR = os.path.join(PKG_DIR, "_build")
 LIB_NAME = "libkessie_mi355x.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
+PROBES_DIR = os.path.join(PKG_DIR, "probes")
+PROBES_LIB_PATH = os.path.join(PROBES_DIR, "libkessie_probes.so")
 ARCH = "gfx950"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -48,8 +52,10 @@ def sources() -> list[str]:
     )
 
 
-def _compile(src: str, extra: list[str]) -> str:
-    obj = os.path.join(BUILD_DIR, os.path.basename(src)[:-4] + ".o")
+def _compile(src: str, extra: list[str], subdir: str = "") -> str:
+    out_dir = os.path.join(BUILD_DIR, subdir)
+    os.makedirs(out_dir, exist_ok=True)
+    obj = os.path.join(out_dir, os.path.basename(src)[:-4] + ".o")
     cmd = [HIPCC, *COMMON_FLAGS, *extra, "-c", src, "-o", obj]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
@@ -79,23 +85,31 @@ def build(verbose: bool = True, jobs: int | None = None, extra: list[str] | None
     srcs = sources()
     extra = list(extra or [])
     jobs = jobs or min(len(srcs), max(1, min(8, os.cpu_count() or 1)))
+    probe_srcs = sorted(os.path.join(PROBES_DIR, f) for f in os.listdir(PROBES_DIR) if f.endswith(".hip"))
     with _fut.ThreadPoolExecutor(max_workers=jobs) as ex:
         objs = list(ex.map(lambda s: _compile(s, extra), srcs))
-    tmp = LIB_PATH + ".tmp"
+        probe_objs = list(ex.map(lambda s: _compile(s, extra, "probes"), probe_srcs))
+    _link(objs, LIB_PATH)
+    _link(probe_objs, PROBES_LIB_PATH)
+    if verbose:
+        print(f"built {LIB_PATH} from {len(srcs)} sources and {PROBES_LIB_PATH}")
+    return LIB_PATH
+
+
+def _link(objs: list[str], path: str) -> None:
+    tmp = path + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{proc.stdout}\n{proc.stderr}")
-    os.replace(tmp, LIB_PATH)
-    if verbose:
-        print(f"built {LIB_PATH} from {len(srcs)} sources")
-    return LIB_PATH
+    os.replace(tmp, path)
 
 
 def clean() -> None:
     shutil.rmtree(BUILD_DIR, ignore_errors=True)
-    if os.path.exists(LIB_PATH):
-        os.remove(LIB_PATH)
+    for path in (LIB_PATH, PROBES_LIB_PATH):
+        if os.path.exists(path):
+            os.remove(path)
 
 
 if __name__ == "__main__":

@@ -16,14 +16,19 @@
 // with 16-byte loads: each lane owns one chunk pair (8 elements of the first
 // half of a head and the matching 8 of the second half), so a wave's loads
 // cover whole 128-byte segments of a token's K row.
+// The access pattern, not the arithmetic, bounds it: the K half (2 KiB) of
+// every 4 KiB token row of random 64 KiB pages.  Measured on MI355X with the
+// measurement probes (bytes read + written per second): that half-row pattern
+// reaches 4.8 TB/s updated in place and the same out of place, 5.9 TB/s when
+// only read; whole rows 5.6 TB/s updated and 6.8 TB/s read.
 #include "common.h"
 
 namespace kessie {
 namespace {
 
-constexpr int kRemapThreads = 256;
-constexpr int kRemapTile = 4;     // tokens per workgroup (8 KiB of K at 8 heads x 128 bf16)
-constexpr int kVecMaxHalf = 128;  // vectorised kernel: head_dim <= 256
+constexpr int kRemapThreads = 256;  // generic instances: 4 tokens per 256-thread workgroup
+constexpr int kRemapTile = 4;
+constexpr int kVecMaxHalf = 128;    // vectorised kernel: head_dim <= 256
 
 // Byte-free addressing helper: element offset of token t's K row, or -1 when
 // the token's page id is out of range.
@@ -63,17 +68,19 @@ struct Vec16<float> {
 // rows and head starts.  The K chunks of a round are loaded into registers
 // before the cos/sin phase, so HBM latency overlaps the trigonometry; the
 // workgroup barrier that publishes cos/sin keeps those loads ahead of it.
-// One chunk pair (two 16-byte loads) per thread per round: the read-modify-
-// write pattern is fastest with many small workgroups (measured, 65,536 bf16
-// tokens: 4 tokens per workgroup 56.6 us; 8: 58.3; 16 tokens with 4 pairs per
-// thread: 61.3; 2: 58.7).
+// One chunk pair (two 16-byte loads) per thread per round.  Tile shape
+// (measured, 65,536 bf16 tokens of 8 heads x 128 in random 16-token pages):
+// one page's 16 tokens per 1,024-thread workgroup 52.1-52.7 us; 8 tokens per
+// 512 threads 54.3; 4 per 256 55.0-55.2; 1 per 64 53.7; 16 tokens with 2 or 4
+// pairs per thread 58.6-58.7; 32 tokens 57.4-59.7.  Exchanging chunk halves
+// by lane shuffle (each wave reading 1 KiB contiguous) measured the same.
 constexpr int kRemapItems = 1;  // chunk pairs per thread per round
 
 // kHalf / kHeads / kPage > 0 fix head_dim/2, the head count and the page size
 // at compile time (the index arithmetic then has no runtime divisions); 0
-// takes them from the arguments.
-template <typename T, int kHalf, int kHeads, int kPage>
-__global__ __launch_bounds__(kRemapThreads) void rope_remap_vec(
+// takes them from the arguments.  kTile tokens per workgroup of kThreads.
+template <typename T, int kHalf, int kHeads, int kPage, int kTile, int kThreads>
+__global__ __launch_bounds__(kThreads) void rope_remap_vec(
     T* __restrict__ pool, int64_t page_stride, int64_t tok_stride, int64_t head_stride,
     const int32_t* __restrict__ page_list, int num_pages, const int32_t* __restrict__ orig_pos,
     const int32_t* __restrict__ tgt_pos, const float* __restrict__ inv_freq, float theta, int num_tokens,
@@ -81,25 +88,25 @@ __global__ __launch_bounds__(kRemapThreads) void rope_remap_vec(
 #pragma clang fp contract(off)
   typedef typename Vec16<T>::type V;
   constexpr int N = Vec16<T>::N;
-  __shared__ float2 cs[kRemapTile * kVecMaxHalf];  // [token][j] = (cos, sin)
+  __shared__ float2 cs[kTile * kVecMaxHalf];  // [token][j] = (cos, sin)
   const int half = kHalf > 0 ? kHalf : half_arg;
   const int num_heads = kHeads > 0 ? kHeads : num_heads_arg;
   const int page_size = kPage > 0 ? kPage : page_size_arg;
 
-  const int t0 = blockIdx.x * kRemapTile;
-  const int ntok = min(kRemapTile, num_tokens - t0);
+  const int t0 = blockIdx.x * kTile;
+  const int ntok = min(kTile, num_tokens - t0);
   const int chunks = half / N;  // chunk pairs per head
   const int per_tok = num_heads * chunks;
   const int n_work = ntok * per_tok;
 
-  for (int round = 0; round * kRemapItems * kRemapThreads < n_work; ++round) {
-    const int base = round * kRemapItems * kRemapThreads;
+  for (int round = 0; round * kRemapItems * kThreads < n_work; ++round) {
+    const int base = round * kRemapItems * kThreads;
     V a[kRemapItems], b[kRemapItems];
     T* p1[kRemapItems];
     int csi[kRemapItems];
 #pragma unroll
     for (int it = 0; it < kRemapItems; ++it) {
-      const int i = base + it * kRemapThreads + threadIdx.x;
+      const int i = base + it * kThreads + threadIdx.x;
       p1[it] = nullptr;
       csi[it] = 0;
       if (i < n_work) {
@@ -120,7 +127,7 @@ __global__ __launch_bounds__(kRemapThreads) void rope_remap_vec(
     }
     if (round == 0) {
       const int n_ang = ntok * half;
-      for (int i = threadIdx.x; i < n_ang; i += kRemapThreads) {
+      for (int i = threadIdx.x; i < n_ang; i += kThreads) {
         const int tt = i / half;
         const int j = i - tt * half;
         const int t = t0 + tt;
@@ -201,17 +208,18 @@ int launch_remap(void* pool, int64_t page_stride, int64_t tok_stride, int64_t he
                       head_stride % N == 0;
   T* p = static_cast<T*>(pool);
   if (vec_ok) {
-    const int grid = div_up(num_tokens, kRemapTile);
     // Specialised instance for the Llama-style K layout (8 kv heads x 128,
-    // 16-token pages or dense rows).
+    // 16-token pages or dense rows): one page's 16 tokens per 1,024-thread
+    // workgroup, one chunk pair per thread (bf16/fp16; fp32 rows hold twice
+    // the chunks and take two rounds).
     if (half == 64 && num_heads == 8 && (page_list == nullptr || page_size == 16))
-      hipLaunchKernelGGL((rope_remap_vec<T, 64, 8, 16>), dim3(grid), dim3(kRemapThreads), 0, stream, p,
-                         page_stride, tok_stride, head_stride, page_list, num_pages, orig_pos, tgt_pos, inv_freq,
-                         theta, num_tokens, num_heads, half, page_size);
+      hipLaunchKernelGGL((rope_remap_vec<T, 64, 8, 16, 16, 1024>), dim3(div_up(num_tokens, 16)), dim3(1024), 0,
+                         stream, p, page_stride, tok_stride, head_stride, page_list, num_pages, orig_pos, tgt_pos,
+                         inv_freq, theta, num_tokens, num_heads, half, page_size);
     else
-      hipLaunchKernelGGL((rope_remap_vec<T, 0, 0, 0>), dim3(grid), dim3(kRemapThreads), 0, stream, p,
-                         page_stride, tok_stride, head_stride, page_list, num_pages, orig_pos, tgt_pos, inv_freq,
-                         theta, num_tokens, num_heads, half, page_size);
+      hipLaunchKernelGGL((rope_remap_vec<T, 0, 0, 0, kRemapTile, kRemapThreads>), dim3(div_up(num_tokens, kRemapTile)),
+                         dim3(kRemapThreads), 0, stream, p, page_stride, tok_stride, head_stride, page_list,
+                         num_pages, orig_pos, tgt_pos, inv_freq, theta, num_tokens, num_heads, half, page_size);
   } else {
     const int64_t total = (int64_t)num_tokens * num_heads * half;
     const int64_t grid = (total + kRemapThreads - 1) / kRemapThreads;

@@ -125,3 +125,25 @@ def test_prefill_and_decode_argument_errors_without_gpu():
     st = lib.kessie_fog_decode_paged(fake, fake, 4096, 65536, 4096, 2048, 128, None, 4096, fake, None, 0,
                                      None, 0, fake, 1, 32, 8, 128, 16, 4096, 0, 0.088, bf16, None, 0, None)
     assert st == _lib.ERR_INVALID
+
+
+PROBES_HEADER = os.path.join(ROOT, "include", "kessie_probes.h")
+
+
+def test_probe_library_is_separate_from_the_product():
+    """The measurement probes live in their own library: declared in
+    kessie_probes.h, exported by libkessie_probes.so, absent from the product."""
+    from kessie_amd import build as kbuild
+
+    text = re.sub(r"/\*.*?\*/", "", open(PROBES_HEADER).read(), flags=re.S)
+    probes = sorted(set(re.findall(r"\b(kessie_probe_[a-z0-9_]+)\s*\(", text)))
+    assert probes == ["kessie_probe_copy", "kessie_probe_page_rows", "kessie_probe_stream_read"]
+    for path, want in ((kbuild.PROBES_LIB_PATH, True), (kbuild.LIB_PATH, False)):
+        if not os.path.exists(path):
+            pytest.fail(f"{path} is not built (run python -m kessie_amd.build)")
+        out = subprocess.run(["nm", "-D", "--defined-only", path], capture_output=True, text=True,
+                             check=True).stdout
+        exported = set(ln.split()[-1] for ln in out.splitlines() if ln.strip())
+        for name in probes:
+            assert (name in exported) == want, (path, name)
+    assert not any(n.startswith("kessie_probe") for n in declared_functions())
