@@ -283,13 +283,26 @@ int kessie_page_evict_list(int8_t* page_valid, const int32_t* page_positions,
 /* Bytes of workspace the page-management calls need for num_pages (host). */
 size_t kessie_page_workspace_bytes(int num_pages);
 
+/* Prepares a page workspace (any size from kessie_page_workspace_bytes) for
+ * kessie_page_select_evict / kessie_page_evict_compact: their scratch, at the
+ * start of the workspace, must hold this state on entry, and each call leaves
+ * it so again.  Call once per workspace allocation, on the stream that will
+ * use it (one fill launch).  A select call on a workspace that was never
+ * initialised writes -2 to its counts and touches nothing else.  (No
+ * reference counterpart: the reference's eviction needs no workspace.) */
+int kessie_page_workspace_init(void* workspace, size_t workspace_bytes,
+                               void* stream);
+
 /* Score eviction: among pages with page_valid==1, evict the k with the
  * smallest keys (score[p], p) under the total order score ascending, then
  * page id ascending (scores compared as IEEE floats, -0 == +0, NaN not
  * allowed).  k = k_evict when k_evict >= 0 (clamped to the valid count),
  * else floor(evict_fraction * n_valid) computed in double.  Evicted pages get
  * page_valid=0; their ids go to evict_list ascending; k to *evict_count.
- * Deterministic: no order depends on atomics.  (The reference only has the
+ * Deterministic: no order depends on atomics.  One launch whose workgroups
+ * meet at bounded grid barriers (*evict_count reads -1 if the device could
+ * not run them at once); the workspace must have been prepared by
+ * kessie_page_workspace_init (-2 otherwise).  (The reference only has the
  * threshold predicate, kessie_kernels_v2.hip:393-407; this applies it with an
  * exact k-th-order-statistic threshold.) */
 int kessie_page_select_evict(const float* scores, int8_t* page_valid,
@@ -310,6 +323,28 @@ int kessie_page_compact(const int32_t* tables, const int32_t* lens,
                         int32_t* gather_count, int num_seqs, int table_stride,
                         int num_pages, void* workspace, size_t workspace_bytes,
                         void* stream);
+
+/* kessie_page_select_evict followed by kessie_page_compact of the tables by
+ * the post-eviction valid flags, in two launches instead of two calls' worth:
+ * every output equals what those two calls produce (evict_list / evict_count /
+ * page_valid as select_evict; new_tables / new_lens / gather_idx /
+ * gather_count as compact).  num_seqs <= 8192 (else KESSIE_ERR_UNSUPPORTED).
+ * Workspace: kessie_page_workspace_bytes(max(num_pages, num_seqs)), prepared
+ * by kessie_page_workspace_init (else both counts read -2).  The launch's
+ * workgroups (at most 64) wait for each other at bounded grid barriers; if
+ * the device cannot run them at once the wait runs out (~0.1 s each), the
+ * outputs are undefined and *evict_count and *gather_count read -1.  (The reference evicts by threshold only and compacts nothing,
+ * kessie_hip_kernels.py:526-564; the caller this serves is the page
+ * manager's evict-then-gather step.) */
+int kessie_page_evict_compact(const float* scores, int8_t* page_valid,
+                              int num_pages, int k_evict, float evict_fraction,
+                              int32_t* evict_list, int32_t* evict_count,
+                              const int32_t* tables, const int32_t* lens,
+                              int num_seqs, int table_stride,
+                              int32_t* new_tables, int32_t* new_lens,
+                              int32_t* gather_idx, int32_t* gather_count,
+                              void* workspace, size_t workspace_bytes,
+                              void* stream);
 
 /* Ids of valid pages in ascending physical order (the order of the
  * reference's get_layer_kv, kessie_hip_kernels.py:558-564) into out_idx,
@@ -434,20 +469,6 @@ int kessie_index_query(const void* index_embeds, int64_t row_stride,
                        float* similarities,
                        int top_k, int32_t* top_ids, float* top_scores,
                        void* workspace, size_t workspace_bytes, void* stream);
-
-/* =========================================================================
- * Measurement probes: the practical HBM bandwidth of the hot path's access
- * patterns with no arithmetic in the way (read-only stream, copy, and the
- * remap's read-modify-write of the first row_bytes of every token row of the
- * listed pages).  `sink` is one uint32 the read probe may write.
- * ========================================================================= */
-int kessie_probe_stream_read(const void* buf, int64_t bytes, void* sink,
-                             void* stream);
-int kessie_probe_copy(void* dst, const void* src, int64_t bytes, void* stream);
-int kessie_probe_page_rmw(void* pool, int64_t page_bytes,
-                          int64_t row_stride_bytes, int rows_per_page,
-                          int row_bytes, const int32_t* pages, int n_pages,
-                          int num_pages, void* stream);
 
 #if defined(__GNUC__) || defined(__clang__)
 #pragma GCC visibility pop

@@ -68,17 +68,18 @@ SIGNATURES = {
         _I, _I, _I, _I, _I, _I, _P]),
     "kessie_page_evict_list": (_I, [_P, _P, _P, _I, _I, _P, _P, _P, _SZ, _P]),
     "kessie_page_workspace_bytes": (_SZ, [_I]),
+    "kessie_page_workspace_init": (_I, [_P, _SZ, _P]),
     "kessie_page_select_evict": (_I, [_P, _P, _I, _I, _F, _P, _P, _P, _SZ, _P]),
     "kessie_page_compact": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _SZ, _P]),
+    # scores, valid, num_pages, k, frac, evict_list, evict_count, tables, lens, S, W, new_tables, new_lens,
+    # gather_idx, gather_count, ws, ws_bytes, stream
+    "kessie_page_evict_compact": (_I, [_P, _P, _I, _I, _F, _P, _P, _P, _P, _I, _I, _P, _P, _P, _P, _P, _SZ, _P]),
     "kessie_page_valid_list": (_I, [_P, _I, _P, _P, _P, _SZ, _P]),
     "kessie_page_gather": (_I, [_P, _I64, _P, _P, _I, _I, _P, _P]),
     # buf, dtype, kv_len, fog_alpha, fog_start, recall, num_recall, boost, stream
     "kessie_fog_bias_fill": (_I, [_P, _I, _I, _D, _D, _P, _I, _D, _P]),
     "kessie_fog_weights_fill": (_I, [_P, _I, _D, _D, _P]),
     # pool + 4 strides, key + 2 strides, value + 2 strides, slots, T, H, D, P, pages, dtype, stream
-    "kessie_probe_stream_read": (_I, [_P, _I64, _P, _P]),
-    "kessie_probe_copy": (_I, [_P, _P, _I64, _P]),
-    "kessie_probe_page_rmw": (_I, [_P, _I64, _I64, _I, _I, _P, _I, _I, _P]),
     "kessie_hf_fog_weights_fill": (_I, [_P, _I, _D, _D, _P]),
     "kessie_hf_append_fog": (_I, [_P, _P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64, _I64, _I64,
                                   _P, _I64, _I64, _I64, _I, _I, _I, _I, _I, _D, _D, _I, _P]),

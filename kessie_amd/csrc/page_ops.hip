@@ -59,9 +59,8 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* total, int* sm) 
 // Predicates for ordered compaction over page ids
 // ---------------------------------------------------------------------------
 enum PredKind : int {
-  kPredValid = 0,      // valid[i] == 1
-  kPredFreed = 1,      // (valid==1 && pos<thr) || (allocated && allocated[i] && valid!=1)
-  kPredScoreEvict = 2  // valid==1 && key(i) <= threshold key (threshold in workspace)
+  kPredValid = 0,  // valid[i] == 1
+  kPredFreed = 1   // (valid==1 && pos<thr) || (allocated && allocated[i] && valid!=1)
 };
 
 struct PredArgs {
@@ -70,17 +69,7 @@ struct PredArgs {
   const int32_t* positions;
   const int8_t* allocated;
   int thr;
-  const float* scores;
-  const unsigned long long* key_thr;  // device, for kPredScoreEvict
-  const int* k_dev;                   // device: number to evict (0 -> none)
 };
-
-__device__ __forceinline__ unsigned long long score_key(float s, int id) {
-  if (s == 0.0f) s = 0.0f;  // -0 == +0
-  const uint32_t bits = __float_as_uint(s);
-  const uint32_t ord = (bits & 0x80000000u) ? ~bits : (bits | 0x80000000u);
-  return ((unsigned long long)ord << 32) | (uint32_t)id;
-}
 
 __device__ __forceinline__ bool pred_eval(const PredArgs& a, int i) {
   switch (a.kind) {
@@ -91,8 +80,6 @@ __device__ __forceinline__ bool pred_eval(const PredArgs& a, int i) {
       if (v && a.positions[i] < a.thr) return true;
       return a.allocated != nullptr && a.allocated[i] != 0 && !v;
     }
-    case kPredScoreEvict:
-      return a.valid[i] == 1 && *a.k_dev > 0 && score_key(a.scores[i], i) <= *a.key_thr;
   }
   return false;
 }
@@ -156,47 +143,74 @@ __global__ __launch_bounds__(kThreads) void compact_write_kernel(PredArgs a, int
 }
 
 // ---------------------------------------------------------------------------
-// Radix select: the key of rank k-1 among valid pages.  Keys are 64-bit
-// (ordered score << 32 | page id), so they are unique and the k smallest form
-// exactly the set the total order (score, id) puts first.  Five launches, no
-// host round trip:
-//   clear     zero the global 4096-bin histogram and counters (a fill kernel:
-//             graph-capture safe);
-//   hist      many workgroups histogram the top 12 bits of the ordered score
-//             of valid pages in LDS and add them to the global histogram;
-//   bucket    one workgroup derives k from the valid count and picks the bin
-//             holding rank k-1 and the rank inside it;
-//   collect   many workgroups append that bin's keys (low 20 score bits, page
-//             id) to a candidate list, one atomic per workgroup tile;
-//   resolve   one workgroup resolves the low 20 bits (two 10-bit passes) and,
-//             when several candidates share that score, the page id (11+11+10
-//             bits) on the candidates -- copied to LDS when they fit, read in
-//             place otherwise (heavily tied scores).
-// Histogram and list atomics only count; the result does not depend on their
-// order.  (Folding bucket and resolve into the last workgroup of hist and
-// collect measured slower: 46 us against 26 us for 65,536 pages.)
+// Score eviction: the key of rank k-1 among valid pages, then the ordered list
+// of the keys up to it.  Keys are 64-bit (ordered score << 32 | page id), so
+// they are unique and the k smallest are exactly the set the total order
+// (score, id) puts first.  Two launches, no host round trip:
+//   clear   a fill kernel zeroes the grid-barrier counter, the 4096-bin
+//           histogram and the counters (graph-capture safe);
+//   fused   G workgroups (G <= kFusedMaxG, one per CU at most: they are all
+//           resident at once) that meet at three grid barriers:
+//     P1  each workgroup histograms the top 12 bits of the ordered scores of
+//         the valid pages of its tiles in LDS and adds them to the global
+//         histogram;                                                    | B1
+//     P2  every workgroup reads the histogram, derives k and the bin holding
+//         rank k-1 and the rank inside it, and appends that bin's keys (low
+//         20 score bits, page id) from its tiles to a candidate list, one
+//         atomic per tile;                                              | B2
+//     P3  every workgroup resolves the threshold key on the candidates (the
+//         low 20 score bits in two 10-bit passes and, for tied scores, the
+//         page id in 11+11+10 bits; the same result in every workgroup, so
+//         no barrier is needed to share it), counts the pages of its tiles
+//         it evicts and, in the fused evict + compact call, the survivors of
+//         its table rows;                                               | B3
+//     P4  prefix sums of those counts place each workgroup's evict-list
+//         entries (ascending page id) and each table row's gather indices;
+//         each workgroup writes its part and clears its evicted pages'
+//         valid flags.
+// A table entry survives when its page is valid and not evicted; the
+// predicate reads page_valid, which other workgroups clear during P4 only for
+// evicted pages, so it answers the same before or after their writes.  The
+// histogram and candidate atomics only count: no result depends on their
+// order.  Each barrier wait is bounded (~0.1 s); a wait that runs out (only
+// possible if the device could not hold the G workgroups at once) marks the
+// call failed and the evict count reads -1.
+// Every workgroup loads its keys once, in P1 -- the 4,096 keys of its tile
+// (4 per thread) and the page keys of its table-row entries (one 1,024-entry
+// chunk per thread per row) -- and keeps them in registers, so P2-P4 touch
+// memory only for the histogram, the candidates, the counts and the outputs.
+// G = one workgroup per 4,096-key tile, at most 64: the barriers cost more
+// with more workgroups (one contended counter; measured on 65,536 pages: 8
+// workgroups 1.2 us per barrier, 16 2.8 us, 32-64 6-7 us), while the table
+// rows spread over fewer workgroups take longer.  (Measured: five select
+// launches + three compaction launches 35 us; one workgroup holding all
+// 65,536 keys in registers 76 us -- a single CU is latency-bound in every
+// phase.)
 // ---------------------------------------------------------------------------
 constexpr int kSelThreads = 1024;
 constexpr int kSelWaves = kSelThreads / 64;
-constexpr int kSelCap = 12288;   // candidate keys held in LDS
+constexpr int kSelCap = 12288;                // candidate keys held in LDS
 constexpr int kSelBins = 4096;
-constexpr int kSelPer = 4;       // keys per thread per hist/collect tile
+constexpr int kSelPer = 4;                    // consecutive keys per thread per tile
 constexpr int kSelTile = kSelThreads * kSelPer;
-constexpr int kSelMaxGrid = 1024;
+constexpr int kFusedMaxG = 64;                // workgroups of the fused launch
+constexpr int kFusedMaxRows = 8192;           // table rows whose offsets fit in LDS
+constexpr int kSpinLimit = 1 << 21;           // barrier polls (s_sleep 2 each: ~0.1 s)
 
-struct SelectOut {
-  unsigned long long key_thr;  // largest evicted key
-  int k;                       // number evicted
-  int n_valid;
-};
-
-struct SelScratch {
-  int hist[kSelBins];
+// Scratch of the fused launch, at the start of the page workspace.  It is
+// zero apart from `magic` between calls: kessie_page_workspace_init writes
+// that state once, and each call's last workgroup to finish restores it, so
+// no call needs a clearing launch of its own.
+constexpr unsigned kScratchMagic = 0x4b535331u;
+struct FusedScratch {
+  unsigned magic;  // kScratchMagic once initialised
+  unsigned bar;    // grid-barrier arrivals
+  unsigned done;   // workgroups past their last read of this scratch
+  int timed_out;
   int n_valid;
   int ncand;
-  int k;      // keys to evict (0: nothing to resolve)
-  int rank;   // rank of key k-1 inside bin `top`
-  uint32_t top;
+  int hist[kSelBins];
+  int wg_evict[kFusedMaxG];  // evicted pages per workgroup (written before B3)
 };
 
 __device__ __forceinline__ uint32_t ordered_score(float s) {
@@ -205,7 +219,8 @@ __device__ __forceinline__ uint32_t ordered_score(float s) {
   return (bits & 0x80000000u) ? ~bits : (bits | 0x80000000u);
 }
 
-// Exclusive scan of one int per thread across the 1024-thread block.
+// Exclusive scan of one int per thread across the 1024-thread block; the
+// block total is left in sm[kSelWaves] until the next call.
 __device__ __forceinline__ int sel_block_scan(int v, int* sm) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int x = v;
@@ -227,6 +242,33 @@ __device__ __forceinline__ int sel_block_scan(int v, int* sm) {
   }
   __syncthreads();
   const int res = x - v + sm[wave];
+  __syncthreads();
+  return res;
+}
+
+// sel_block_scan for 64-bit values (four 16-bit counts packed in one word);
+// the block total is left in sm64[kSelWaves].
+__device__ __forceinline__ unsigned long long sel_block_scan64(unsigned long long v, unsigned long long* sm64) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  unsigned long long x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const unsigned long long y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) sm64[wave] = x;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned long long acc = 0;
+    for (int w = 0; w < kSelWaves; ++w) {
+      const unsigned long long t = sm64[w];
+      sm64[w] = acc;
+      acc += t;
+    }
+    sm64[kSelWaves] = acc;
+  }
+  __syncthreads();
+  const unsigned long long res = x - v + sm64[wave];
   __syncthreads();
   return res;
 }
@@ -256,243 +298,594 @@ __device__ __forceinline__ void sel_pick(const int* bins, int nb, int rank, int*
   __syncthreads();
 }
 
-__global__ __launch_bounds__(kThreads) void sel_clear_kernel(SelScratch* ss) {
-  for (int e = threadIdx.x; e < kSelBins; e += kThreads) ss->hist[e] = 0;
+__global__ __launch_bounds__(kThreads) void scratch_init_kernel(FusedScratch* fs) {
+  for (int e = threadIdx.x; e < kSelBins; e += kThreads) fs->hist[e] = 0;
   if (threadIdx.x == 0) {
-    ss->n_valid = 0;
-    ss->ncand = 0;
-    ss->k = 0;
-    ss->rank = 0;
-    ss->top = 0;
+    fs->bar = 0;
+    fs->done = 0;
+    fs->timed_out = 0;
+    fs->n_valid = 0;
+    fs->ncand = 0;
+    fs->magic = kScratchMagic;
   }
 }
 
-__global__ __launch_bounds__(kSelThreads) void sel_hist_kernel(const float* __restrict__ scores,
-                                                               const int8_t* __restrict__ valid, int n,
-                                                               SelScratch* ss) {
-  __shared__ int hist[kSelBins];
-  for (int e = threadIdx.x; e < kSelBins; e += kSelThreads) hist[e] = 0;
+// All G workgroups arrive; returns once arrivals reach `target` or the bounded
+// wait runs out (then fs->timed_out is set).  Release/acquire at agent scope
+// make every write before the barrier visible to every workgroup after it.
+__device__ __forceinline__ void grid_barrier(FusedScratch* fs, unsigned target) {
   __syncthreads();
-  int c = 0;
-  for (int64_t t0 = (int64_t)blockIdx.x * kSelTile; t0 < n; t0 += (int64_t)gridDim.x * kSelTile) {
-    float sc[kSelPer];
-    int8_t vv[kSelPer];
-#pragma unroll
-    for (int j = 0; j < kSelPer; ++j) {
-      const int64_t i = t0 + j * kSelThreads + threadIdx.x;
-      vv[j] = i < n ? valid[i] : (int8_t)0;
-      sc[j] = i < n ? scores[i] : 0.0f;
+  if (threadIdx.x == 0) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __hip_atomic_fetch_add(&fs->bar, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    int spins = 0;
+    while (__hip_atomic_load(&fs->bar, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+      __builtin_amdgcn_s_sleep(2);
+      if (++spins > kSpinLimit) {
+        __hip_atomic_store(&fs->timed_out, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
     }
-#pragma unroll
-    for (int j = 0; j < kSelPer; ++j) {
-      if (vv[j] != 1) continue;
-      ++c;
-      atomicAdd(&hist[ordered_score(sc[j]) >> 20], 1);
-    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   }
-  for (int o = 32; o >= 1; o >>= 1) c += __shfl_xor(c, o, 64);
-  if ((threadIdx.x & 63) == 0 && c) atomicAdd(&ss->n_valid, c);
   __syncthreads();
-  for (int e = threadIdx.x; e < kSelBins; e += kSelThreads)
-    if (hist[e]) atomicAdd(&ss->hist[e], hist[e]);
 }
 
-__global__ __launch_bounds__(kSelThreads) void sel_bucket_kernel(SelScratch* ss, int k_evict, float evict_fraction,
-                                                                 SelectOut* out) {
-  __shared__ int hist[kSelBins];
+struct FusedArgs {
+  const float* scores;
+  int8_t* valid;
+  int n;
+  int k_evict;
+  float evict_fraction;
+  int32_t* evict_list;
+  int32_t* evict_count;
+  // table compaction (tables == nullptr: select + evict only)
+  const int32_t* tables;
+  const int32_t* lens;
+  int num_seqs;
+  int table_stride;
+  int32_t* new_tables;
+  int32_t* new_lens;
+  int32_t* gather_idx;
+  int32_t* gather_count;
+  // workspace
+  FusedScratch* fs;
+  uint32_t* cand_s;
+  uint32_t* cand_i;
+  int* row_count;
+  int tiles_per_wg;
+};
+
+// LDS of the fused kernel, in 32-bit words: P1/P2 use the first kSelBins as
+// the histogram; P3 the 2048-bin resolve histogram plus the candidate copy;
+// P4 the table row offsets.
+constexpr int kFusedLdsWords = 2048 + 2 * kSelCap;
+static_assert(kFusedLdsWords >= kSelBins && kFusedLdsWords >= kFusedMaxRows, "fused LDS layout");
+
+constexpr int kTileRegs = 4;  // key tiles per workgroup held in registers (4 keys per thread each)
+constexpr int kRowRegs = 4;   // 1,024-entry table-row chunks per workgroup held in registers
+
+__global__ __launch_bounds__(kSelThreads) void sel_fused_kernel(FusedArgs a) {
+  __shared__ uint32_t smem[kFusedLdsWords];
   __shared__ int sm[kSelWaves + 1];
-  __shared__ int s_digit, s_rank;
-  for (int e = threadIdx.x; e < kSelBins; e += kSelThreads) hist[e] = ss->hist[e];
-  const int n_valid = ss->n_valid;
-  long long k;
-  if (k_evict >= 0) {
-    k = min(k_evict, n_valid);
-  } else {
-    k = (long long)floor((double)evict_fraction * (double)n_valid);
-    if (k < 0) k = 0;
-    if (k > n_valid) k = n_valid;
+  __shared__ int s_digit, s_rank, s_id, s_base;
+  FusedScratch* fs = a.fs;
+  const int tid = threadIdx.x;
+  const int G = gridDim.x;
+  const int g = blockIdx.x;
+  const int ntiles = div_up(a.n, kSelTile);
+  const int t_begin = min(ntiles, g * a.tiles_per_wg);
+  const int t_end = min(ntiles, t_begin + a.tiles_per_wg);
+  int* lhist = reinterpret_cast<int*>(smem);
+  __shared__ unsigned long long sm64[kSelWaves + 1];
+  // Read with the first input loads (one round trip for both); checked before
+  // the first write to the scratch.
+  const unsigned magic = __hip_atomic_load(&fs->magic, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+  // Key of page i: its ordered score when valid, ~0 otherwise (~0 sorts after
+  // every valid key: the largest non-NaN ordered score is +inf's 0xFF800000).
+  // Both loads are issued together (one round trip, not two).
+  auto page_key = [&](int i) -> uint32_t {
+    const float sc = a.scores[i];
+    const int8_t v = a.valid[i];
+    return v == 1 ? ordered_score(sc) : 0xFFFFFFFFu;
+  };
+  auto tile_key = [&](int t, int j) -> uint32_t {
+    const int i = t * kSelTile + tid * kSelPer + j;
+    return i < a.n ? page_key(i) : 0xFFFFFFFFu;
+  };
+  // Table rows: this workgroup owns rows g, g + G, ...; each row is cut into
+  // chunks of 1,024 entries (one per thread); chunk c of the workgroup is
+  // chunk c % cpr of its (c / cpr)-th row.
+  const bool tables = a.tables != nullptr;
+  const int cpr = tables ? max(1, div_up(a.table_stride, kSelThreads)) : 0;
+  const int my_rows = tables && g < a.num_seqs ? div_up(a.num_seqs - g, G) : 0;
+  const int my_chunks = my_rows * cpr;
+  auto row_len = [&](int row) { return min(max(a.lens[row], 0), a.table_stride); };
+  // Entry of chunk c for this thread: page id (-1 when absent) and the key of
+  // that page when it is a valid page id (~0 otherwise).
+  // The row length and the table entry are loaded together (every entry below
+  // table_stride is in bounds), then the page's flag and score together: two
+  // round trips, not three.
+  auto chunk_entry = [&](int c, int* id_out) -> uint32_t {
+    const int row = g + (c / cpr) * G;
+    const int j = (c % cpr) * kSelThreads + tid;
+    const int len = row_len(row);
+    const int raw = j < a.table_stride ? a.tables[(int64_t)row * a.table_stride + j] : -1;
+    const int id = j < len ? raw : -1;
+    *id_out = id;
+    return (id >= 0 && id < a.n) ? page_key(id) : 0xFFFFFFFFu;
+  };
+
+  // P1: load this workgroup's keys (tiles and table entries) into registers;
+  // histogram the top 12 ordered-score bits of its valid pages.
+  uint32_t tk[kTileRegs][kSelPer];
+  uint32_t rk[kRowRegs];
+  int rid[kRowRegs];
+#pragma unroll
+  for (int u = 0; u < kTileRegs; ++u)
+#pragma unroll
+    for (int j = 0; j < kSelPer; ++j) tk[u][j] = t_begin + u < t_end ? tile_key(t_begin + u, j) : 0xFFFFFFFFu;
+#pragma unroll
+  for (int u = 0; u < kRowRegs; ++u) {
+    rid[u] = -1;
+    rk[u] = u < my_chunks ? chunk_entry(u, &rid[u]) : 0xFFFFFFFFu;
   }
-  __syncthreads();
-  if (k == 0) {
-    if (threadIdx.x == 0) {
-      out->key_thr = 0;
-      out->k = 0;
-      out->n_valid = n_valid;
-      ss->k = 0;
+  if (magic != kScratchMagic) {
+    // The workspace was never initialised (kessie_page_workspace_init): touch
+    // nothing.  `magic` is the same for every workgroup, so all return here.
+    if (g == 0 && tid == 0) {
+      *a.evict_count = -2;
+      if (a.tables != nullptr) *a.gather_count = -2;
     }
     return;
   }
-  sel_pick(hist, kSelBins, (int)k - 1, sm, &s_digit, &s_rank);
-  if (threadIdx.x == 0) {
-    ss->k = (int)k;
-    ss->top = (uint32_t)s_digit;
-    ss->rank = s_rank;
-    out->k = (int)k;
-    out->n_valid = n_valid;
-  }
-}
-
-__global__ __launch_bounds__(kSelThreads) void sel_collect_kernel(const float* __restrict__ scores,
-                                                                  const int8_t* __restrict__ valid, int n,
-                                                                  SelScratch* ss, uint32_t* __restrict__ cand_s,
-                                                                  uint32_t* __restrict__ cand_i) {
-  __shared__ int sm[kSelWaves + 1];
-  __shared__ int s_base;
-  if (ss->k == 0) return;  // written by the previous launch; uniform
-  const int tid = threadIdx.x;
-  const uint32_t top = ss->top;
-  for (int64_t t0 = (int64_t)blockIdx.x * kSelTile; t0 < n; t0 += (int64_t)gridDim.x * kSelTile) {
-    uint32_t ks[kSelPer];
-    int cnt = 0, mbits = 0;
+  for (int e = tid; e < kSelBins; e += kSelThreads) lhist[e] = 0;
+  __syncthreads();
+  int c = 0;
+  for (int t = t_begin; t < t_end; ++t) {
 #pragma unroll
     for (int j = 0; j < kSelPer; ++j) {
-      const int64_t i = t0 + j * kSelThreads + tid;
-      ks[j] = 0;
-      if (i < n && valid[i] == 1) {
-        ks[j] = ordered_score(scores[i]);
-        if ((ks[j] >> 20) == top) {
+      uint32_t x = 0xFFFFFFFFu;
+#pragma unroll
+      for (int u = 0; u < kTileRegs; ++u)
+        if (t - t_begin == u) x = tk[u][j];
+      if (t - t_begin >= kTileRegs) x = tile_key(t, j);
+      if (x != 0xFFFFFFFFu) {
+        atomicAdd(&lhist[x >> 20], 1);
+        ++c;
+      }
+    }
+  }
+  for (int o = 32; o >= 1; o >>= 1) c += __shfl_xor(c, o, 64);
+  if ((tid & 63) == 0 && c) atomicAdd(&fs->n_valid, c);
+  __syncthreads();
+  if (t_end > t_begin)
+    for (int e = tid; e < kSelBins; e += kSelThreads)
+      if (lhist[e]) atomicAdd(&fs->hist[e], lhist[e]);
+  grid_barrier(fs, (unsigned)G);
+
+  // P2: k, the bin of rank k-1, and that bin's candidates.
+  for (int e = tid; e < kSelBins; e += kSelThreads)
+    lhist[e] = __hip_atomic_load(&fs->hist[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const int n_valid = __hip_atomic_load(&fs->n_valid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  long long kk;
+  if (a.k_evict >= 0) {
+    kk = min(a.k_evict, n_valid);
+  } else {
+    kk = (long long)floor((double)a.evict_fraction * (double)n_valid);
+    kk = max(0LL, min(kk, (long long)n_valid));
+  }
+  const int k = (int)kk;
+  __syncthreads();
+  uint32_t top = 0;
+  int rank = 0;
+  if (k > 0) {
+    sel_pick(lhist, kSelBins, k - 1, sm, &s_digit, &s_rank);
+    top = (uint32_t)s_digit;
+    rank = s_rank;
+    for (int t = t_begin; t < t_end; ++t) {
+      const int base = t * kSelTile + tid * kSelPer;
+      uint32_t ks[kSelPer];
+      int cnt = 0, mbits = 0;
+#pragma unroll
+      for (int j = 0; j < kSelPer; ++j) {
+        uint32_t x = 0xFFFFFFFFu;
+#pragma unroll
+        for (int u = 0; u < kTileRegs; ++u)
+          if (t - t_begin == u) x = tk[u][j];
+        if (t - t_begin >= kTileRegs) x = tile_key(t, j);
+        ks[j] = x;
+        if (x != 0xFFFFFFFFu && (x >> 20) == top) {
           mbits |= 1 << j;
           ++cnt;
         }
       }
-    }
-    int pos = sel_block_scan(cnt, sm);
-    if (tid == 0 && sm[kSelWaves] > 0) s_base = atomicAdd(&ss->ncand, sm[kSelWaves]);
-    __syncthreads();
-    pos += s_base;
+      int pos = sel_block_scan(cnt, sm);
+      if (tid == 0 && sm[kSelWaves] > 0) s_base = atomicAdd(&fs->ncand, sm[kSelWaves]);
+      __syncthreads();
+      pos += s_base;
 #pragma unroll
-    for (int j = 0; j < kSelPer; ++j) {
-      if (!((mbits >> j) & 1)) continue;
-      cand_s[pos] = ks[j] & 0xFFFFFu;
-      cand_i[pos] = (uint32_t)(t0 + j * kSelThreads + tid);
-      ++pos;
+      for (int j = 0; j < kSelPer; ++j) {
+        if (!((mbits >> j) & 1)) continue;
+        a.cand_s[pos] = ks[j] & 0xFFFFFu;
+        a.cand_i[pos] = (uint32_t)(base + j);
+        ++pos;
+      }
+      __syncthreads();  // s_base and sm are reused by the next tile
     }
-    __syncthreads();  // s_base and sm are reused by the next tile
   }
-}
+  grid_barrier(fs, 2u * G);
 
-__global__ __launch_bounds__(kSelThreads) void sel_resolve_kernel(const SelScratch* ss, const uint32_t* g_cand_s,
-                                                                  const uint32_t* g_cand_i, SelectOut* out) {
-  __shared__ int hist[2048];
-  __shared__ uint32_t lds_s[kSelCap];  // low 20 bits of the ordered score
-  __shared__ uint32_t lds_i[kSelCap];  // page id
-  __shared__ int sm[kSelWaves + 1];
-  __shared__ int s_digit, s_rank, s_id;
-  if (ss->k == 0) return;
-  const int tid = threadIdx.x;
-  const int nc = ss->ncand;
-  const uint32_t top = ss->top;
-  int rank = ss->rank;
-  const uint32_t* cs = g_cand_s;
-  const uint32_t* ci = g_cand_i;
-  if (nc <= kSelCap) {
-    for (int q = tid; q < nc; q += kSelThreads) {
-      lds_s[q] = g_cand_s[q];
-      lds_i[q] = g_cand_i[q];
-    }
-    cs = lds_s;
-    ci = lds_i;
-  }
-  __syncthreads();
-  auto cand_score = [&](int q) { return cs[q]; };
-  auto cand_id = [&](int q) { return ci[q]; };
-  uint32_t low = 0;
-  int ties = 0;
-  for (int pass = 0; pass < 2; ++pass) {
-    const int sh = 10 - 10 * pass;
-    for (int e = tid; e < 1024; e += kSelThreads) hist[e] = 0;
-    __syncthreads();
-    for (int q = tid; q < nc; q += kSelThreads) {
-      const uint32_t v = cand_score(q);
-      if (pass == 0 || (v >> 10) == low) atomicAdd(&hist[(v >> sh) & 1023u], 1);
+  // P3: the threshold key (identical in every workgroup), then the counts.
+  unsigned long long key_thr = 0;
+  if (k > 0) {
+    int* rhist = reinterpret_cast<int*>(smem);
+    uint32_t* lds_s = smem + 2048;
+    uint32_t* lds_i = smem + 2048 + kSelCap;
+    const int nc = __hip_atomic_load(&fs->ncand, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t* cs = a.cand_s;
+    const uint32_t* ci = a.cand_i;
+    if (nc <= kSelCap) {
+      for (int q = tid; q < nc; q += kSelThreads) {
+        lds_s[q] = a.cand_s[q];
+        lds_i[q] = a.cand_i[q];
+      }
+      cs = lds_s;
+      ci = lds_i;
     }
     __syncthreads();
-    sel_pick(hist, 1024, rank, sm, &s_digit, &s_rank);
-    low = (low << 10) | (uint32_t)s_digit;
-    rank = s_rank;
-    ties = hist[s_digit];
-    __syncthreads();
-  }
-  const uint32_t score = (top << 20) | low;
-  uint32_t idp = 0;
-  if (ties == 1) {
-    for (int q = tid; q < nc; q += kSelThreads)
-      if (cand_score(q) == low) s_id = (int)cand_id(q);
-    __syncthreads();
-    idp = (uint32_t)s_id;
-  } else {
-    for (int pass = 0; pass < 3; ++pass) {
-      const int width = pass < 2 ? 11 : 10;
-      const int sh = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
-      for (int e = tid; e < 2048; e += kSelThreads) hist[e] = 0;
+    uint32_t low = 0;
+    int ties = 0;
+    for (int pass = 0; pass < 2; ++pass) {
+      const int sh = 10 - 10 * pass;
+      for (int e = tid; e < 1024; e += kSelThreads) rhist[e] = 0;
       __syncthreads();
       for (int q = tid; q < nc; q += kSelThreads) {
-        if (cand_score(q) != low) continue;
-        const uint32_t id = cand_id(q);
-        if (pass == 0 || (id >> (sh + width)) == idp) atomicAdd(&hist[(id >> sh) & ((1u << width) - 1u)], 1);
+        const uint32_t v = cs[q];
+        if (pass == 0 || (v >> 10) == low) atomicAdd(&rhist[(v >> sh) & 1023u], 1);
       }
       __syncthreads();
-      sel_pick(hist, 2048, rank, sm, &s_digit, &s_rank);
-      idp = (idp << width) | (uint32_t)s_digit;
+      sel_pick(rhist, 1024, rank, sm, &s_digit, &s_rank);
+      low = (low << 10) | (uint32_t)s_digit;
       rank = s_rank;
+      ties = rhist[s_digit];
+      __syncthreads();
+    }
+    uint32_t idp = 0;
+    if (ties == 1) {
+      for (int q = tid; q < nc; q += kSelThreads)
+        if (cs[q] == low) s_id = (int)ci[q];
+      __syncthreads();
+      idp = (uint32_t)s_id;
+    } else {
+      for (int pass = 0; pass < 3; ++pass) {
+        const int width = pass < 2 ? 11 : 10;
+        const int sh = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
+        for (int e = tid; e < 2048; e += kSelThreads) rhist[e] = 0;
+        __syncthreads();
+        for (int q = tid; q < nc; q += kSelThreads) {
+          if (cs[q] != low) continue;
+          const uint32_t id = ci[q];
+          if (pass == 0 || (id >> (sh + width)) == idp) atomicAdd(&rhist[(id >> sh) & ((1u << width) - 1u)], 1);
+        }
+        __syncthreads();
+        sel_pick(rhist, 2048, rank, sm, &s_digit, &s_rank);
+        idp = (idp << width) | (uint32_t)s_digit;
+        rank = s_rank;
+        __syncthreads();
+      }
+    }
+    key_thr = ((unsigned long long)((top << 20) | low) << 32) | idp;
+  }
+  // Evicted: a valid page whose (key, id) is <= the threshold (k > 0 only).
+  auto evicted_key = [&](uint32_t x, int i) -> bool {
+    return k > 0 && x != 0xFFFFFFFFu && (((unsigned long long)x << 32) | (uint32_t)i) <= key_thr;
+  };
+  auto tile_key_at = [&](int t, int j) -> uint32_t {
+    uint32_t x = 0xFFFFFFFFu;
+#pragma unroll
+    for (int u = 0; u < kTileRegs; ++u)
+      if (t - t_begin == u) x = tk[u][j];
+    if (t - t_begin >= kTileRegs) x = tile_key(t, j);
+    return x;
+  };
+  // Table entry of chunk c: survives when it names a valid page that is not evicted.
+  auto chunk_survivor = [&](int cc, int* id_out) -> bool {
+    int id = -1;
+    uint32_t x = 0xFFFFFFFFu;
+#pragma unroll
+    for (int u = 0; u < kRowRegs; ++u)
+      if (cc == u) {
+        id = rid[u];
+        x = rk[u];
+      }
+    if (cc >= kRowRegs) x = chunk_entry(cc, &id);
+    *id_out = id;
+    return x != 0xFFFFFFFFu && !evicted_key(x, id);
+  };
+  {
+    int ce = 0;
+    for (int t = t_begin; t < t_end; ++t)
+#pragma unroll
+      for (int j = 0; j < kSelPer; ++j) ce += evicted_key(tile_key_at(t, j), t * kSelTile + tid * kSelPer + j);
+    for (int o = 32; o >= 1; o >>= 1) ce += __shfl_xor(ce, o, 64);
+    if ((tid & 63) == 0) sm[tid >> 6] = ce;
+    __syncthreads();
+    if (tid == 0) {
+      int s = 0;
+      for (int w = 0; w < kSelWaves; ++w) s += sm[w];
+      __hip_atomic_store(&fs->wg_evict[g], s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+  }
+  // Rows of at most 1,024 entries, at most kRowRegs of them: all counted (and
+  // later placed) by one packed scan, a 16-bit field per row.
+  const bool packed_rows = cpr == 1 && my_rows <= kRowRegs;
+  unsigned long long pk = 0;
+  if (packed_rows) {
+#pragma unroll
+    for (int u = 0; u < kRowRegs; ++u) {
+      int id;
+      if (u < my_rows && chunk_survivor(u, &id)) pk += 1ull << (16 * u);
+    }
+    unsigned long long wsum = pk;  // pk itself is kept for the placing scan in P4
+    for (int o = 32; o >= 1; o >>= 1) wsum += __shfl_xor(wsum, o, 64);
+    if ((tid & 63) == 0) sm64[tid >> 6] = wsum;
+    __syncthreads();
+    if (tid < my_rows) {
+      unsigned long long t = 0;
+      for (int w = 0; w < kSelWaves; ++w) t += sm64[w];
+      __hip_atomic_store(&a.row_count[g + tid * G], (int)((t >> (16 * tid)) & 0xFFFFull), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+  } else {
+    for (int rr = 0; rr < my_rows; ++rr) {
+      int cs = 0;
+      for (int cc = rr * cpr; cc < (rr + 1) * cpr; ++cc) {
+        int id;
+        cs += chunk_survivor(cc, &id);
+      }
+      for (int o = 32; o >= 1; o >>= 1) cs += __shfl_xor(cs, o, 64);
+      if ((tid & 63) == 0) sm[tid >> 6] = cs;
+      __syncthreads();
+      if (tid == 0) {
+        int s = 0;
+        for (int w = 0; w < kSelWaves; ++w) s += sm[w];
+        __hip_atomic_store(&a.row_count[g + rr * G], s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
       __syncthreads();
     }
   }
-  if (tid == 0) out->key_thr = ((unsigned long long)score << 32) | idp;
-}
+  grid_barrier(fs, 3u * G);
 
-// ---------------------------------------------------------------------------
-// Table compaction
-// ---------------------------------------------------------------------------
-// One block per table row: survivors keep logical order; the rest of the row
-// is filled with -1; new_lens[row] = survivors.
-__global__ __launch_bounds__(kThreads) void compact_rows_kernel(const int32_t* tables, const int32_t* lens,
-                                                                const int8_t* valid, int32_t* new_tables,
-                                                                int32_t* new_lens, int table_stride, int num_pages) {
-  __shared__ int sm[kWaves + 1];
-  const int row = blockIdx.x;
-  const int32_t* in = tables + (int64_t)row * table_stride;
-  int32_t* outr = new_tables + (int64_t)row * table_stride;
-  const int len = min(max(lens[row], 0), table_stride);
-  int carry = 0;
-  for (int base = 0; base < table_stride; base += kChunk) {
-    const int first = base + threadIdx.x * kItems;
-    unsigned flags = 0;
-    int ids[kItems];
-    int c = 0;
-#pragma unroll
-    for (int e = 0; e < kItems; ++e) {
-      const int j = first + e;
-      ids[e] = -1;
-      if (j < len) {
-        const int id = in[j];
-        ids[e] = id;
-        if (id >= 0 && id < num_pages && valid[id] == 1) {
-          flags |= 1u << e;
-          ++c;
-        }
-      }
+  // P4: read what the other workgroups published, leave the scratch, then
+  // write the evict list (ascending ids, clearing the pages' valid flags) and
+  // the compacted tables.
+  const bool failed = __hip_atomic_load(&fs->timed_out, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+  if (tid < 64) {
+    int v = 0;
+    if (tid < g) v = __hip_atomic_load(&fs->wg_evict[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    if (tid == 0) s_base = v;
+  }
+  int* row_off = reinterpret_cast<int*>(smem);  // gather-list offset of every row
+  int run = 0;
+  if (tables) {
+    for (int r0 = 0; r0 < a.num_seqs; r0 += kSelThreads) {
+      const int r = r0 + tid;
+      const int v = r < a.num_seqs ? __hip_atomic_load(&a.row_count[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                   : 0;
+      const int ex = sel_block_scan(v, sm);
+      if (r < a.num_seqs) row_off[r] = run + ex;
+      run += sm[kSelWaves];
     }
-    int total;
-    int pos = carry + block_exclusive_scan(c, &total, sm);
-#pragma unroll
-    for (int e = 0; e < kItems; ++e)
-      if (flags & (1u << e)) outr[pos++] = ids[e];
-    carry += total;
   }
   __syncthreads();
-  for (int j = carry + threadIdx.x; j < table_stride; j += kThreads) outr[j] = -1;
-  if (threadIdx.x == 0) new_lens[row] = carry;
+  // The last workgroup out restores the scratch for the next call: every other
+  // workgroup has passed its last barrier and its last read of it.
+  if (tid == 0) s_id = (int)__hip_atomic_fetch_add(&fs->done, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  if (s_id == G - 1) {
+    for (int e = tid; e < kSelBins; e += kSelThreads)
+      __hip_atomic_store(&fs->hist[e], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) {
+      __hip_atomic_store(&fs->bar, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&fs->done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&fs->timed_out, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&fs->n_valid, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&fs->ncand, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  int carry = s_base;
+  for (int t = t_begin; t < t_end; ++t) {
+    const int base = t * kSelTile + tid * kSelPer;
+    unsigned flags = 0;
+    int cnt = 0;
+#pragma unroll
+    for (int j = 0; j < kSelPer; ++j)
+      if (evicted_key(tile_key_at(t, j), base + j)) {
+        flags |= 1u << j;
+        ++cnt;
+      }
+    int pos = carry + sel_block_scan(cnt, sm);
+    const int total = sm[kSelWaves];
+#pragma unroll
+    for (int j = 0; j < kSelPer; ++j) {
+      if (!(flags & (1u << j))) continue;
+      a.evict_list[pos++] = base + j;
+      a.valid[base + j] = 0;
+    }
+    carry += total;
+  }
+  if (tables) {
+    if (packed_rows) {
+      const unsigned long long ex = sel_block_scan64(pk, sm64);
+      const unsigned long long tot = sm64[kSelWaves];
+#pragma unroll
+      for (int u = 0; u < kRowRegs; ++u) {
+        if (u >= my_rows) continue;
+        const int row = g + u * G;
+        int32_t* outr = a.new_tables + (int64_t)row * a.table_stride;
+        int id;
+        if (chunk_survivor(u, &id)) {
+          const int pos = (int)((ex >> (16 * u)) & 0xFFFFull);
+          outr[pos] = id;
+          a.gather_idx[row_off[row] + pos] = id;
+        }
+        const int rc = (int)((tot >> (16 * u)) & 0xFFFFull);
+        for (int j = rc + tid; j < a.table_stride; j += kSelThreads) outr[j] = -1;
+        if (tid == 0) a.new_lens[row] = rc;
+      }
+    } else {
+      for (int rr = 0; rr < my_rows; ++rr) {
+        const int row = g + rr * G;
+        int32_t* outr = a.new_tables + (int64_t)row * a.table_stride;
+        const int off = row_off[row];
+        int rc = 0;
+        for (int cc = rr * cpr; cc < (rr + 1) * cpr; ++cc) {
+          int id;
+          const int sv = chunk_survivor(cc, &id) ? 1 : 0;
+          const int pos = rc + sel_block_scan(sv, sm);
+          rc += sm[kSelWaves];
+          if (sv) {
+            outr[pos] = id;
+            a.gather_idx[off + pos] = id;
+          }
+        }
+        for (int j = rc + tid; j < a.table_stride; j += kSelThreads) outr[j] = -1;
+        if (tid == 0) a.new_lens[row] = rc;
+      }
+    }
+    if (g == 0 && tid == 0) *a.gather_count = failed ? -1 : run;
+  }
+  if (g == 0 && tid == 0) *a.evict_count = failed ? -1 : k;
 }
 
-// gather_idx[row_off[row] + j] = new_tables[row][j], j < new_lens[row].
-__global__ __launch_bounds__(kThreads) void flatten_rows_kernel(const int32_t* new_tables, const int32_t* new_lens,
-                                                                const int* row_off, int table_stride,
-                                                                int32_t* gather_idx) {
+// ---------------------------------------------------------------------------
+// Table compaction in one launch: one workgroup per table row; the row's
+// offset in the gather list comes from a decoupled look-back over the rows
+// before it (flags[row] = state << 62 | value, state 1 = the row's own count
+// published, 2 = the inclusive prefix published), so no second pass and no
+// second launch.  The flags must be zero on entry (the single-workgroup score
+// eviction clears them in the fused call; kessie_page_compact launches a fill
+// kernel first).  Workgroups only wait for lower-numbered rows, which were
+// dispatched earlier and publish without waiting; each wait is bounded and a
+// workgroup whose wait runs out counts the earlier rows itself, so the result
+// never depends on the wait.
+// ---------------------------------------------------------------------------
+constexpr int kLbThreads = 256;
+constexpr unsigned long long kLbAgg = 1ull << 62, kLbPre = 2ull << 62, kLbMask = (1ull << 62) - 1ull;
+
+__device__ __forceinline__ bool lb_survives(int id, const int8_t* valid, int num_pages) {
+  return id >= 0 && id < num_pages && valid[id] == 1;
+}
+
+__global__ __launch_bounds__(kLbThreads) void compact_lookback_kernel(
+    const int32_t* __restrict__ tables, const int32_t* __restrict__ lens, const int8_t* __restrict__ valid,
+    int32_t* __restrict__ new_tables, int32_t* __restrict__ new_lens, int32_t* __restrict__ gather_idx,
+    int32_t* __restrict__ gather_count, int num_seqs, int table_stride, int num_pages,
+    unsigned long long* flags) {
+  __shared__ int sm[kWaves + 1];
+  __shared__ long long s_prefix;
   const int row = blockIdx.x;
-  const int n = new_lens[row];
-  const int off = row_off[row];
-  for (int j = threadIdx.x; j < n; j += kThreads) gather_idx[off + j] = new_tables[(int64_t)row * table_stride + j];
+  const int tid = threadIdx.x;
+  const int32_t* in = tables + (int64_t)row * table_stride;
+  int32_t* outr = new_tables + (int64_t)row * table_stride;
+  auto row_len = [&](int rr) { return min(max(lens[rr], 0), table_stride); };
+  const int len = row_len(row);
+
+  int cnt = 0;
+  for (int j = tid; j < len; j += kLbThreads) cnt += lb_survives(in[j], valid, num_pages);
+  int total;
+  block_exclusive_scan(cnt, &total, sm);
+
+  // Look-back by the first wave: lane l reads the flag of row (j_hi - l); the
+  // nearest row that has published its inclusive prefix ends the walk (rows
+  // before 0 read as an inclusive prefix of 0).
+  if (tid < 64) {
+    const int lane = tid;
+    if (lane == 0)
+      __hip_atomic_store(&flags[row], (row == 0 ? kLbPre : kLbAgg) | (unsigned long long)total, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    long long prefix = 0;
+    int j_hi = row - 1, spins = 0;
+    bool fallback = false;
+    while (j_hi >= 0) {
+      const int j = j_hi - lane;
+      const unsigned long long f =
+          j >= 0 ? __hip_atomic_load(&flags[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : kLbPre;
+      const unsigned long long st = f & ~kLbMask;
+      const unsigned long long pre = __builtin_amdgcn_ballot_w64(st == kLbPre);
+      const unsigned long long nr = __builtin_amdgcn_ballot_w64(st != kLbPre && st != kLbAgg);
+      const int stop = pre ? __builtin_ctzll(pre) : 64;               // nearest inclusive prefix
+      const unsigned long long need = stop == 64 ? ~0ull : ((2ull << stop) - 1ull);  // lanes 0..stop
+      if (nr & need) {  // a needed row has not published yet
+        if (++spins > kSpinLimit) {
+          fallback = true;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+        continue;
+      }
+      long long v = ((need >> lane) & 1ull) ? (long long)(f & kLbMask) : 0;
+      for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+      prefix += v;
+      if (stop < 64) break;
+      j_hi -= 64;
+    }
+    if (lane == 0) {
+      if (fallback) {
+        s_prefix = -1;  // counted below by the whole workgroup
+      } else {
+        s_prefix = prefix;
+        if (row > 0)
+          __hip_atomic_store(&flags[row], kLbPre | (unsigned long long)(prefix + total), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+  __syncthreads();
+  long long prefix = s_prefix;
+  if (prefix < 0) {  // bounded wait ran out: count the earlier rows directly
+    int c = 0;
+    for (int rr = 0; rr < row; ++rr) {
+      const int l = row_len(rr);
+      const int32_t* rin = tables + (int64_t)rr * table_stride;
+      for (int j = tid; j < l; j += kLbThreads) c += lb_survives(rin[j], valid, num_pages);
+    }
+    int t2;
+    block_exclusive_scan(c, &t2, sm);
+    prefix = t2;
+    if (tid == 0)
+      __hip_atomic_store(&flags[row], kLbPre | (unsigned long long)(prefix + total), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+  }
+
+  // Write the row: survivors in logical order, -1 after them.
+  int rc = 0;
+  for (int j0 = 0; j0 < len; j0 += kLbThreads) {
+    const int j = j0 + tid;
+    const int id = j < len ? in[j] : -1;
+    const int sv = (j < len && lb_survives(id, valid, num_pages)) ? 1 : 0;
+    int t3;
+    const int pos = rc + block_exclusive_scan(sv, &t3, sm);
+    if (sv) {
+      outr[pos] = id;
+      gather_idx[prefix + pos] = id;
+    }
+    rc += t3;
+  }
+  for (int j = rc + tid; j < table_stride; j += kLbThreads) outr[j] = -1;
+  if (tid == 0) {
+    new_lens[row] = rc;
+    if (row == num_seqs - 1) *gather_count = (int32_t)(prefix + rc);
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void clear_flags_kernel(unsigned long long* flags, int n) {
+  for (int j = blockIdx.x * kThreads + threadIdx.x; j < n; j += gridDim.x * kThreads) flags[j] = 0ull;
 }
 
 // ---------------------------------------------------------------------------
@@ -738,11 +1131,11 @@ __global__ __launch_bounds__(kThreads) void insert_vec_kernel(InsertArgs a) {
 int num_blocks(int n) { return div_up(max(n, 1), kChunk); }
 
 struct Workspace {
-  SelectOut* sel;
   int* counts;
   int* offsets;
-  int* rows;  // per-row offsets (table compaction)
-  SelScratch* ss;
+  int* rows;                   // per-row counts (table compaction of the grid-barrier call)
+  unsigned long long* flags;   // per-row look-back flags (same memory as rows)
+  FusedScratch* fs;
   uint32_t* cand_s;  // select candidates (n each)
   uint32_t* cand_i;
 };
@@ -751,11 +1144,10 @@ constexpr size_t round256(size_t b) { return (b + 255) / 256 * 256; }
 
 size_t workspace_bytes(int n) {
   const size_t nb = (size_t)num_blocks(n);
-  size_t b = 256;                                   // SelectOut + misc
+  size_t b = round256(sizeof(FusedScratch));        // fused-select scratch (first: its offset is fixed)
   b += round256(nb * sizeof(int));                  // counts
   b += round256(nb * sizeof(int));                  // offsets
-  b += round256(((size_t)n + 1) * sizeof(int));     // row offsets
-  b += round256(sizeof(SelScratch));                // select histogram + counters
+  b += round256(((size_t)n + 1) * sizeof(unsigned long long));  // per-row counts / look-back flags
   b += 2 * round256((size_t)n * sizeof(uint32_t));  // select candidates
   return b;
 }
@@ -764,16 +1156,15 @@ Workspace carve(void* ws, int n) {
   Workspace w;
   char* c = static_cast<char*>(ws);
   const size_t nb = (size_t)num_blocks(n);
-  w.sel = reinterpret_cast<SelectOut*>(c);
-  c += 256;
+  w.fs = reinterpret_cast<FusedScratch*>(c);
+  c += round256(sizeof(FusedScratch));
   w.counts = reinterpret_cast<int*>(c);
   c += round256(nb * sizeof(int));
   w.offsets = reinterpret_cast<int*>(c);
   c += round256(nb * sizeof(int));
   w.rows = reinterpret_cast<int*>(c);
-  c += round256(((size_t)n + 1) * sizeof(int));
-  w.ss = reinterpret_cast<SelScratch*>(c);
-  c += round256(sizeof(SelScratch));
+  w.flags = reinterpret_cast<unsigned long long*>(c);
+  c += round256(((size_t)n + 1) * sizeof(unsigned long long));
   w.cand_s = reinterpret_cast<uint32_t*>(c);
   c += round256((size_t)n * sizeof(uint32_t));
   w.cand_i = reinterpret_cast<uint32_t*>(c);
@@ -843,6 +1234,29 @@ int insert_dispatch(InsertArgs& a, int dtype, hipStream_t s) {
   return KESSIE_ERR_UNSUPPORTED;
 }
 
+// Score eviction (+ table compaction when tables != nullptr): the clear launch
+// and the fused launch.
+int select_dispatch(const float* scores, int8_t* page_valid, int num_pages, int k_evict, float evict_fraction,
+                    int32_t* evict_list, int32_t* evict_count, const int32_t* tables, const int32_t* lens,
+                    int num_seqs, int table_stride, int32_t* new_tables, int32_t* new_lens, int32_t* gather_idx,
+                    int32_t* gather_count, void* workspace, size_t workspace_bytes, hipStream_t s) {
+  KESSIE_REQUIRE(num_pages >= 0, KESSIE_ERR_INVALID, "select evict: num_pages %d", num_pages);
+  KESSIE_REQUIRE(scores && page_valid && evict_list && evict_count, KESSIE_ERR_INVALID, "select evict: null pointer");
+  KESSIE_REQUIRE(k_evict >= 0 || (evict_fraction >= 0.0f && evict_fraction <= 1.0f), KESSIE_ERR_INVALID,
+                 "select evict: evict_fraction %g outside [0,1]", (double)evict_fraction);
+  const int nws = max(num_pages, num_seqs);
+  int st = check_ws(workspace, workspace_bytes, nws, "select evict");
+  if (st) return st;
+  Workspace w = carve(workspace, nws);
+  const int ntiles = div_up(max(num_pages, 1), kSelTile);
+  const int G = max(1, min(kFusedMaxG, ntiles));
+  FusedArgs a{scores,       page_valid, num_pages, k_evict,  evict_fraction, evict_list, evict_count,
+              tables,       lens,       num_seqs,  table_stride, new_tables, new_lens,   gather_idx,
+              gather_count, w.fs,       w.cand_s,  w.cand_i,   w.rows,       div_up(ntiles, G)};
+  hipLaunchKernelGGL(sel_fused_kernel, dim3(G), dim3(kSelThreads), 0, s, a);
+  return check_launch("select evict");
+}
+
 }  // namespace pages
 }  // namespace kessie
 
@@ -850,6 +1264,16 @@ using namespace kessie;
 using namespace kessie::pages;
 
 extern "C" size_t kessie_page_workspace_bytes(int num_pages) { return pages::workspace_bytes(max(num_pages, 0)); }
+
+extern "C" int kessie_page_workspace_init(void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  KESSIE_REQUIRE(workspace != nullptr && workspace_bytes >= pages::workspace_bytes(0), KESSIE_ERR_WORKSPACE,
+                 "page workspace init: %zu bytes (at least %zu)", workspace_bytes, pages::workspace_bytes(0));
+  KESSIE_REQUIRE(aligned16(workspace), KESSIE_ERR_INVALID, "page workspace init: not 16-byte aligned");
+  hipLaunchKernelGGL(scratch_init_kernel, dim3(1), dim3(kThreads), 0, as_stream(stream),
+                     static_cast<FusedScratch*>(workspace));
+  return check_launch("page workspace init");
+}
 
 extern "C" int kessie_page_insert_paged(void* kv_pool, int64_t page_stride, int64_t tok_stride, int64_t kv_stride,
                                         int64_t head_stride, const void* new_k, const void* new_v,
@@ -875,7 +1299,7 @@ extern "C" int kessie_page_evict_list(int8_t* page_valid, const int32_t* page_po
   if (st) return st;
   hipStream_t s = as_stream(stream);
   Workspace w = carve(workspace, num_pages);
-  PredArgs a{kPredFreed, page_valid, page_positions, allocated, evict_before_pos, nullptr, nullptr, nullptr};
+  PredArgs a{kPredFreed, page_valid, page_positions, allocated, evict_before_pos};
   return ordered_compact(a, num_pages, freed_list, freed_count, w, s, page_valid, allocated);
 }
 
@@ -883,25 +1307,30 @@ extern "C" int kessie_page_select_evict(const float* scores, int8_t* page_valid,
                                         float evict_fraction, int32_t* evict_list, int32_t* evict_count,
                                         void* workspace, size_t workspace_bytes, void* stream) {
   clear_error();
-  KESSIE_REQUIRE(num_pages >= 0, KESSIE_ERR_INVALID, "select evict: num_pages %d", num_pages);
-  KESSIE_REQUIRE(scores && page_valid && evict_list && evict_count, KESSIE_ERR_INVALID, "select evict: null pointer");
-  KESSIE_REQUIRE(k_evict >= 0 || (evict_fraction >= 0.0f && evict_fraction <= 1.0f), KESSIE_ERR_INVALID,
-                 "select evict: evict_fraction %g outside [0,1]", (double)evict_fraction);
-  int st = check_ws(workspace, workspace_bytes, num_pages, "select evict");
-  if (st) return st;
-  hipStream_t s = as_stream(stream);
-  Workspace w = carve(workspace, num_pages);
-  const int sg = max(1, min(kSelMaxGrid, div_up(num_pages, kSelTile)));
-  hipLaunchKernelGGL(sel_clear_kernel, dim3(1), dim3(kThreads), 0, s, w.ss);
-  hipLaunchKernelGGL(sel_hist_kernel, dim3(sg), dim3(kSelThreads), 0, s, scores, page_valid, num_pages, w.ss);
-  hipLaunchKernelGGL(sel_bucket_kernel, dim3(1), dim3(kSelThreads), 0, s, w.ss, k_evict, evict_fraction, w.sel);
-  hipLaunchKernelGGL(sel_collect_kernel, dim3(sg), dim3(kSelThreads), 0, s, scores, page_valid, num_pages, w.ss,
-                     w.cand_s, w.cand_i);
-  hipLaunchKernelGGL(sel_resolve_kernel, dim3(1), dim3(kSelThreads), 0, s, w.ss, w.cand_s, w.cand_i, w.sel);
-  st = check_launch("select evict (radix select)");
-  if (st) return st;
-  PredArgs a{kPredScoreEvict, page_valid, nullptr, nullptr, 0, scores, &w.sel->key_thr, &w.sel->k};
-  return ordered_compact(a, num_pages, evict_list, evict_count, w, s, page_valid);
+  return pages::select_dispatch(scores, page_valid, num_pages, k_evict, evict_fraction, evict_list, evict_count,
+                                nullptr, nullptr, 0, 0, nullptr, nullptr, nullptr, nullptr, workspace,
+                                workspace_bytes, as_stream(stream));
+}
+
+extern "C" int kessie_page_evict_compact(const float* scores, int8_t* page_valid, int num_pages, int k_evict,
+                                         float evict_fraction, int32_t* evict_list, int32_t* evict_count,
+                                         const int32_t* tables, const int32_t* lens, int num_seqs,
+                                         int table_stride, int32_t* new_tables, int32_t* new_lens,
+                                         int32_t* gather_idx, int32_t* gather_count, void* workspace,
+                                         size_t workspace_bytes, void* stream) {
+  clear_error();
+  KESSIE_REQUIRE(num_seqs >= 0 && table_stride >= 0, KESSIE_ERR_INVALID, "evict compact: S=%d W=%d", num_seqs,
+                 table_stride);
+  KESSIE_REQUIRE(num_seqs <= kFusedMaxRows, KESSIE_ERR_UNSUPPORTED,
+                 "evict compact: %d sequences (at most %d; call select_evict + compact)", num_seqs, kFusedMaxRows);
+  KESSIE_REQUIRE((int64_t)num_seqs * table_stride <= INT_MAX, KESSIE_ERR_UNSUPPORTED, "evict compact: table too big");
+  KESSIE_REQUIRE(num_seqs == 0 || (tables && lens && new_tables && new_lens && gather_idx && gather_count),
+                 KESSIE_ERR_INVALID, "evict compact: null table pointer");
+  KESSIE_REQUIRE(tables == nullptr || tables != new_tables, KESSIE_ERR_INVALID,
+                 "evict compact: tables and new_tables must differ");
+  return pages::select_dispatch(scores, page_valid, num_pages, k_evict, evict_fraction, evict_list, evict_count,
+                                num_seqs > 0 ? tables : nullptr, lens, num_seqs, table_stride, new_tables, new_lens,
+                                gather_idx, gather_count, workspace, workspace_bytes, as_stream(stream));
 }
 
 extern "C" int kessie_page_compact(const int32_t* tables, const int32_t* lens, const int8_t* page_valid,
@@ -921,11 +1350,12 @@ extern "C" int kessie_page_compact(const int32_t* tables, const int32_t* lens, c
   if (st) return st;
   hipStream_t s = as_stream(stream);
   Workspace w = carve(workspace, max(n, num_seqs));
-  hipLaunchKernelGGL(compact_rows_kernel, dim3(num_seqs), dim3(kThreads), 0, s, tables, lens, page_valid, new_tables,
-                     new_lens, table_stride, num_pages);
-  hipLaunchKernelGGL(scan_counts_kernel, dim3(1), dim3(kThreads), 0, s, new_lens, num_seqs, w.rows, gather_count);
-  hipLaunchKernelGGL(flatten_rows_kernel, dim3(num_seqs), dim3(kThreads), 0, s, new_tables, new_lens, w.rows,
-                     table_stride, gather_idx);
+  // A fill kernel zeroes the look-back flags (graph-capture safe), then one
+  // workgroup per row compacts it and places it in the gather list.
+  hipLaunchKernelGGL(clear_flags_kernel, dim3(max(1, min(64, div_up(num_seqs, kThreads)))), dim3(kThreads), 0, s,
+                     w.flags, num_seqs);
+  hipLaunchKernelGGL(compact_lookback_kernel, dim3(num_seqs), dim3(kLbThreads), 0, s, tables, lens, page_valid,
+                     new_tables, new_lens, gather_idx, gather_count, num_seqs, table_stride, num_pages, w.flags);
   return check_launch("page compact");
 }
 
@@ -937,7 +1367,7 @@ extern "C" int kessie_page_valid_list(const int8_t* page_valid, int num_pages, i
   int st = check_ws(workspace, workspace_bytes, num_pages, "valid list");
   if (st) return st;
   Workspace w = carve(workspace, num_pages);
-  PredArgs a{kPredValid, page_valid, nullptr, nullptr, 0, nullptr, nullptr, nullptr};
+  PredArgs a{kPredValid, page_valid, nullptr, nullptr, 0};
   return ordered_compact(a, num_pages, out_idx, out_count, w, as_stream(stream));
 }
 

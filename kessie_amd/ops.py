@@ -65,13 +65,21 @@ def _stream_ptr(stream, device) -> C.c_void_p:
 # ---------------------------------------------------------------------------
 _ws_lock = threading.Lock()
 _ws: dict = {}
+# Buffers a larger request superseded.  They are never freed: a HIP graph
+# captured while one of them was current still writes to its address on every
+# replay, so handing that memory back to the caching allocator would let the
+# replay overwrite whatever tensor is allocated there next.  Growth at least
+# doubles the size, so a device/tag pair retires O(log(max bytes)) buffers.
+_ws_retired: list = []
 
 
-def workspace(nbytes: int, device, tag: str = "attn") -> Optional[torch.Tensor]:
+def workspace(nbytes: int, device, tag: str = "attn", init=None) -> Optional[torch.Tensor]:
     """A cached uint8 device buffer of at least ``nbytes`` (None when 0).
 
     Buffers are reused across calls on the same device and tag; callers on
-    different streams that overlap must pass their own buffers instead.
+    different streams that overlap must pass their own buffers instead.  A
+    buffer outgrown by a larger request is kept alive, not freed (graphs
+    captured earlier may still address it).
     """
     if nbytes <= 0:
         return None
@@ -80,7 +88,13 @@ def workspace(nbytes: int, device, tag: str = "attn") -> Optional[torch.Tensor]:
     with _ws_lock:
         buf = _ws.get(key)
         if buf is None or buf.numel() < nbytes:
-            buf = torch.empty(max(nbytes, 1 << 16), dtype=torch.uint8, device=dev)
+            size = max(nbytes, 1 << 16)
+            if buf is not None:
+                _ws_retired.append(buf)
+                size = max(size, 2 * buf.numel())
+            buf = torch.empty(size, dtype=torch.uint8, device=dev)
+            if init is not None:
+                init(buf)
             _ws[key] = buf
         return buf
 
@@ -397,8 +411,15 @@ def rope_remap_paged(pool: torch.Tensor, orig_pos: torch.Tensor, tgt_pos: torch.
 # ---------------------------------------------------------------------------
 # Page management
 # ---------------------------------------------------------------------------
+def _init_page_workspace(buf: torch.Tensor) -> None:
+    _lib.check("kessie_page_workspace_init", _lib.load().kessie_page_workspace_init(
+        _ptr(buf), buf.numel(), _stream_ptr(None, buf.device)))
+
+
 def page_workspace(num_pages: int, device) -> Optional[torch.Tensor]:
-    return workspace(_lib.load().kessie_page_workspace_bytes(num_pages), device, "pages")
+    """The cached page-management workspace, prepared by
+    kessie_page_workspace_init when it is (re)allocated."""
+    return workspace(_lib.load().kessie_page_workspace_bytes(num_pages), device, "pages", init=_init_page_workspace)
 
 
 def page_insert(pool: torch.Tensor, new_k: torch.Tensor, new_v: torch.Tensor, target_pages: torch.Tensor,
@@ -492,6 +513,43 @@ def page_compact(tables: torch.Tensor, lens: torch.Tensor, page_valid: torch.Ten
         _ptr(gather_idx), _ptr(gather_count), s, w, page_valid.numel(), _ptr(ws), ws.numel(),
         _stream_ptr(stream, dev)))
     return new_tables, new_lens, gather_idx, gather_count
+
+
+def page_evict_compact(scores: torch.Tensor, page_valid: torch.Tensor, tables: torch.Tensor, lens: torch.Tensor,
+                       k_evict: int = -1, evict_fraction: float = 0.25, evict_list: Optional[torch.Tensor] = None,
+                       evict_count: Optional[torch.Tensor] = None, new_tables: Optional[torch.Tensor] = None,
+                       new_lens: Optional[torch.Tensor] = None, gather_idx: Optional[torch.Tensor] = None,
+                       gather_count: Optional[torch.Tensor] = None, stream=None):
+    """page_select_evict then page_compact by the post-eviction flags, fused
+    into two launches.  Returns (evict_list, evict_count, new_tables, new_lens,
+    gather_idx, gather_count), each equal to the two calls' outputs."""
+    n = page_valid.numel()
+    dev = page_valid.device
+    if scores.dtype != torch.float32 or scores.numel() < n:
+        raise ValueError("scores must be float32 with one entry per page")
+    tables = _contig(tables, "tables")
+    if tables.dtype != torch.int32 or lens.dtype != torch.int32:
+        raise TypeError("tables and lens must be int32")
+    s, w = tables.shape
+    if evict_list is None:
+        evict_list = torch.empty(max(n, 1), dtype=torch.int32, device=dev)
+    if evict_count is None:
+        evict_count = torch.zeros(1, dtype=torch.int32, device=dev)
+    if new_tables is None:
+        new_tables = torch.empty_like(tables)
+    if new_lens is None:
+        new_lens = torch.empty(s, dtype=torch.int32, device=dev)
+    if gather_idx is None:
+        gather_idx = torch.empty(max(s * w, 1), dtype=torch.int32, device=dev)
+    if gather_count is None:
+        gather_count = torch.zeros(1, dtype=torch.int32, device=dev)
+    ws = page_workspace(max(n, s), dev)
+    lib = _lib.load()
+    _lib.check("kessie_page_evict_compact", lib.kessie_page_evict_compact(
+        _ptr(_contig(scores, "scores")), _ptr(page_valid), n, int(k_evict), float(evict_fraction),
+        _ptr(evict_list), _ptr(evict_count), _ptr(tables), _ptr(_contig(lens, "lens")), s, w, _ptr(new_tables),
+        _ptr(new_lens), _ptr(gather_idx), _ptr(gather_count), _ptr(ws), ws.numel(), _stream_ptr(stream, dev)))
+    return evict_list, evict_count, new_tables, new_lens, gather_idx, gather_count
 
 
 def page_valid_list(page_valid: torch.Tensor, stream=None):

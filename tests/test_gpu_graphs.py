@@ -162,3 +162,85 @@ def test_graph_prefill_varlen_split(dev, monkeypatch):
         ops.fog_prefill_varlen(q, qsl, 200, pool, table, lens, max(ctxs), fog_bias=bias, out=want)
         torch.cuda.synchronize()
         assert torch.equal(got, want), f"replay {i}"
+
+
+def test_graph_evict_compact_fused(dev):
+    """The fused evict + compact call (clear + one grid-barrier launch)
+    captured with the gather and replayed; each replay equals the eager
+    two-call pipeline (select_evict, compact) bit for bit."""
+    from kessie_amd import ops
+
+    num_pages, s, w = 20000, 16, 1000
+    pool = paged_pool(num_pages, 16, 2, 64, torch.bfloat16, dev, seed=15)
+    tables = randperm(num_pages, dev, 16)[: s * w].view(s, w).contiguous()
+    lens = torch.randint(0, w + 1, (s,), generator=torch.Generator(device=dev).manual_seed(17), device=dev,
+                         dtype=torch.int32)
+    scores = torch.empty(num_pages, device=dev)
+    valid = torch.ones(num_pages, dtype=torch.int8, device=dev)
+    bufs = dict(evict_list=torch.empty(num_pages, dtype=torch.int32, device=dev),
+                evict_count=torch.zeros(1, dtype=torch.int32, device=dev), new_tables=torch.empty_like(tables),
+                new_lens=torch.empty(s, dtype=torch.int32, device=dev),
+                gather_idx=torch.empty(s * w, dtype=torch.int32, device=dev),
+                gather_count=torch.zeros(1, dtype=torch.int32, device=dev))
+    out = torch.empty((s * w,) + tuple(pool.shape[1:]), dtype=pool.dtype, device=dev)
+
+    def pipeline():
+        ops.page_evict_compact(scores, valid, tables, lens, -1, 0.3, **bufs)
+        ops.page_gather(pool, bufs["gather_idx"], bufs["gather_count"], out=out, n=s * w)
+
+    scores.copy_(torch.rand(num_pages, generator=torch.Generator(device=dev).manual_seed(18), device=dev))
+    g = _capture(pipeline)
+    for i in range(3):
+        scores.copy_(torch.rand(num_pages, generator=torch.Generator(device=dev).manual_seed(50 + i), device=dev))
+        if i == 1:
+            scores[::2] = 0.25  # heavy ties at the threshold
+        valid.fill_(1)
+        valid[::7] = 0
+        v0 = valid.clone()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        c, n = int(bufs["evict_count"].item()), int(bufs["gather_count"].item())
+        got = (bufs["evict_list"][:c].clone(), valid.clone(), bufs["new_tables"].clone(), bufs["new_lens"].clone(),
+               bufs["gather_idx"][:n].clone(), out[:n].clone())
+        valid.copy_(v0)
+        lst, cnt = ops.page_select_evict(scores, valid, -1, 0.3)
+        nt, nl, gi, gc = ops.page_compact(tables, lens, valid)
+        ref_out = ops.page_gather(pool, gi, gc, n=s * w)
+        torch.cuda.synchronize()
+        assert c == int(cnt.item()) and n == int(gc.item()), f"replay {i}"
+        want = (lst[:c], valid, nt, nl, gi[:n], ref_out[:n])
+        for a, b in zip(got, want):
+            assert torch.equal(a, b), f"replay {i}"
+
+
+def test_graph_survives_workspace_growth(dev):
+    """A captured decode keeps writing its split partials to the cached
+    workspace it was captured with.  A later, larger eager call replaces the
+    cached buffer; the superseded one must stay allocated, so a tensor
+    allocated afterwards is never overwritten by a replay."""
+    from kessie_amd import ops
+
+    ctx = 3000
+    q, pool, table, lens = decode_case(2, 32, 8, 128, ctx, 16, torch.bfloat16, dev, seed=21)
+    out = torch.empty_like(q)
+    g = _capture(lambda: ops.fog_decode(q, pool, table, lens, max_ctx=ctx, out=out))
+    old = ops.workspace(1, dev, "attn")  # the buffer the graph was captured with
+    # A larger call (here: a request one byte past the cached size, as a split
+    # prefill's larger workspace would make) replaces the cached buffer.
+    ops.workspace(old.numel() + 1, dev, "attn")
+    torch.cuda.synchronize()
+    assert ops.workspace(1, dev, "attn").data_ptr() != old.data_ptr(), "the workspace did not grow"
+    n_old = old.numel()
+    del old
+    sentinels = [torch.full((n_old,), 0x5A, dtype=torch.uint8, device=dev) for _ in range(4)]
+    torch.cuda.synchronize()
+    for i in range(2):
+        q.copy_(randn(q.shape, torch.bfloat16, dev, 400 + i))
+        g.replay()
+        torch.cuda.synchronize()
+        for t in sentinels:
+            assert bool((t == 0x5A).all()), f"replay {i} overwrote a tensor allocated after the growth"
+        want = ops.fog_decode(q, pool, table, lens, max_ctx=ctx)
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), f"replay {i}"

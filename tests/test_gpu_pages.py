@@ -153,14 +153,11 @@ def test_score_evict_full_config(dev):
     assert np.array_equal(_np(nt), rt) and np.array_equal(_np(nl), rl)
     c = int(gc.item())
     assert c == 49152 and np.array_equal(_np(gi[:c]), rg)
-    # Gathered bytes: checksum per page plus a full compare of 512 sampled pages.
-    sample = np.random.default_rng(0).choice(c, 512, replace=False)
-    got = out[torch.from_numpy(sample).to(dev)]
-    ref = pool[torch.from_numpy(rg[sample]).long().to(dev)]
-    assert torch.equal(got, ref)
-    sums_got = out[:c].view(c, -1).view(torch.int16).to(torch.int64).sum(1)
-    sums_ref = pool[gi[:c].long()].view(c, -1).view(torch.int16).to(torch.int64).sum(1)
-    assert torch.equal(sums_got, sums_ref)
+    # Gathered bytes: every gathered page compared with its source page, on the
+    # device, 4,096 pages (256 MiB) at a time.
+    ref_idx = torch.from_numpy(rg).to(dev).long()
+    for i in range(0, c, 4096):
+        assert torch.equal(out[i:i + 4096], pool[ref_idx[i:i + 4096]]), f"pages {i}.."
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
@@ -228,3 +225,118 @@ def test_legacy_page_insert_fp16(dev):
     torch.cuda.synchronize()
     assert np.array_equal(pool.cpu().numpy(), rp)
     assert np.array_equal(_np(valid), rv) and np.array_equal(_np(posn), rpos)
+
+
+@pytest.mark.parametrize("n,s,w,frac,k,distinct", [
+    (65536, 64, 1024, 0.25, -1, 0),       # the full config's shape
+    (1000, 3, 700, 0.25, -1, 0),
+    (5000, 8, 600, 0.5, -1, 40),          # many tied scores at the threshold
+    (65536, 2, 30000, 0.25, -1, 1),       # one score for every page (candidates overflow LDS)
+    (20000, 100, 150, 0.0, 17, 0),        # explicit k
+    (3000, 5, 500, 0.0, -1, 0),           # nothing evicted
+    (70000, 300, 200, 0.999, -1, 0),      # more tiles than workgroups' first pass; nearly all evicted
+])
+def test_evict_compact_matches_oracle(dev, n, s, w, frac, k, distinct):
+    """The fused call equals select_evict followed by compact (the oracle),
+    bit for bit: evict list and count, valid flags, compacted tables, lengths,
+    gather indices and count."""
+    from kessie_amd import ops
+
+    g = torch.Generator().manual_seed(n + s)
+    if distinct:
+        values = torch.rand(distinct, generator=g)
+        scores = values[torch.randint(0, distinct, (n,), generator=g)]
+    else:
+        scores = torch.rand(n, generator=g)
+        scores[5] = -0.0
+        scores[6] = 0.0
+        scores[7] = -2.0
+    valid = (torch.rand(n, generator=g) < 0.9).to(torch.int8)
+    tables = torch.randint(-3, n + 3, (s, w), generator=g, dtype=torch.int32)  # incl. out-of-range ids
+    lens = torch.randint(0, w + 1, (s,), generator=g, dtype=torch.int32)
+    lens[0] = w
+    rv, rlist = P.select_evict(scores.numpy(), valid.numpy(), k, frac)
+    rt, rl, rg = P.compact(tables.numpy(), lens.numpy(), rv)
+    dv = valid.to(dev)
+    lst, cnt, nt, nl, gi, gc = ops.page_evict_compact(scores.to(dev), dv, tables.to(dev), lens.to(dev), k, frac)
+    torch.cuda.synchronize()
+    c = int(cnt.item())
+    assert c == len(rlist) and np.array_equal(_np(lst[:c]), rlist)
+    assert np.array_equal(_np(dv), rv)
+    assert np.array_equal(_np(nt), rt) and np.array_equal(_np(nl), rl)
+    m = int(gc.item())
+    assert m == len(rg) and np.array_equal(_np(gi[:m]), rg)
+
+
+def test_evict_compact_rejects_too_many_rows(dev):
+    from kessie_amd import _lib, ops
+
+    n = 100
+    tables = torch.zeros(8193, 1, dtype=torch.int32, device=dev)
+    lens = torch.ones(8193, dtype=torch.int32, device=dev)
+    with pytest.raises(_lib.KeSSieError) as e:
+        ops.page_evict_compact(torch.rand(n, device=dev), torch.ones(n, dtype=torch.int8, device=dev), tables, lens)
+    assert e.value.status == _lib.ERR_UNSUPPORTED
+
+
+def test_evict_compact_full_config_then_gather(dev):
+    """Config: 65,536-page pool, 64 x 1,024 tables, evict the lowest 25%, fused
+    evict + compact, gather every survivor; every gathered page compared."""
+    from kessie_amd import ops
+
+    num_pages, s, w = 65536, 64, 1024
+    pool = paged_pool(num_pages, 16, 8, 128, torch.bfloat16, dev, 0)
+    tables = randperm(num_pages, dev, 1).view(s, w).contiguous()
+    scores = torch.rand(num_pages, generator=gen(dev, 2), device=dev)
+    valid = torch.ones(num_pages, dtype=torch.int8, device=dev)
+    lens = torch.full((s,), w, dtype=torch.int32, device=dev)
+    lst, cnt, nt, nl, gi, gc = ops.page_evict_compact(scores, valid, tables, lens, -1, 0.25)
+    out = ops.page_gather(pool, gi, gc, n=s * w)
+    torch.cuda.synchronize()
+    rv, rlist = P.select_evict(_np(scores), np.ones(num_pages, np.int8), -1, 0.25)
+    rt, rl, rg = P.compact(_np(tables), _np(lens), rv)
+    assert int(cnt.item()) == 16384 and np.array_equal(_np(lst[:16384]), rlist)
+    assert np.array_equal(_np(valid), rv)
+    assert np.array_equal(_np(nt), rt) and np.array_equal(_np(nl), rl)
+    c = int(gc.item())
+    assert c == 49152 and np.array_equal(_np(gi[:c]), rg)
+    ref_idx = torch.from_numpy(rg).to(dev).long()
+    for i in range(0, c, 4096):
+        assert torch.equal(out[i:i + 4096], pool[ref_idx[i:i + 4096]]), f"pages {i}.."
+
+
+def test_select_evict_needs_an_initialised_workspace(dev):
+    """Through the C ABI with a caller-owned workspace: a workspace that was
+    never prepared by kessie_page_workspace_init is refused (count -2, flags
+    untouched); once prepared, repeated calls on it (each restoring the
+    scratch for the next) all match the oracle."""
+    from kessie_amd import _lib
+
+    lib = _lib.load()
+    n = 5000
+    g = torch.Generator().manual_seed(11)
+    scores = torch.rand(n, generator=g)
+    ptr = lambda t: ctypes.c_void_p(t.data_ptr())
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    nbytes = lib.kessie_page_workspace_bytes(n)
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+    sc = scores.to(dev)
+    valid = torch.ones(n, dtype=torch.int8, device=dev)
+    lst = torch.empty(n, dtype=torch.int32, device=dev)
+    cnt = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def call():
+        _lib.check("kessie_page_select_evict", lib.kessie_page_select_evict(
+            ptr(sc), ptr(valid), n, -1, 0.25, ptr(lst), ptr(cnt), ptr(ws), nbytes, stream))
+        torch.cuda.synchronize()
+
+    call()
+    assert int(cnt.item()) == -2 and bool((valid == 1).all())
+    _lib.check("kessie_page_workspace_init", lib.kessie_page_workspace_init(ptr(ws), nbytes, stream))
+    ref_valid, ref_list = P.select_evict(scores.numpy(), np.ones(n, np.int8), -1, 0.25)
+    for _ in range(3):
+        valid.fill_(1)
+        call()
+        c = int(cnt.item())
+        assert c == len(ref_list) and np.array_equal(_np(lst[:c]), ref_list)
+        assert np.array_equal(_np(valid), ref_valid)
