@@ -277,9 +277,10 @@ class KeSSieCache:
         if target is None:
             return False
         start, end, cpu_layers = self.cpu_kv_store[target]
-        event = self._store_events[target]
-        if event is not None:
-            torch.cuda.current_stream(device).wait_event(event)
+        # Wait for every pending eviction copy, not only this chunk's: the
+        # prepend below writes the arena slots in front of the window, which
+        # are the source of the most recent eviction's copy to host memory.
+        self._wait_evictions()
         recalled = 0
         for i, L in enumerate(self._layers):
             if i >= len(cpu_layers) or cpu_layers[i][0] is None:

@@ -161,3 +161,43 @@ def test_hf_cache_sequence(dev):
     assert st["kv_cpu_chunks"] == len(model.cpu_kv_store)
     cache.full_reset()
     assert len(cache) == 0 and cache.get_seq_length() == 0
+
+
+def test_hf_recall_right_after_eviction_keeps_host_copies(dev):
+    """Evict, then at once (no synchronisation) recall an OLDER chunk: the
+    recall prepends into the arena slots in front of the window, which are the
+    source of the eviction's asynchronous copy to pinned host memory.  The
+    recall must wait for that copy; every chunk still on the host must equal
+    the reference algorithm's."""
+    from kessie_amd.hf_cache import KeSSieCache
+
+    L, H, D, W = 2, 8, 128, 1024
+    cache = KeSSieCache(window_size=W, fog_alpha=0.5, fog_start=0.5)
+    model = HFCacheModel(window_size=W, fog_alpha=0.5, fog_start=0.5)
+    seed = [500]
+
+    def step(t):
+        for li in range(L):
+            seed[0] += 1
+            k = randn((1, H, t, D), torch.bfloat16, dev, seed[0])
+            v = randn((1, H, t, D), torch.bfloat16, dev, seed[0] + 1000)
+            cache.update(k, v, li)
+            model.update(k, v, li)
+
+    step(2100)
+    cache.evict_if_needed()
+    model.evict_if_needed()
+    step(1100)
+    cache.evict_if_needed()  # the newest chunk's device-to-host copy is now in flight
+    model.evict_if_needed()
+    assert len(cache.cpu_kv_store) == len(model.cpu_kv_store) == 2
+    pos = cache.cpu_kv_store[0][0] + 1
+    assert cache.recall_from_cpu(pos, dev) and model.recall_from_cpu(pos)
+    torch.cuda.synchronize()
+    assert len(cache.cpu_kv_store) == len(model.cpu_kv_store) == 1
+    for (s0, e0, lay0), (s1, e1, lay1) in zip(cache.cpu_kv_store, model.cpu_kv_store):
+        assert (s0, e0) == (s1, e1)
+        for (kc, vc), (km, vm) in zip(lay0, lay1):
+            assert torch.equal(kc, km.cpu()) and torch.equal(vc, vm.cpu())
+    for li in range(L):
+        _check_layer(cache, model, li)
