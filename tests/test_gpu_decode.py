@@ -135,9 +135,9 @@ def test_decode_generic_path_matches_mfma_path(dev, monkeypatch):
     assert (a.float() - b.float()).abs().max().item() < 2e-2
 
 
-def test_decode_llama8b_128k_sampled(dev):
+def test_decode_llama8b_128k_all_sequences(dev):
     """Config: bf16, B=16, 32q/8kv, D=128, 131,072-token context in 16-token pages,
-    V-fog defaults.  Full-size run; two sequences checked against the oracle."""
+    V-fog defaults.  Full-size run; every sequence checked against the oracle."""
     from kessie_amd import ops
 
     b, ctx = 16, 131072
@@ -146,7 +146,7 @@ def test_decode_llama8b_128k_sampled(dev):
     out = ops.fog_decode(q, pool, table, lens, ctx, fog_vscale=vs)
     torch.cuda.synchronize()
     assert torch.isfinite(out.float()).all()
-    for s in (0, 11):
+    for s in range(b):
         # Gather the sequence's pages on the device first (8192 pages), then run
         # the blockwise oracle on the CPU copy of just those pages.
         sub_pool = pool[table[s].long()].cpu()

@@ -116,10 +116,12 @@ def test_prefill_mfma_matches_generic(dev, monkeypatch):
     assert (a.float() - b.float()).abs().max().item() < 2e-2
 
 
-def test_prefill_1m_context_sampled(dev):
+def test_prefill_1m_context_every_query_tile(dev):
     """Config: bf16, 2,048-query chunk appended to a 1,048,576-token paged KV
     (65,664 pages), 32 q / 8 kv heads, D=128, causal, V-fog over the full
-    context.  Full-size GPU run; 6 rows checked against the blockwise oracle."""
+    context.  Full-size GPU run; the first and the last query position of each
+    of the kernel's 32 query tiles (64 positions x the 4 heads of a kv head per
+    tile), all 32 heads, checked against the blockwise oracle."""
     from kessie_amd import ops
 
     c, L = 2048, 1 << 20
@@ -133,7 +135,7 @@ def test_prefill_1m_context_sampled(dev):
     out = ops.fog_prefill(q, pool, table, lens, ctx, fog_vscale=fog)
     torch.cuda.synchronize()
     assert torch.isfinite(out.float()).all()
-    rows = torch.tensor([0, 1, 777, 1500, 2046, 2047])
+    rows = torch.tensor(sorted([64 * t for t in range(32)] + [64 * t + 63 for t in range(32)] + [777, 1500]))
     ref = paged_prefill_blockwise(q.cpu(), pool, table.cpu(), lens.cpu(), rows, fog.cpu(), block_pages=4096)
     _check(out[:, rows], ref, torch.bfloat16)
 
