@@ -139,6 +139,30 @@ int kessie_fog_decode_paged(
     int page_size, int max_ctx, int window, float sm_scale, int dtype,
     void* workspace, size_t workspace_bytes, void* stream);
 
+/* Size of the static device scratch of kessie_fog_decode_paged_noalloc. */
+#define KESSIE_DECODE_NOALLOC_SCRATCH_BYTES (16u << 20)
+
+/* kessie_fog_decode_paged without a workspace argument, allocating nothing:
+ * the split partials go to a static device array of
+ * KESSIE_DECODE_NOALLOC_SCRATCH_BYTES (16 MiB) per GPU, held until the
+ * process ends.  Same arguments (minus workspace / workspace_bytes),
+ * semantics and results, bit for bit, as kessie_fog_decode_paged.  Returns
+ * KESSIE_ERR_WORKSPACE, launching nothing, when the partials of these sizes
+ * exceed the array (B * Hq * S * (head_dim + 2) * 4 bytes plus alignment, S =
+ * kessie_fog_decode_num_splits(...)).  Calls that overlap on one GPU share
+ * the array and race: serialise them (one stream, or events).  No
+ * counterpart in the reference: it exists for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, hosts
+ * that forbid allocation). */
+int kessie_fog_decode_paged_noalloc(
+    const void* q, const void* kv_pool, int num_pages, int64_t page_stride,
+    int64_t tok_stride, int64_t kv_stride, int64_t head_stride,
+    const int32_t* page_table, int64_t table_stride, const int32_t* ctx_lens,
+    const float* fog_vscale, int64_t fog_vscale_bstride, const float* fog_bias,
+    int64_t fog_bias_bstride, void* out, int batch, int num_q_heads,
+    int num_kv_heads, int head_dim, int page_size, int max_ctx, int window,
+    float sm_scale, int dtype, void* stream);
+
 /* Number of key splits S the decode uses for these sizes (host call). */
 int kessie_fog_decode_num_splits(int batch, int num_kv_heads, int max_ctx,
                                  int page_size);

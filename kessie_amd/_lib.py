@@ -46,6 +46,10 @@ SIGNATURES = {
     "kessie_fog_decode_paged": (_I, [
         _P, _P, _I, _I64, _I64, _I64, _I64, _P, _I64, _P, _P, _I64, _P, _I64,
         _P, _I, _I, _I, _I, _I, _I, _I, _F, _I, _P, _SZ, _P]),
+    # as kessie_fog_decode_paged without ws, ws_bytes
+    "kessie_fog_decode_paged_noalloc": (_I, [
+        _P, _P, _I, _I64, _I64, _I64, _I64, _P, _I64, _P, _P, _I64, _P, _I64,
+        _P, _I, _I, _I, _I, _I, _I, _I, _F, _I, _P]),
     "kessie_fog_decode_num_splits": (_I, [_I, _I, _I, _I]),
     # as kessie_fog_decode_paged without `out`
     "kessie_fog_decode_partials": (_I, [

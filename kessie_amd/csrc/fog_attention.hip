@@ -26,6 +26,7 @@
 #include <cstdlib>
 
 #include <atomic>
+#include <mutex>
 
 #include "attn_common.h"
 
@@ -860,6 +861,74 @@ extern "C" int kessie_fog_decode_partials(const void* q, const void* kv_pool, in
                                     fog_bias_bstride, nullptr, batch, num_q_heads, num_kv_heads, head_dim,
                                     page_size, max_ctx, window, sm_scale, dtype, workspace, workspace_bytes, stream,
                                     true);
+}
+
+// ---------------------------------------------------------------------------
+// Decode that allocates nothing: the split partials go to a file-scope device
+// array instead of a caller workspace (for callers that cannot allocate:
+// code under graph capture, tight serving loops).  Each GPU holds its own copy
+// of the array, at its own address, until the process ends; host code uses
+// that address (from hipGetSymbolAddress, once per device), never the array's
+// name.  Calls that overlap on one GPU share the array and race.  The decode
+// kernels write every partial of every (row, split) on each call, so nothing
+// needs clearing between calls.
+// ---------------------------------------------------------------------------
+namespace {
+static __device__ __align__(256) unsigned char scratch[KESSIE_DECODE_NOALLOC_SCRATCH_BYTES];
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[64];  // device address of `scratch`, per device ordinal
+
+// Address of this device's copy of `scratch` (looked up on the first call on
+// the device, with that device current), or nullptr with the error recorded.
+void* device_scratch() {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    kessie::set_error(KESSIE_ERR_HIP, "fog decode (no-alloc): hipGetDevice: %s", hipGetErrorString(e));
+    return nullptr;
+  }
+  if (dev < 0 || dev >= 64) {
+    kessie::set_error(KESSIE_ERR_UNSUPPORTED, "fog decode (no-alloc): device ordinal %d", dev);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+      kessie::set_error(KESSIE_ERR_HIP, "fog decode (no-alloc): hipGetSymbolAddress: %s", hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  return g_scratch_ptr[dev];
+}
+}  // namespace
+
+extern "C" int kessie_fog_decode_paged_noalloc(const void* q, const void* kv_pool, int num_pages,
+                                               int64_t page_stride, int64_t tok_stride, int64_t kv_stride,
+                                               int64_t head_stride, const int32_t* page_table, int64_t table_stride,
+                                               const int32_t* ctx_lens, const float* fog_vscale,
+                                               int64_t fog_vscale_bstride, const float* fog_bias,
+                                               int64_t fog_bias_bstride, void* out, int batch, int num_q_heads,
+                                               int num_kv_heads, int head_dim, int page_size, int max_ctx,
+                                               int window, float sm_scale, int dtype, void* stream) {
+  using namespace kessie;
+  clear_error();
+  if (batch > 0 && num_q_heads > 0 && num_kv_heads > 0 && head_dim > 0) {
+    const int S = attn::decode_splits(batch, num_kv_heads, max_ctx, page_size);
+    const size_t need = S > 1 ? attn::partial_bytes((int64_t)batch * num_q_heads, S, head_dim) : 0;
+    KESSIE_REQUIRE(need <= (size_t)KESSIE_DECODE_NOALLOC_SCRATCH_BYTES, KESSIE_ERR_WORKSPACE,
+                   "fog decode (no-alloc): %zu bytes of split partials needed for B=%d Hq=%d ctx=%d, more than "
+                   "the %zu-byte static scratch; call kessie_fog_decode_paged with a workspace",
+                   need, batch, num_q_heads, max_ctx, (size_t)KESSIE_DECODE_NOALLOC_SCRATCH_BYTES);
+  }
+  void* ws = device_scratch();
+  if (ws == nullptr) return last_status();
+  return attn::decode_entry(q, kv_pool, num_pages, page_stride, tok_stride, kv_stride, head_stride, page_table,
+                            table_stride, ctx_lens, fog_vscale, fog_vscale_bstride, fog_bias, fog_bias_bstride, out,
+                            batch, num_q_heads, num_kv_heads, head_dim, page_size, max_ctx, window, sm_scale, dtype,
+                            ws, KESSIE_DECODE_NOALLOC_SCRATCH_BYTES, stream, false);
 }
 
 extern "C" int kessie_fog_decode_num_splits(int batch, int num_kv_heads, int max_ctx, int page_size) {
