@@ -11,7 +11,8 @@
 // rescale, so a fully masked stretch contributes nothing.
 //
 // Kernels:
-//   decode_mfma   bf16/f16, head_dim 128, 16-token pages.  One workgroup =
+//   decode_mfma   bf16/f16 (fp32: decode_mfma_f32 on v_mfma_f32_16x16x4_f32,
+//                 same decomposition), head_dim 128, 16-token pages.  One workgroup =
 //                 one (sequence, split) x 2 kv heads, one wave per kv head; a
 //                 wave streams its kv head's 256-byte K and V rows of every
 //                 page in its split with 16-byte loads (register prefetch of
@@ -19,8 +20,9 @@
 //                 dtype, accumulation in fp32), V transposed through LDS.
 //   attn_generic  any dtype / head_dim <= 256 / page size / GQA ratio: K and
 //                 V tiles staged in LDS as fp32, one workgroup per
-//                 (row tile, kv head, sequence, split).  Serves fp32 decode,
-//                 chunked prefill and the dense launchers.
+//                 (row tile, kv head, sequence, split).  Serves the shapes the
+//                 MFMA kernels do not take (fp32 prefill, other head_dims,
+//                 page sizes and GQA ratios).
 //   combine       merges the per-split (m, l, o) partials of either kernel.
 #include <cmath>
 #include <cstdlib>
@@ -583,6 +585,200 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) 
 }
 
 // ---------------------------------------------------------------------------
+// fp32 decode on MFMA (head_dim 128, 16-token pages): the bf16 kernel's
+// decomposition with v_mfma_f32_16x16x4_f32 and the probabilities kept in
+// fp32 (no rounding of p, so fp32 inputs meet a 1e-5 tolerance).
+//   * K: lane (grp, row) loads token `row`'s d = 32*grp .. 32*grp+31 (128
+//     contiguous bytes, eight 16-byte loads); MFMA kb (0..31) takes d =
+//     32*grp + kb of that token as its A element, and the query element of the
+//     same d as B (held in 32 registers), so the 32 MFMAs cover all 128 d;
+//   * scores land in the same layout as the bf16 kernel's (lane: head `row`,
+//     tokens 4*grp + i), so the softmax is identical;
+//   * PV k-step ks takes tokens 4*grp' + ks over the four k lanes: each lane's
+//     own p[ks] is its B element with no exchange, and V (staged in LDS as
+//     token rows of 132 floats -- two token rows read by one half-wave fall on
+//     different banks) supplies A = V[4*grp + ks][16*blk + row].
+// ---------------------------------------------------------------------------
+constexpr int kVRowF = 132;  // LDS row stride of the fp32 V tile (floats)
+
+template <int G, int PREF, int W, int FOG>
+__global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_mfma_f32_kernel(
+    Params p) {
+  __shared__ __align__(16) float vtile_all[W][16 * kVRowF];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int g = blockIdx.z * W + wave;
+  if (g >= p.Hkv) return;  // no workgroup barriers below
+  float* vtile = vtile_all[wave];
+  const int b = blockIdx.y;
+  const int split = blockIdx.x;
+  const int S = p.num_splits;
+  const int row = lane & 15;
+  const int grp = lane >> 4;
+
+  const int ctx = seq_ctx(p, b);
+  const int lo = p.window > 0 ? max(0, ctx - p.window) : 0;
+  const int pg_lo = lo >> 4;
+  const int pg_hi = (ctx + 15) >> 4;
+  const int per = (pg_hi - pg_lo + S - 1) / S;
+  const int p0 = pg_lo + split * per;
+  const int p1 = min(pg_hi, p0 + per);
+
+  const float* kbase = static_cast<const float*>(p.k) + (int64_t)g * p.head_stride;
+  const float* vbase = static_cast<const float*>(p.v) + (int64_t)g * p.head_stride;
+  const int32_t* table = p.page_table + (int64_t)b * p.table_stride;
+  const int64_t ts = p.tok_stride;
+  const int64_t koff = (int64_t)row * ts + 32 * grp;
+  const int64_t voff = (int64_t)(4 * grp) * ts + 8 * row;  // + i*ts, +4
+
+  // B operand of QK^T: query element d = 32*grp + kb of head `row` (zero past G).
+  f32x4 qreg[8];
+  {
+    const float* qrow = static_cast<const float*>(p.q) + (int64_t)b * p.q_bs + (int64_t)(g * G + row) * p.q_hs;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      qreg[j] = row < G ? *reinterpret_cast<const f32x4*>(qrow + 32 * grp + 4 * j) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+
+  f32x4 oacc[8];  // O^T[d = 16*blk + 4*grp + i][head = row]
+#pragma unroll
+  for (int blk = 0; blk < 8; ++blk) oacc[blk] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  float m_run = kNegInf, l_run = 0.0f;
+
+  f32x4 kreg[PREF][8], vreg[PREF][8];
+  int pid_s[PREF];
+  float fb_cur = 0.0f, fv_cur = 0.0f;
+  const float* fog_b = (FOG & kFogBias) ? p.bias + (int64_t)b * p.bias_bs : nullptr;
+  const float* fog_v = (FOG & kFogVs) ? p.vscale + (int64_t)b * p.vs_bs : nullptr;
+  auto load_fog = [&](int lp) {
+    const int tl = 16 * lp + lane;
+    const bool in = lane < 16 && tl >= lo && tl < ctx;
+    if (FOG & kFogBias) fb_cur = in ? fog_b[tl] : 0.0f;
+    if (FOG & kFogVs) fv_cur = in ? fog_v[tl] : 0.0f;
+  };
+  auto issue = [&](int st, int lp) {
+    const int pid = table[lp];
+    pid_s[st] = pid;
+    if (pid >= 0 && pid < p.num_pages) {
+      const float* kp = kbase + (int64_t)pid * p.page_stride;
+      const float* vp = vbase + (int64_t)pid * p.page_stride;
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        kreg[st][j] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(kp + koff + 4 * j));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        vreg[st][2 * i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(vp + voff + i * ts));
+        vreg[st][2 * i + 1] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(vp + voff + i * ts + 4));
+      }
+    }
+  };
+
+#pragma unroll
+  for (int st = 0; st < PREF; ++st)
+    if (p0 + st < p1) issue(st, p0 + st);
+  if (FOG && p0 < p1) load_fog(p0);
+
+  for (int base = p0; base < p1; base += PREF) {
+#pragma unroll
+    for (int st = 0; st < PREF; ++st) {
+      const int lp = base + st;
+      if (lp >= p1) break;
+      const int pid = pid_s[st];
+      if (pid < 0 || pid >= p.num_pages) {
+        if (FOG && lp + 1 < p1) load_fog(lp + 1);
+        if (lp + PREF < p1) issue(st, lp + PREF);
+        continue;
+      }
+      const int t_page = lp << 4;
+      const bool full = t_page >= lo && t_page + 16 <= ctx;
+      f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kreg[st][j][e], qreg[j][e], acc, 0, 0, 0);
+      float sc[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = t_page + 4 * grp + i;
+        const bool ok = full || (t >= lo && t < ctx);
+        float s = acc[i] * p.sm_scale;
+        if (FOG & kFogBias) s += __shfl(fb_cur, 4 * grp + i);
+        sc[i] = ok ? s : kNegInf;
+      }
+      float mloc = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+      mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
+      mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+      const float mnew = fmaxf(m_run, mloc);
+      const float alpha = (m_run == kNegInf) ? 0.0f : __expf(m_run - mnew);
+      float pr[4];
+      float psum = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        pr[i] = (sc[i] == kNegInf) ? 0.0f : __expf(sc[i] - mnew);
+        psum += pr[i];
+      }
+      psum += __shfl_xor(psum, 16);
+      psum += __shfl_xor(psum, 32);
+      l_run = l_run * alpha + psum;
+      m_run = mnew;
+      if (FOG & kFogVs) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pr[i] *= __shfl(fv_cur, 4 * grp + i);
+      }
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
+#pragma unroll
+        for (int blk = 0; blk < 8; ++blk) oacc[blk] *= alpha;
+      }
+      if (!full) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int t = t_page + 4 * grp + i;
+          if (!(t >= lo && t < ctx)) {
+            vreg[st][2 * i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            vreg[st][2 * i + 1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+          }
+        }
+      }
+      wave_lds_sync();  // the previous page's reads are done
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        *reinterpret_cast<f32x4*>(vtile + (4 * grp + i) * kVRowF + 8 * row) = vreg[st][2 * i];
+        *reinterpret_cast<f32x4*>(vtile + (4 * grp + i) * kVRowF + 8 * row + 4) = vreg[st][2 * i + 1];
+      }
+      wave_lds_sync();
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int blk = 0; blk < 8; ++blk)
+          oacc[blk] = __builtin_amdgcn_mfma_f32_16x16x4f32(vtile[(4 * grp + ks) * kVRowF + 16 * blk + row], pr[ks],
+                                                           oacc[blk], 0, 0, 0);
+      if (FOG && lp + 1 < p1) load_fog(lp + 1);
+      if (lp + PREF < p1) issue(st, lp + PREF);
+    }
+  }
+
+  // Lane (grp, row) holds head `row`, d = 16*blk + 4*grp + i.
+  if (row >= G) return;
+  const int head = g * G + row;
+  if (p.direct_out) {
+    const float il = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+    float* dst = static_cast<float*>(p.out) + (int64_t)b * p.o_bs + (int64_t)head * p.o_hs + 4 * grp;
+#pragma unroll
+    for (int blk = 0; blk < 8; ++blk) *reinterpret_cast<f32x4*>(dst + 16 * blk) = oacc[blk] * il;
+  } else {
+    const int64_t r = row_id(p, b, 0, head);
+    float* dst = p.ws_o + (r * S + split) * 128 + 4 * grp;
+#pragma unroll
+    for (int blk = 0; blk < 8; ++blk) *reinterpret_cast<f32x4*>(dst + 16 * blk) = oacc[blk];
+    if (grp == 0) {
+      p.ws_m[r * S + split] = m_run;
+      p.ws_l[r * S + split] = l_run;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
 
@@ -694,6 +890,45 @@ int launch_decode_mfma(Params& p, hipStream_t stream) {
   return KESSIE_OK;
 }
 
+template <int G>
+int launch_decode_mfma_f32(Params& p, hipStream_t stream) {
+  dim3 grid(p.num_splits, p.B, div_up(p.Hkv, kDecWaves));
+  const int fog = (p.bias ? kFogBias : 0) | (p.vscale ? kFogVs : 0);
+  const dim3 block(kDecWaves * 64);
+  switch (fog) {
+    case 0: hipLaunchKernelGGL((decode_mfma_f32_kernel<G, kDecPref, kDecWaves, 0>), grid, block, 0, stream, p); break;
+    case kFogBias:
+      hipLaunchKernelGGL((decode_mfma_f32_kernel<G, kDecPref, kDecWaves, kFogBias>), grid, block, 0, stream, p);
+      break;
+    case kFogVs:
+      hipLaunchKernelGGL((decode_mfma_f32_kernel<G, kDecPref, kDecWaves, kFogVs>), grid, block, 0, stream, p);
+      break;
+    default:
+      hipLaunchKernelGGL((decode_mfma_f32_kernel<G, kDecPref, kDecWaves, kFogBias | kFogVs>), grid, block, 0, stream,
+                         p);
+  }
+  if (check_launch("fog decode (mfma fp32)") != KESSIE_OK) return KESSIE_ERR_HIP;
+  if (!p.direct_out && p.launch_combine) {
+    const int64_t rows = (int64_t)p.B * p.Hq;
+    hipLaunchKernelGGL(combine_kernel<float>, dim3((unsigned)rows, combine_dsplit(rows, p.D)), dim3(kCombineThreads),
+                       0, stream, p);
+    return check_launch("fog decode (combine)");
+  }
+  return KESSIE_OK;
+}
+
+int run_decode_mfma_f32(Params& p, hipStream_t s) {
+  switch (p.G) {
+    case 1: return launch_decode_mfma_f32<1>(p, s);
+    case 2: return launch_decode_mfma_f32<2>(p, s);
+    case 4: return launch_decode_mfma_f32<4>(p, s);
+    case 8: return launch_decode_mfma_f32<8>(p, s);
+    case 16: return launch_decode_mfma_f32<16>(p, s);
+  }
+  set_error(KESSIE_ERR_UNSUPPORTED, "fog decode: GQA ratio %d", p.G);
+  return KESSIE_ERR_UNSUPPORTED;
+}
+
 int run_generic(int dtype, Params& p, hipStream_t s) {
   switch (dtype) {
     case KESSIE_DTYPE_F32: return launch_generic<float>(p, s);
@@ -706,12 +941,14 @@ int run_generic(int dtype, Params& p, hipStream_t s) {
 
 bool decode_mfma_ok(const Params& p, int dtype) {
   if (env_int("KESSIE_FORCE_GENERIC", 0)) return false;
-  if (dtype != KESSIE_DTYPE_BF16 && dtype != KESSIE_DTYPE_F16) return false;
+  if (dtype != KESSIE_DTYPE_BF16 && dtype != KESSIE_DTYPE_F16 && dtype != KESSIE_DTYPE_F32) return false;
   if (p.D != 128 || p.page_size != 16 || p.page_table == nullptr) return false;
   if (!(p.G == 1 || p.G == 2 || p.G == 4 || p.G == 8 || p.G == 16)) return false;
   if (!aligned16(p.q) || !aligned16(p.k) || !aligned16(p.v) || !aligned16(p.out)) return false;
-  if (p.page_stride % 8 || p.tok_stride % 8 || p.head_stride % 8 || p.q_bs % 8 || p.q_hs % 8 || p.o_bs % 8 ||
-      p.o_hs % 8)
+  // 16-byte rows: 8 elements of bf16/fp16, 4 of fp32.
+  const int64_t vec = dtype == KESSIE_DTYPE_F32 ? 4 : 8;
+  if (p.page_stride % vec || p.tok_stride % vec || p.head_stride % vec || p.q_bs % vec || p.q_hs % vec ||
+      p.o_bs % vec || p.o_hs % vec)
     return false;
   return true;
 }
@@ -826,6 +1063,7 @@ static int decode_entry(const void* q, const void* kv_pool, int num_pages, int64
   }
   hipStream_t s = as_stream(stream);
   if (decode_mfma_ok(p, dtype)) {
+    if (dtype == KESSIE_DTYPE_F32) return run_decode_mfma_f32(p, s);
     return dtype == KESSIE_DTYPE_BF16 ? run_decode_mfma<bf16_t>(p, s) : run_decode_mfma<f16_t>(p, s);
   }
   return run_generic(dtype, p, s);

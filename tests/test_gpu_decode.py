@@ -153,3 +153,29 @@ def test_decode_llama8b_128k_all_sequences(dev):
         sub_table = torch.arange(table.shape[1], dtype=torch.int32).view(1, -1)
         ref = paged_decode_blockwise(q[s:s + 1].cpu(), sub_pool, sub_table, lens[s:s + 1].cpu(), vs.cpu())
         _check(out[s:s + 1], ref, torch.bfloat16)
+
+
+@pytest.mark.parametrize("hq,hkv,fog,window,ctx_lens", [
+    (32, 8, "vscale", 0, None),
+    (32, 8, "both", 100, [4096, 1000, 17]),
+    (16, 16, "bias", 0, [333, 0, 4096]),
+    (64, 4, "none", 5000, None),
+])
+def test_decode_fp32_mfma_matches_oracle_and_generic(dev, monkeypatch, hq, hkv, fog, window, ctx_lens):
+    """fp32 decode on the MFMA kernel (v_mfma_f32_16x16x4_f32, probabilities in
+    fp32): within the fp32 tolerance of the oracle and of the VALU kernel."""
+    from kessie_amd import ops
+
+    b = 3 if ctx_lens else 2
+    ctx = 4096
+    q, pool, table, lens = decode_case(b, hq, hkv, 128, ctx, 16, torch.float32, dev, seed=71, ctx_lens=ctx_lens)
+    vs = build_fog_weights(ctx).to(dev) if fog in ("vscale", "both") else None
+    bias = fog_bias(ctx, 0.5, 0.5, [3, 900], 0.1, dtype=torch.float32, device=dev) if fog in ("bias", "both") else None
+    a = ops.fog_decode(q, pool, table, lens, ctx, fog_vscale=vs, fog_bias=bias, window=window)
+    monkeypatch.setenv("KESSIE_FORCE_GENERIC", "1")
+    g = ops.fog_decode(q, pool, table, lens, ctx, fog_vscale=vs, fog_bias=bias, window=window)
+    torch.cuda.synchronize()
+    ref = paged_decode_ref(q.cpu(), pool.cpu(), table.cpu(), lens.cpu(), None if vs is None else vs.cpu(),
+                           None if bias is None else bias.cpu(), window=window)
+    _check(a, ref, torch.float32)
+    _check(g, ref, torch.float32)
