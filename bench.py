@@ -429,8 +429,8 @@ def bench_prefill(dev, reps=3, c=2048, L=1 << 20, hq=32, hkv=8, d=128, cpu=False
 def bench_dense(dev, reps=3, b=1, h=32, n=8192, d=128, cpu=False, cpu_heads=4):
     """The reference's dense launcher launch_kessie_fused_fog_attn through
     KeSSieKernels.fused_fog_attention: fp16 [B, H, N, D] with every position a
-    query, causal, V rows scaled by fog weights.  D=128 with H*N a multiple of
-    16 runs on the MFMA prefill kernel with table-less pages."""
+    query, causal, V rows scaled by fog weights.  D=128 or 64 with H*N a
+    multiple of 16 runs on the MFMA prefill kernel with table-less pages."""
     import torch
 
     from kessie_amd.kessie_hip_ctypes import KeSSieKernels
@@ -907,6 +907,7 @@ SECONDARY = {
     "fp32": bench_decode_fp32,
     "prefill": bench_prefill,
     "dense": bench_dense,
+    "dense64": lambda dev, cpu=False: bench_dense(dev, d=64, cpu=cpu),
     "fog_bias": bench_fog_bias,
     "recall": bench_recall_inject,
     "index": bench_index_query,
@@ -1013,6 +1014,9 @@ def main():
         torch.cuda.empty_cache()
         log("secondary: dense fused fog attention (reference launcher)")
         sec["dense_fused_fog_8k"] = bench_dense(dev, cpu=not args.no_cpu)
+        torch.cuda.empty_cache()
+        log("secondary: dense fused fog attention, head_dim 64 (reference launcher)")
+        sec["dense_fused_fog_8k_d64"] = bench_dense(dev, d=64, cpu=not args.no_cpu)
         torch.cuda.empty_cache()
         log("secondary: fog bias producer")
         sec["fog_bias_131k"] = bench_fog_bias(dev)

@@ -1445,13 +1445,13 @@ static void dense_fp16(const void* Q, const void* K, const void* V, void* O, con
     set_error(KESSIE_ERR_INVALID, "dense attention: null pointer or window %d", window);
     return;
   }
-  // head_dim 128: the MFMA prefill kernel, reading the dense tensors as
+  // head_dim 128 or 64: the MFMA prefill kernel, reading the dense tensors as
   // table-less 16-token pages (page b*H*N/16 + j = tokens 16j..16j+15 of every
   // head of sequence b, heads N*D apart; H*N a multiple of 16 keeps sequences
   // on whole pages, and the kernel reads no token past N).  One key split:
   // these launchers take no workspace.
   const int64_t dense_pages = (int64_t)B * H * N / 16;
-  if (D == 128 && ((int64_t)H * N) % 16 == 0 && dense_pages <= INT_MAX) {
+  if (((int64_t)H * N) % 16 == 0 && dense_pages <= INT_MAX) {
     Params m = p;
     m.page_size = 16;
     m.page_stride = 16 * (int64_t)D;
@@ -1461,6 +1461,13 @@ static void dense_fp16(const void* Q, const void* K, const void* V, void* O, con
       prefill_mfma(m, KESSIE_DTYPE_F16, as_stream(stream));  // records any launch error
       return;
     }
+  }
+  // Testing switch: KESSIE_REQUIRE_MFMA=1 makes a shape that would fall back
+  // to the generic kernel an error instead (the tests use it to show which
+  // route ran).
+  if (env_int("KESSIE_REQUIRE_MFMA", 0)) {
+    set_error(KESSIE_ERR_UNSUPPORTED, "dense attention: B=%d H=%d N=%d D=%d runs on the generic kernel", B, H, N, D);
+    return;
   }
   launch_generic<f16_t>(p, as_stream(stream));
 }

@@ -48,11 +48,15 @@ constexpr int kPfThreads = kPfWaves * 64;
 constexpr int kPfRows = kPfWaves * 32;  // query rows (position, head) per workgroup
 constexpr int kPfKT = 64;               // keys per tile (4 pages)
 constexpr int kPfStages = 3;            // LDS ring depth
-constexpr int kKRow = 128 + 8;          // K tile row stride (elements)
 constexpr int kVRowW = kPfKT / 2 + 4;   // V^T tile row stride (32-bit words)
-constexpr int kKStage = kPfKT * kKRow;  // elements per K stage
-constexpr int kVStage = 128 * kVRowW;   // words per V^T stage
-constexpr size_t kPfLdsBytes = (size_t)kPfStages * (kKStage * 2 + kVStage * 4 + 2 * kPfKT * 4);
+// LDS geometry for head_dim D: 128, or 64 (the dense launchers only).
+template <int D>
+struct PfGeom {
+  static constexpr int kKRow = D + 8;            // K tile row stride (elements)
+  static constexpr int kKStage = kPfKT * kKRow;  // elements per K stage
+  static constexpr int kVStage = D * kVRowW;     // words per V^T stage
+  static constexpr size_t kLdsBytes = (size_t)kPfStages * (kKStage * 2 + kVStage * 4 + 2 * kPfKT * 4);
+};
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
@@ -115,9 +119,15 @@ __device__ __forceinline__ float max3(float a, float b, float c) {
 
 __device__ __forceinline__ bool page_ok(int pid, int num_pages) { return pid >= 0 && pid < num_pages; }
 
-template <typename T, int G, bool kBias, bool kVs, bool kSplit, int kMode>
+template <typename T, int G, bool kBias, bool kVs, bool kSplit, int kMode, int kD>
 __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
+  static_assert(kD == 128 || kD == 64, "head_dim 128, or 64 on table-less pages");
   constexpr bool kDense = kMode == 1;
+  constexpr int kKRow = PfGeom<kD>::kKRow;
+  constexpr int kKStage = PfGeom<kD>::kKStage;
+  constexpr int kVStage = PfGeom<kD>::kVStage;
+  constexpr int kDS = kD / 16;  // QK d-steps (B operand registers)
+  constexpr int kDB = kD / 32;  // PV d-blocks (O accumulators)
   typedef typename Mma32<T>::v8 v8;
   typedef typename Mma32<T>::v4 v4;
   constexpr int kPos = kPfRows / G;  // query positions per workgroup
@@ -211,12 +221,12 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
   const bool row_ok = qi <= qi_last && q_pos >= 0;
 
   // B operand of S^T = K Q^T: d-step s holds d = 16s + 8*half .. +8.
-  v8 qv[8];
+  v8 qv[kDS];
   {
     const T* qr = static_cast<const T*>(p.q) + q_off + (int64_t)min(qi, qi_last) * p.q_is +
                   (int64_t)head * p.q_hs;
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
+    for (int s = 0; s < kDS; ++s) {
       if (row_ok) {
         qv[s] = *reinterpret_cast<const v8*>(qr + 16 * s + 8 * half);
       } else {
@@ -226,15 +236,20 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
     }
   }
 
-  // Loader: K keys kr and kr+32 (page slots kr/16 and 2+kr/16, both
-  // wave-uniform), V keys 2kr and 2kr+1 (page slot kr/8 = wave/2), 16-byte
-  // chunk kc of the 256-byte token row.
-  const int kc = tid & 15, kr = tid >> 4;
+  // Loader, head_dim 128: K keys kr and kr+32 (page slots kr/16 and 2+kr/16,
+  // both wave-uniform), V keys 2kr and 2kr+1 (page slot kr/8 = wave/2), 16-byte
+  // chunk kc of the 256-byte token row.  Head_dim 64: K key kr (page slot
+  // wave/2), V keys 2kr and 2kr+1 by waves 0-3 (page slot = wave), chunk kc of
+  // the 128-byte row.
+  constexpr int kCh = kD / 8;  // 16-byte chunks per token row
+  const int kc = tid & (kCh - 1), kr = tid / kCh;
   const T* kbase = static_cast<const T*>(p.k) + (int64_t)g * p.head_stride + 8 * kc;
   const T* vbase = static_cast<const T*>(p.v) + (int64_t)g * p.head_stride + 8 * kc;
   const int32_t* table = kDense ? nullptr : p.page_table + (int64_t)b * p.table_stride;
   const int dense0 = kDense ? b * p.dense_ppb : 0;  // table-less pages: sequence b's first
-  const int kslot = wave >> 2, vslot = wave >> 1;
+  const int kslot = kD == 128 ? wave >> 2 : wave >> 1;
+  const int vslot = kD == 128 ? wave >> 1 : wave;
+  const bool vload = kD == 128 || wave < 4;
 
   // Page ids of a tile (4 uniform values; -1 past the end).
   auto fetch_ids = [&](int tile) {
@@ -252,13 +267,17 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
     return m;
   };
 
-  v8 kreg[2], vreg[2];
+  constexpr int kKL = kD == 128 ? 2 : 1;  // K rows loaded per thread per tile
+  auto slot_id = [&](i32x4 ids, int slot) {
+    return uniform(slot & 2 ? (slot & 1 ? ids[3] : ids[2]) : (slot & 1 ? ids[1] : ids[0]));
+  };
+  v8 kreg[kKL], vreg[2];
   float fw_r = 1.0f, fb_r = 0.0f;
   auto issue = [&](int tile, i32x4 ids) {
     const int t0 = t_begin + tile * kPfKT;
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int pid = uniform(kslot ? ids[2 * r + 1] : ids[2 * r]);
+    for (int r = 0; r < kKL; ++r) {
+      const int pid = kD == 128 ? uniform(kslot ? ids[2 * r + 1] : ids[2 * r]) : slot_id(ids, kslot);
       // Dense pages may end inside the last one: tokens past the key range
       // are not read (past the tensor's end for its last head).
       const bool kin = !kDense || t0 + 32 * r + kr < hi;
@@ -269,8 +288,8 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
         for (int e = 0; e < 8; ++e) kreg[r][e] = static_cast<T>(0.0f);
       }
     }
-    {
-      const int pid = uniform(vslot & 2 ? (vslot & 1 ? ids[3] : ids[2]) : (vslot & 1 ? ids[1] : ids[0]));
+    if (vload) {
+      const int pid = slot_id(ids, vslot);
       if (page_ok(pid, p.num_pages)) {
         const T* vp = vbase + (int64_t)pid * p.page_stride + (int64_t)((2 * kr) & 15) * p.tok_stride;
         if (kDense) {
@@ -298,10 +317,12 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
   auto store = [&](int stage) {
     T* kd = ks + stage * kKStage + 8 * kc;
 #pragma unroll
-    for (int r = 0; r < 2; ++r) *reinterpret_cast<v8*>(kd + (32 * r + swap23(kr)) * kKRow) = kreg[r];
-    uint32_t* vd = vts + stage * kVStage + 4 * ((kr >> 2) ^ (kc >> 1)) + (kr & 3);
+    for (int r = 0; r < kKL; ++r) *reinterpret_cast<v8*>(kd + (32 * r + swap23(kr)) * kKRow) = kreg[r];
+    if (vload) {
+      uint32_t* vd = vts + stage * kVStage + 4 * ((kr >> 2) ^ (kc >> 1)) + (kr & 3);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) vd[(8 * kc + e) * kVRowW] = bits16(vreg[0][e]) | (bits16(vreg[1][e]) << 16);
+      for (int e = 0; e < 8; ++e) vd[(8 * kc + e) * kVRowW] = bits16(vreg[0][e]) | (bits16(vreg[1][e]) << 16);
+    }
     if ((kVs || kBias) && tid < kPfKT) {
       if (kVs) fws[stage * kPfKT + tid] = fw_r;
       if (kBias) fbs[stage * kPfKT + tid] = fb_r;
@@ -316,7 +337,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
     for (int kb = 0; kb < 2; ++kb) {
       s[kb] = f32x16{};
 #pragma unroll
-      for (int st = 0; st < 8; ++st)
+      for (int st = 0; st < kDS; ++st)
         s[kb] = Mma32<T>::mma(*reinterpret_cast<const v8*>(kb0 + 32 * kb * kKRow + 16 * st), qv[st], s[kb]);
     }
   };
@@ -324,9 +345,9 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
   // at chunk (2s + half) ^ (d / 16) = 2(s ^ db) + (half ^ col / 16).
   const uint32_t* vread = vts + col * kVRowW + 4 * (half ^ (col >> 4));
 
-  f32x16 oacc[4];
+  f32x16 oacc[kDB];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) oacc[i] = f32x16{};
+  for (int i = 0; i < kDB; ++i) oacc[i] = f32x16{};
   float m_run = kNegInf, l_half = 0.0f;
   const float c2 = p.sm_scale * kLog2e;
 
@@ -423,14 +444,14 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
     m_run = mnew;
     if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) oacc[i] *= alpha;
+      for (int i = 0; i < kDB; ++i) oacc[i] *= alpha;
     }
     // O^T += V^T P^T over four 16-key steps.
     const uint32_t* vr = vread + st_cur * kVStage;
 #pragma unroll
     for (int s = 0; s < 4; ++s)
 #pragma unroll
-      for (int db = 0; db < 4; ++db) {
+      for (int db = 0; db < kDB; ++db) {
         const v8 a = *reinterpret_cast<const v8*>(vr + 32 * db * kVRowW + 8 * (s ^ db));
         oacc[db] = Mma32<T>::mma(a, __builtin_bit_cast(v8, pb[s]), oacc[db]);
       }
@@ -455,9 +476,9 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
     // Split partial: unnormalised O, the running max in natural-log units
     // (the softmax here is base 2) and the sum, merged by the combine kernel.
     const int64_t r = row_id(p, b, qi, head) * S + split;
-    float* dst = p.ws_o + r * 128 + 4 * half;
+    float* dst = p.ws_o + r * kD + 4 * half;
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
+    for (int db = 0; db < kDB; ++db)
 #pragma unroll
       for (int vq = 0; vq < 4; ++vq)
         *reinterpret_cast<f32x4*>(dst + 32 * db + 8 * vq) =
@@ -471,7 +492,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
   const float il = l > 0.0f ? 1.0f / l : 0.0f;
   T* orow = static_cast<T*>(p.out) + o_off + (int64_t)qi * p.o_is + (int64_t)head * p.o_hs;
 #pragma unroll
-  for (int db = 0; db < 4; ++db)
+  for (int db = 0; db < kDB; ++db)
 #pragma unroll
     for (int vq = 0; vq < 4; ++vq) {
       v4 o;
@@ -481,20 +502,22 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
     }
 }
 
-template <typename T, int G, bool kBias, bool kVs, bool kSplit, int kMode = 0>
+template <typename T, int G, bool kBias, bool kVs, bool kSplit, int kMode = 0, int kD = 128>
 int launch_one(const Params& p, dim3 grid, hipStream_t stream) {
   static bool lds_set[64] = {};  // per instance and device
+  constexpr size_t lds = PfGeom<kD>::kLdsBytes;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-  const void* fn = reinterpret_cast<const void*>(prefill_mfma_kernel<T, G, kBias, kVs, kSplit, kMode>);
+  const void* fn = reinterpret_cast<const void*>(prefill_mfma_kernel<T, G, kBias, kVs, kSplit, kMode, kD>);
   if (!lds_set[dev]) {
-    if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPfLdsBytes) != hipSuccess) {
-      set_error(KESSIE_ERR_HIP, "fog prefill (mfma): %zu bytes of LDS unavailable", kPfLdsBytes);
+    if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
+      set_error(KESSIE_ERR_HIP, "fog prefill (mfma): %zu bytes of LDS unavailable", lds);
       return KESSIE_ERR_HIP;
     }
     lds_set[dev] = true;
   }
-  hipLaunchKernelGGL((prefill_mfma_kernel<T, G, kBias, kVs, kSplit, kMode>), grid, dim3(kPfThreads), kPfLdsBytes, stream, p);
+  hipLaunchKernelGGL((prefill_mfma_kernel<T, G, kBias, kVs, kSplit, kMode, kD>), grid, dim3(kPfThreads), lds, stream,
+                     p);
   return check_launch("fog prefill (mfma)");
 }
 
@@ -521,9 +544,13 @@ int launch_prefill(Params& p, hipStream_t stream) {
   const int kpos = kPfRows / p.G;
   // Varlen: the live (sequence, query tile) pairs are numbered along x.
   dim3 grid(div_up(p.C, kpos) * p.Hkv * (p.q_start ? p.B : 1), p.q_start ? 1 : p.B, max(p.num_splits, 1));
-  if (p.page_table == nullptr)  // table-less pages (dense launchers): G 1, no bias, one split
+  if (p.page_table == nullptr) {  // table-less pages (dense launchers): G 1, no bias, one split
+    if (p.D == 64)
+      return p.vscale ? launch_one<T, 1, false, true, false, 1, 64>(p, grid, stream)
+                      : launch_one<T, 1, false, false, false, 1, 64>(p, grid, stream);
     return p.vscale ? launch_one<T, 1, false, true, false, 1>(p, grid, stream)
                     : launch_one<T, 1, false, false, false, 1>(p, grid, stream);
+  }
   switch (p.G) {
     case 1: return launch_split<T, 1>(p, grid, stream);
     case 2: return launch_split<T, 2>(p, grid, stream);
@@ -541,7 +568,8 @@ int launch_prefill(Params& p, hipStream_t stream) {
 bool prefill_mfma_ok(const Params& p, int dtype) {
   if (env_int("KESSIE_FORCE_GENERIC", 0)) return false;
   if (dtype != KESSIE_DTYPE_BF16 && dtype != KESSIE_DTYPE_F16) return false;
-  if (p.D != 128 || p.page_size != 16) return false;
+  // Head_dim 64 only on table-less pages (the dense launchers).
+  if (!(p.D == 128 || (p.D == 64 && p.page_table == nullptr)) || p.page_size != 16) return false;
   // Table-less pages: instantiated for the dense launchers' form only.
   if (p.page_table == nullptr && (p.dense_ppb <= 0 || p.G != 1 || p.bias || p.num_splits > 1)) return false;
   if (!(p.G == 1 || p.G == 2 || p.G == 4 || p.G == 8 || p.G == 16)) return false;

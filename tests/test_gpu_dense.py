@@ -1,8 +1,9 @@
 """GPU parity: the reference's dense launchers (launch_kessie_windowed_attn,
 launch_kessie_fused_fog_attn: fp16 [B, H, N, D], every position a query)
 through KeSSieKernels vs the CPU oracle (fp32 on upcast inputs).  head_dim 128
-with H*N a multiple of 16 runs on the MFMA prefill kernel (table-less pages),
-other shapes on the generic kernel.  Tolerance |gpu - ref| <= 2e-2 + 1e-2*|ref|."""
+or 64 with H*N a multiple of 16 runs on the MFMA prefill kernel (table-less
+pages), other shapes on the generic kernel.  Tolerance |gpu - ref| <= 2e-2 +
+1e-2*|ref|."""
 import pytest
 import torch
 
@@ -23,17 +24,22 @@ def _qkv(dev, b, h, n, d, seed):
     return [torch.randn(b, h, n, d, generator=gen(dev, seed + i), device=dev).to(torch.float16) for i in range(3)]
 
 
-# MFMA route: D = 128 and H*N a multiple of 16 (N itself need not be: the last
-# page of every head ends inside it); the rest run on the generic kernel.
+# MFMA route: D = 128 or 64 and H*N a multiple of 16 (N itself need not be:
+# the last page of every head ends inside it); the rest (here (2, 2, 100, *)
+# and (1, 3, 50, 64)) run on the generic kernel.
 SHAPES = [(2, 4, 256, 128), (1, 3, 1024, 128), (2, 32, 100, 128), (1, 4, 1000, 128), (3, 16, 37, 128),
-          (2, 2, 100, 128), (2, 3, 64, 64), (1, 2, 48, 64)]
+          (2, 2, 100, 128), (2, 3, 64, 64), (1, 2, 48, 64), (2, 4, 256, 64), (1, 4, 1000, 64), (3, 16, 37, 64),
+          (2, 2, 100, 64), (1, 3, 50, 64)]
+MFMA_ROUTE = {s for s in SHAPES if (s[1] * s[2]) % 16 == 0}
 
 
 @pytest.mark.parametrize("b,h,n,d", SHAPES)
 @pytest.mark.parametrize("window,causal", [(0, True), (37, True), (0, False), (1, True)])
-def test_windowed_attention(dev, b, h, n, d, window, causal):
+def test_windowed_attention(dev, monkeypatch, b, h, n, d, window, causal):
     from kessie_amd.kessie_hip_ctypes import KeSSieKernels
 
+    if (b, h, n, d) in MFMA_ROUTE:
+        monkeypatch.setenv("KESSIE_REQUIRE_MFMA", "1")  # the launcher errors if it would use the generic kernel
     q, k, v = _qkv(dev, b, h, n, d, seed=n + d + window)
     out = KeSSieKernels().windowed_attention(q, k, v, window_size=window, causal=causal)
     ref = windowed_attention_ref(q.float().cpu(), k.float().cpu(), v.float().cpu(), window, causal)
@@ -42,9 +48,11 @@ def test_windowed_attention(dev, b, h, n, d, window, causal):
 
 @pytest.mark.parametrize("b,h,n,d", SHAPES)
 @pytest.mark.parametrize("window", [0, 200])
-def test_fused_fog_attention(dev, b, h, n, d, window):
+def test_fused_fog_attention(dev, monkeypatch, b, h, n, d, window):
     from kessie_amd.kessie_hip_ctypes import KeSSieKernels
 
+    if (b, h, n, d) in MFMA_ROUTE:
+        monkeypatch.setenv("KESSIE_REQUIRE_MFMA", "1")
     q, k, v = _qkv(dev, b, h, n, d, seed=2 * n + d)
     w = torch.rand(n, generator=gen(dev, 7), device=dev)
     out = KeSSieKernels().fused_fog_attention(q, k, v, w, window_size=window)
@@ -52,18 +60,33 @@ def test_fused_fog_attention(dev, b, h, n, d, window):
     _check(out, ref)
 
 
-def test_dense_mfma_matches_generic(dev, monkeypatch):
+@pytest.mark.parametrize("d", [128, 64])
+def test_dense_mfma_matches_generic(dev, monkeypatch, d):
     """The MFMA route (table-less pages) and the generic kernel agree on a
     2,048-token causal fog case, both within tolerance of the oracle."""
     from kessie_amd.kessie_hip_ctypes import KeSSieKernels
 
-    q, k, v = _qkv(dev, 1, 8, 2048, 128, seed=11)
+    q, k, v = _qkv(dev, 1, 8, 2048, d, seed=11)
     w = torch.rand(2048, generator=gen(dev, 12), device=dev)
     kk = KeSSieKernels()
+    monkeypatch.setenv("KESSIE_REQUIRE_MFMA", "1")
     fast = kk.fused_fog_attention(q, k, v, w)
+    monkeypatch.delenv("KESSIE_REQUIRE_MFMA")
     monkeypatch.setenv("KESSIE_FORCE_GENERIC", "1")
     slow = kk.fused_fog_attention(q, k, v, w)
     ref = fused_fog_attention_ref(q.float().cpu(), k.float().cpu(), v.float().cpu(), w.cpu())
     _check(fast, ref)
     _check(slow, ref)
     assert not torch.equal(fast, slow)  # two different kernels ran
+
+
+def test_require_mfma_switch_rejects_a_generic_shape(dev, monkeypatch):
+    """H*N not a multiple of 16 has no MFMA route: with the switch set the
+    launcher reports it instead of running the generic kernel."""
+    from kessie_amd import _lib
+    from kessie_amd.kessie_hip_ctypes import KeSSieKernels
+
+    monkeypatch.setenv("KESSIE_REQUIRE_MFMA", "1")
+    q, k, v = _qkv(dev, 1, 3, 50, 64, seed=13)
+    with pytest.raises(_lib.KeSSieError, match="generic kernel"):
+        KeSSieKernels().windowed_attention(q, k, v)
