@@ -403,6 +403,23 @@ int kessie_fog_bias_fill(void* buf, int dtype, int kv_len, double fog_alpha,
                          double fog_start, const int32_t* recall_positions,
                          int num_recall, double recall_boost, void* stream);
 
+/* Per-sequence fog logit bias for a batch, as fp32 rows the attention
+ * kernels read with fog_bias_bstride = row_stride: row b (b < num_rows)
+ * holds, at positions p < seq_lens[b] (device int32, clamped to [0, max_len]),
+ * exactly what kessie_fog_bias_fill computes in `dtype` for kv_len =
+ * seq_lens[b] (each sequence its own fog boundary
+ * B_b = int(seq_lens[b] * (1.0 - fog_start))), widened to fp32; positions
+ * from seq_lens[b] to max_len - 1 get 0.  Recalled positions below a row's
+ * length get dtype(recall_boost).  Two launches, no host synchronisation.
+ * (kessie_attention.py:114-139 builds one vector per call, for one kv_len;
+ * this is that vector for every sequence of a mixed batch.) */
+int kessie_fog_bias_fill_rows(float* out, int64_t row_stride,
+                              const int32_t* seq_lens, int num_rows,
+                              int max_len, int dtype, double fog_alpha,
+                              double fog_start,
+                              const int32_t* recall_positions, int num_recall,
+                              double recall_boost, void* stream);
+
 /* Fog V weights (fp32) into weights[0:seq_len], replacing
  * kessie_build_fog_weights (kessie_hip_kernels.py:403-413): 1 everywhere;
  * with c = int(seq_len * (1.0 - fog_start)) and fog_alpha > 0,

@@ -82,6 +82,8 @@ SIGNATURES = {
     "kessie_page_gather": (_I, [_P, _I64, _P, _P, _I, _I, _P, _P]),
     # buf, dtype, kv_len, fog_alpha, fog_start, recall, num_recall, boost, stream
     "kessie_fog_bias_fill": (_I, [_P, _I, _I, _D, _D, _P, _I, _D, _P]),
+    # out, row_stride, seq_lens, rows, max_len, dtype, fog_alpha, fog_start, recall, num_recall, boost, stream
+    "kessie_fog_bias_fill_rows": (_I, [_P, _I64, _P, _I, _I, _I, _D, _D, _P, _I, _D, _P]),
     "kessie_fog_weights_fill": (_I, [_P, _I, _D, _D, _P]),
     # pool + 4 strides, key + 2 strides, value + 2 strides, slots, T, H, D, P, pages, dtype, stream
     "kessie_hf_fog_weights_fill": (_I, [_P, _I, _D, _D, _P]),

@@ -60,6 +60,58 @@ __global__ __launch_bounds__(kThreads) void recall_scatter_kernel(T* buf, int kv
   if (p >= 0 && p < kv_len) buf[p] = round_to<T>(boost);
 }
 
+// One row per sequence: row b is the vector above for kv_len = seq_lens[b]
+// (its own fog boundary B_b = int(len * (1 - fog_start)), computed in double
+// as in Python), every value rounded as in `T` and stored as fp32 -- the form
+// the attention kernels read; positions at or past the row's length are 0.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void fog_bias_rows_kernel(float* out, int64_t row_stride,
+                                                                 const int32_t* seq_lens, int max_len,
+                                                                 double one_minus_fs, float neg_alpha) {
+#pragma clang fp contract(off)
+  const int b = blockIdx.y;
+  const int i = blockIdx.x * kThreads + threadIdx.x;
+  if (i >= max_len) return;
+  const int len = min(max(seq_lens[b], 0), max_len);
+  const double bd = (double)len * one_minus_fs;
+  const int64_t big_b = bd <= 0.0 ? 0 : (int64_t)bd;
+  const int boundary = (int)(big_b < len ? big_b : len);
+  float v = 0.0f;
+  if (i < boundary) {
+    const float inv_b = __frcp_rn((float)big_b);  // fp32 1/B, rounded to nearest as on the host
+    const T pos = round_to<T>((float)i);
+    const T x = round_to<T>(to_f32(pos) * inv_b);
+    const T d = round_to<T>(1.0f - to_f32(x));
+    const T d2 = round_to<T>(to_f32(d) * to_f32(d));
+    v = to_f32(round_to<T>(to_f32(d2) * neg_alpha));
+  }
+  out[(int64_t)b * row_stride + i] = v;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void recall_rows_kernel(float* out, int64_t row_stride,
+                                                               const int32_t* seq_lens, int max_len,
+                                                               const int32_t* pos, int n, float boost) {
+  const int b = blockIdx.y;
+  const int r = blockIdx.x * kThreads + threadIdx.x;
+  if (r >= n) return;
+  const int len = min(max(seq_lens[b], 0), max_len);
+  const int p = pos[r];
+  if (p >= 0 && p < len) out[(int64_t)b * row_stride + p] = to_f32(round_to<T>(boost));
+}
+
+template <typename T>
+int fog_bias_rows_launch(float* out, int64_t row_stride, const int32_t* seq_lens, int rows, int max_len,
+                         double one_minus_fs, float neg_alpha, const int32_t* recall, int n_recall, float boost,
+                         hipStream_t s) {
+  hipLaunchKernelGGL(fog_bias_rows_kernel<T>, dim3(div_up(max_len, kThreads), rows), dim3(kThreads), 0, s, out,
+                     row_stride, seq_lens, max_len, one_minus_fs, neg_alpha);
+  if (n_recall > 0)
+    hipLaunchKernelGGL(recall_rows_kernel<T>, dim3(div_up(n_recall, kThreads), rows), dim3(kThreads), 0, s, out,
+                       row_stride, seq_lens, max_len, recall, n_recall, boost);
+  return check_launch("fog bias rows");
+}
+
 // Exponent forms torch's device pow(tensor, scalar) special-cases, so the
 // weights take the same arithmetic route (alpha > 0 only reaches here).
 enum PowForm { kPowGeneral = 0, kPowOne = 1, kPowHalf = 2, kPowTwo = 3, kPowThree = 4 };
@@ -333,6 +385,40 @@ extern "C" int kessie_fog_bias_fill(void* buf, int dtype, int kv_len, double fog
       return fog_bias_launch<f16_t>(buf, kv_len, boundary, inv_b, neg_alpha, recall_positions, num_recall, boost, s);
   }
   set_error(KESSIE_ERR_UNSUPPORTED, "fog bias: dtype %d", dtype);
+  return KESSIE_ERR_UNSUPPORTED;
+}
+
+extern "C" int kessie_fog_bias_fill_rows(float* out, int64_t row_stride, const int32_t* seq_lens, int num_rows,
+                                         int max_len, int dtype, double fog_alpha, double fog_start,
+                                         const int32_t* recall_positions, int num_recall, double recall_boost,
+                                         void* stream) {
+  clear_error();
+  KESSIE_REQUIRE(num_rows >= 0 && max_len >= 0 && num_recall >= 0 && row_stride >= max_len, KESSIE_ERR_INVALID,
+                 "fog bias rows: rows %d, max_len %d, row_stride %lld, num_recall %d", num_rows, max_len,
+                 (long long)row_stride, num_recall);
+  if (num_rows == 0 || max_len == 0) return KESSIE_OK;
+  KESSIE_REQUIRE(num_rows <= 65535, KESSIE_ERR_UNSUPPORTED, "fog bias rows: %d rows (at most 65,535)", num_rows);
+  KESSIE_REQUIRE(out != nullptr && seq_lens != nullptr, KESSIE_ERR_INVALID, "fog bias rows: null pointer");
+  KESSIE_REQUIRE(num_recall == 0 || recall_positions != nullptr, KESSIE_ERR_INVALID,
+                 "fog bias rows: null recall list");
+  KESSIE_REQUIRE((double)max_len * (1.0 - fog_start) < 2147483648.0, KESSIE_ERR_INVALID,
+                 "fog bias rows: fog boundary out of range");
+  const double omf = 1.0 - fog_start;
+  const float neg_alpha = (float)(-fog_alpha);
+  const float boost = (float)recall_boost;
+  const hipStream_t s = as_stream(stream);
+  switch (dtype) {
+    case KESSIE_DTYPE_F32:
+      return fog_bias_rows_launch<float>(out, row_stride, seq_lens, num_rows, max_len, omf, neg_alpha,
+                                         recall_positions, num_recall, boost, s);
+    case KESSIE_DTYPE_BF16:
+      return fog_bias_rows_launch<bf16_t>(out, row_stride, seq_lens, num_rows, max_len, omf, neg_alpha,
+                                          recall_positions, num_recall, boost, s);
+    case KESSIE_DTYPE_F16:
+      return fog_bias_rows_launch<f16_t>(out, row_stride, seq_lens, num_rows, max_len, omf, neg_alpha,
+                                         recall_positions, num_recall, boost, s);
+  }
+  set_error(KESSIE_ERR_UNSUPPORTED, "fog bias rows: dtype %d", dtype);
   return KESSIE_ERR_UNSUPPORTED;
 }
 

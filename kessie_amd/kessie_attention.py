@@ -205,6 +205,34 @@ class _FogCache:
             return self._view
 
 
+    def get_fog_bias_rows(self, seq_lens, kv_len, device, dtype, state, seq_lens_host=None):
+        """fp32 [B, kv_len] bias for a batch: row b is the vector get_fog_bias
+        builds (in ``dtype``, widened to fp32) for that sequence's own kv_len =
+        seq_lens[b], zero past it.  One launch on the current stream, no host
+        synchronisation.  Shared by the layers of a step when the lengths are
+        known on the host (``seq_lens_host``): cached per generation and length
+        tuple; without them it is recomputed on every call."""
+        from . import ops
+
+        b = int(seq_lens.numel())
+        key = None
+        if seq_lens_host is not None:
+            key = (state["generation"], kv_len, str(device), dtype, tuple(int(x) for x in seq_lens_host.tolist()))
+            if key == getattr(self, "_rows_key", None):
+                return self._rows_view
+        rows_buf = getattr(self, "_rows_buf", None)
+        if (rows_buf is None or rows_buf.shape[0] < b or rows_buf.shape[1] < kv_len
+                or rows_buf.device != torch.device(device)):
+            cols = (max(kv_len, 2048) + 255) & ~255
+            self._rows_buf = rows_buf = torch.empty(max(b, 16), cols, dtype=torch.float32, device=device)
+        view = rows_buf[:b, :kv_len]
+        lens = seq_lens if seq_lens.dtype == torch.int32 else seq_lens.to(torch.int32)
+        recall = self._recall_for(frozenset(state["recall_positions"]), device)
+        ops.fog_bias_rows(view, lens, dtype, state["fog_alpha"], state["fog_start"], recall,
+                          state.get("recall_boost", 0.1))
+        self._rows_key, self._rows_view = key, view
+        return view
+
     def get_fog_bias_f32(self, kv_len, device, dtype, state):
         """The current generation's bias (computed in ``dtype`` as above)
         widened to fp32 [kv_len] for the kernels, once per generation."""
@@ -335,7 +363,8 @@ class KeSSieAttentionImpl:
     attn_metadata, output=None, ...) follows the reference's bypass rules
     (disabled, fog_alpha <= 0, prompt_len <= 0, an explicit attn_bias, fewer
     than four positional arguments) and otherwise attends with the fog bias of
-    the current generation over kv_len = the metadata's max_seq_len.
+    the current generation, each sequence's bias built for its own length
+    (seq_lens[b]).
     """
 
     def __init__(self, *args, **kwargs):
@@ -385,23 +414,30 @@ class KeSSieAttentionImpl:
         return getattr(inner, name)
 
     # -- the kernels --------------------------------------------------------------
-    _split_meta = None
+    _split_key = None
     _split_val = None
 
     @classmethod
     def _split(cls, meta):
-        """(query_start_loc on the host, decode sequences, prefill sequences),
-        computed once per metadata object: every layer of a step shares it, so
-        the one device-to-host copy happens once per step, not per layer."""
-        if cls._split_meta is meta:
-            return cls._split_val
-        qsl = meta.query_start_loc_cpu if getattr(meta, "query_start_loc_cpu", None) is not None \
-            else meta.query_start_loc.cpu()
-        qsl = [int(x) for x in qsl.tolist()]
+        """(query_start_loc on the host, decode sequences, prefill sequences).
+        Keyed by the content of the metadata's host copy query_start_loc_cpu,
+        so every layer of a step shares one computation and a runner that
+        refills one metadata object in place between steps is still seen;
+        without a host copy, query_start_loc is copied from the device on each
+        call."""
+        host = getattr(meta, "query_start_loc_cpu", None)
+        if host is not None:
+            key = tuple(int(x) for x in host.tolist())
+            if key == cls._split_key:
+                return cls._split_val
+            qsl = list(key)
+        else:
+            key = None
+            qsl = [int(x) for x in meta.query_start_loc.cpu().tolist()]
         nseq = len(qsl) - 1
         decode = [i for i in range(nseq) if qsl[i + 1] - qsl[i] == 1]
         prefill = [i for i in range(nseq) if qsl[i + 1] - qsl[i] > 1]
-        cls._split_meta, cls._split_val = meta, (qsl, decode, prefill)
+        cls._split_key, cls._split_val = key, (qsl, decode, prefill)
         return cls._split_val
 
     def _attend(self, args, kwargs, state):
@@ -435,27 +471,32 @@ class KeSSieAttentionImpl:
                                layout=layout, stream=sp)
 
         kv_len = int(meta.max_seq_len)
-        bias = None
-        if state is not None and kv_len > 0:
-            bias = _FOG_CACHE.get_fog_bias_f32(kv_len, query.device, query.dtype, state)
-
         qsl, decode, prefill = self._split(meta)
         nseq = len(qsl) - 1
         table = meta.block_table[:nseq]
         lens = meta.seq_lens[:nseq]
+        # Fog bias per sequence (row b built for that sequence's own length),
+        # rows read with a batch stride by the kernels.
+        bias = None
+        if state is not None and kv_len > 0 and nseq > 0:
+            lens_host = getattr(meta, "seq_lens_cpu", None)
+            bias = _FOG_CACHE.get_fog_bias_rows(lens, kv_len, query.device, query.dtype, state,
+                                                lens_host[:nseq] if lens_host is not None else None)
 
         if decode:
             if decode == list(range(decode[0], decode[0] + len(decode))):
                 lo, hi = decode[0], decode[-1] + 1
                 q_dec = q[qsl[lo]:qsl[lo] + (hi - lo)]
-                ops.fog_decode(q_dec, kv_cache, table[lo:hi], lens[lo:hi], kv_len, fog_bias=bias,
+                ops.fog_decode(q_dec, kv_cache, table[lo:hi], lens[lo:hi], kv_len,
+                               fog_bias=None if bias is None else bias[lo:hi],
                                window=self.window, sm_scale=self.scale, layout=layout,
                                out=out[qsl[lo]:qsl[lo] + (hi - lo)], stream=sp)
             else:
                 idx = torch.tensor(decode, device=q.device)
                 rows = torch.tensor([qsl[i] for i in decode], device=q.device)
                 o_dec = ops.fog_decode(q.index_select(0, rows).contiguous(), kv_cache, table.index_select(0, idx),
-                                       lens.index_select(0, idx), kv_len, fog_bias=bias, window=self.window,
+                                       lens.index_select(0, idx), kv_len,
+                                       fog_bias=None if bias is None else bias.index_select(0, idx), window=self.window,
                                        sm_scale=self.scale, layout=layout, stream=sp)
                 out.index_copy_(0, rows, o_dec)
         if len(prefill) > 1 and prefill == list(range(prefill[0], prefill[-1] + 1)):
@@ -467,13 +508,15 @@ class KeSSieAttentionImpl:
             if qs.dtype != torch.int32:
                 qs = qs.to(torch.int32)
             if ops.fog_prefill_varlen(q[s0:s1], qs, max(qsl[i + 1] - qsl[i] for i in prefill), kv_cache,
-                                      table[lo:hi], lens[lo:hi], kv_len, fog_bias=bias, window=self.window,
+                                      table[lo:hi], lens[lo:hi], kv_len,
+                                      fog_bias=None if bias is None else bias[lo:hi], window=self.window,
                                       causal=True, sm_scale=self.scale, layout=layout, out=out[s0:s1],
                                       stream=sp):
                 prefill = []
         for i in prefill:
             s, e = qsl[i], qsl[i + 1]
-            ops.fog_prefill(q[s:e].unsqueeze(0), kv_cache, table[i:i + 1], lens[i:i + 1], kv_len, fog_bias=bias,
+            ops.fog_prefill(q[s:e].unsqueeze(0), kv_cache, table[i:i + 1], lens[i:i + 1], kv_len,
+                            fog_bias=None if bias is None else bias[i:i + 1],
                             window=self.window, causal=True, sm_scale=self.scale, layout=layout,
                             out=out[s:e].unsqueeze(0), stream=sp)
         return output

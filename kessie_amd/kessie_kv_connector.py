@@ -278,6 +278,7 @@ class KeSSieKVConnector(KVConnectorBase_v1):
         self._block_size = 16
         self._copy_streams: Dict[int, torch.cuda.Stream] = {}
         self._pending_saves: List[Tuple[torch.cuda.Event, list]] = []
+        self._step = 0  # forward steps seen by this worker (start_load_kv runs once per step)
         self._scratch: Dict[Tuple[int, int], Tuple[torch.Tensor, torch.Tensor]] = {}
         logger.info(f"KeSSieKVConnector initialized (CPU budget: {max_gb:.0f} GB)")
 
@@ -353,6 +354,7 @@ class KeSSieKVConnector(KVConnectorBase_v1):
         insert (+ optional RoPE remap) launch, on the copy stream."""
         from . import ops
 
+        self._step += 1
         caches = kv_caches if kv_caches is not None else self._kv_caches
         names = layer_names if layer_names is not None else self._layer_names
         if isinstance(caches, dict):
@@ -464,10 +466,13 @@ class KeSSieKVConnector(KVConnectorBase_v1):
 
     def _save_plan(self, meta):
         """[(block_id, position_start, tokens)] of the blocks written this step,
-        computed once per metadata object (all layers share it)."""
+        computed once per step and metadata object (all layers of the step
+        share it; a runner that refills one metadata object in place is seen
+        again on the next step, which start_load_kv counts)."""
         if meta is None:
             return []
-        if getattr(self, "_plan_meta", None) is meta:
+        key = (self._step, id(meta))
+        if getattr(self, "_plan_key", None) == key and getattr(self, "_plan_meta", None) is meta:
             return self._plan
         block_tables = getattr(meta, "block_tables", None)
         if block_tables is None:
@@ -490,7 +495,7 @@ class KeSSieKVConnector(KVConnectorBase_v1):
                     if bid < 0 or (touched is not None and bid not in touched):
                         continue
                     plan.append((bid, bi * p, min(p, n - bi * p)))
-        self._plan_meta, self._plan = meta, plan
+        self._plan_meta, self._plan_key, self._plan = meta, key, plan
         return plan
 
     def _flush_saves(self, block: bool):

@@ -609,6 +609,32 @@ def fog_bias_fill(buf: torch.Tensor, kv_len: int, fog_alpha: float, fog_start: f
     return buf[:kv_len]
 
 
+def fog_bias_rows(out: torch.Tensor, seq_lens: torch.Tensor, dtype: torch.dtype, fog_alpha: float,
+                  fog_start: float, recall_positions: Optional[torch.Tensor] = None, recall_boost: float = 0.1,
+                  stream=None) -> torch.Tensor:
+    """Per-sequence fog bias: row b of ``out`` (fp32 [B, N], rows contiguous)
+    receives fog_bias_fill's vector for kv_len = seq_lens[b] (int32 device
+    tensor), computed in ``dtype`` and widened to fp32; positions at or past
+    seq_lens[b] are 0.  Returns out."""
+    if out.dtype != torch.float32 or out.dim() != 2 or out.stride(1) != 1:
+        raise ValueError("out must be fp32 [B, N] with contiguous rows")
+    b, n = out.shape
+    if seq_lens.dtype != torch.int32 or seq_lens.numel() < b or seq_lens.device != out.device:
+        raise ValueError("seq_lens must be int32 with one entry per row, on out's device")
+    nr = 0
+    if recall_positions is not None:
+        if recall_positions.dtype != torch.int32 or recall_positions.device != out.device:
+            raise TypeError("recall_positions must be int32 on out's device")
+        recall_positions = _contig(recall_positions.reshape(-1), "recall_positions")
+        nr = recall_positions.numel()
+    lib = _lib.load()
+    _lib.check("kessie_fog_bias_fill_rows", lib.kessie_fog_bias_fill_rows(
+        _ptr(out), out.stride(0), _ptr(_contig(seq_lens, "seq_lens")), b, n, dtype_code(dtype), float(fog_alpha),
+        float(fog_start), _ptr(recall_positions) if nr else None, nr, float(recall_boost),
+        _stream_ptr(stream, out.device)))
+    return out
+
+
 def fog_weights(seq_len: int, fog_alpha: float = 0.5, fog_start: float = 0.5, device=None,
                 out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
     """Fog V weights, fp32 [seq_len], computed on the device (the device

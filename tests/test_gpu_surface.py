@@ -199,12 +199,12 @@ def test_attention_impl_forward(dev, monkeypatch, order, fog):
     assert torch.equal(kv_cache.cpu(), ref_cache)
 
     pool = ref_cache.permute(1, 2, 0, 3, 4).contiguous()  # native [pages, P, 2, H, D]
-    kv_len = meta.max_seq_len
-    bias = fog_bias(kv_len, 0.5, 0.5, {5, 250}, 0.1, dtype=torch.bfloat16).float() if fog else None
     table, lens = meta.block_table.cpu(), meta.seq_lens.cpu()
     q = query.cpu().view(-1, hq, d)
     o = out.view(-1, hq, d)
     for i, (ql, ctx) in enumerate(seqs):
+        # Each sequence's bias is the reference's vector for its own length.
+        bias = fog_bias(ctx, 0.5, 0.5, {5, 250}, 0.1, dtype=torch.bfloat16).float() if fog else None
         s, e = qsl[i], qsl[i + 1]
         if ql == 1:
             ref = paged_decode_ref(q[s:e], pool, table[i:i + 1], lens[i:i + 1], None, bias)
@@ -323,3 +323,25 @@ def test_connector_save_and_recall(dev, monkeypatch, remap):
         mask = torch.ones(32, dtype=torch.bool)
         mask[[20, 21]] = False
         assert torch.equal(kf[:, mask].cpu(), bf[:, mask].cpu())
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_fog_bias_rows_match_the_reference_vector_per_sequence(dev, dtype):
+    """Row b of the batched producer equals, bit for bit, the reference's op
+    sequence run by torch on the same device for kv_len = seq_lens[b] (widened
+    to fp32), zero past the row's length; recalled positions past a row's
+    length leave it untouched."""
+    from kessie_amd import ops
+
+    lens = [0, 1, 7, 300, 4096, 131072, 999, 2]
+    n = max(lens)
+    rec = [5, 250, 4000, 131071]
+    out = torch.full((len(lens), n), float("nan"), dtype=torch.float32, device=dev)
+    ops.fog_bias_rows(out, torch.tensor(lens, dtype=torch.int32, device=dev), dtype, 0.5, 0.5,
+                      torch.tensor(rec, dtype=torch.int32, device=dev), 0.1)
+    torch.cuda.synchronize()
+    for b, ln in enumerate(lens):
+        if ln:
+            ref = fog_bias(ln, 0.5, 0.5, set(rec), 0.1, dtype=dtype, device=dev).reshape(-1).float()
+            assert torch.equal(out[b, :ln], ref), f"row {b} (len {ln})"
+        assert bool((out[b, ln:] == 0).all()), f"row {b} past its length"

@@ -169,3 +169,42 @@ def test_connector_save_plan_uses_slot_mapping():
     meta = Meta()
     assert conn._save_plan(meta) == [(9, 32, 8), (1, 16, 4)]
     assert conn._save_plan(meta) is conn._plan  # cached per metadata object
+
+
+def test_connector_save_plan_follows_metadata_refilled_in_place():
+    """A runner that reuses one metadata object and refills its tensors
+    between steps gets a fresh plan on the next step (start_load_kv counts
+    the steps); within a step the plan is shared by the layers."""
+    from kessie_amd import kessie_kv_connector as kc
+
+    class Meta:
+        block_table = torch.tensor([[5, 2, 9, 0]], dtype=torch.int32)
+        seq_lens = torch.tensor([40], dtype=torch.int32)
+        slot_mapping = torch.tensor([9 * 16 + 7], dtype=torch.int64)
+
+    conn = kc.KeSSieKVConnector()
+    meta = Meta()
+    conn.start_load_kv(kv_caches=[], layer_names=[])
+    assert conn._save_plan(meta) == [(9, 32, 8)]
+    meta.seq_lens[0] = 41                      # next step, same object, refilled in place
+    meta.block_table[0, 2] = 3
+    meta.slot_mapping[0] = 3 * 16 + 8
+    assert conn._save_plan(meta) == [(9, 32, 8)]  # same step: the shared plan
+    conn.start_load_kv(kv_caches=[], layer_names=[])
+    assert conn._save_plan(meta) == [(3, 32, 9)]
+
+
+def test_attention_split_follows_metadata_refilled_in_place():
+    """The decode / prefill split is keyed by the content of
+    query_start_loc_cpu, not by the metadata object."""
+    from kessie_amd import kessie_attention as ka
+
+    class Meta:
+        query_start_loc_cpu = torch.tensor([0, 1, 5, 6], dtype=torch.int32)
+
+    meta = Meta()
+    qsl, dec, pre = ka.KeSSieAttentionImpl._split(meta)
+    assert (qsl, dec, pre) == ([0, 1, 5, 6], [0, 2], [1])
+    meta.query_start_loc_cpu[1:] = torch.tensor([3, 4, 5], dtype=torch.int32)
+    qsl, dec, pre = ka.KeSSieAttentionImpl._split(meta)
+    assert (qsl, dec, pre) == ([0, 3, 4, 5], [1, 2], [0])
