@@ -7,22 +7,23 @@
 //
 // Work decomposition: one workgroup = 256 query rows (256/G positions x the G
 // heads of one kv head) of one sequence; 8 waves x 32 rows.  The workgroup
-// streams its kv head's keys in tiles of 64 (4 pages) through a three-stage
-// LDS ring, one barrier per tile:
-//   iteration t:  global loads of tile t+2 (page ids fetched one iteration
+// streams its kv head's keys in tiles of 64 (4 pages) through a four-stage
+// LDS ring (stage = tile & 3), one barrier per tile:
+//   iteration t:  global loads of tile t+2 (page ids fetched two iterations
 //                 earlier, wave-uniform, so no load waits on another);
-//                 S^T(t+1) = K Q^T on MFMA, independent of ...
-//                 ... the softmax of tile t (VALU), then O^T += V^T P^T(t);
-//                 tile t+2 to LDS; barrier.
+//                 the softmax of tile t (VALU) interleaved with S^T(t+1) =
+//                 K Q^T on MFMA, which does not depend on it; O^T += V^T
+//                 P^T(t); tile t+2 to LDS; barrier.
 // Per wave and tile: S^T (64 keys x 32 rows) on v_mfma_f32_32x32x16 (16
 // MFMAs) and O^T (128 d x 32 rows) likewise (16 MFMAs).  Key j of a 32-key
 // block sits in LDS row swap23(j), so register v of lane l of the S^T
 // accumulator holds key 16(v/8) + 8(l/32) + (v%8) of row l%32: the softmax is
-// lane-local plus one xor-32 shuffle, and p is already in the B-operand
+// lane-local plus one half-wave swap, and p is already in the B-operand
 // layout of PV.  V is stored transposed ([d][key], key pairs packed into
-// 32-bit words) with the 16-byte key chunks XOR-swizzled by d/16, so both the
-// transposing stores and the 16-byte operand reads are free of bank
-// conflicts; the K rows are padded to 68 words for the same reason.
+// 32-bit words, already scaled by the V-fog weights) with the 16-byte key
+// chunks XOR-swizzled by d/16, so both the transposing stores and the 16-byte
+// operand reads are free of bank conflicts; the K rows are padded to 68 words
+// for the same reason.  The softmax sum is taken from p as rounded for PV.
 // Grid index x = qtile * Hkv + g, so with 8 kv heads (and the hardware's
 // round-robin of workgroups over the 8 XCDs) every workgroup of kv head g
 // sits on one XCD and the query tiles of that head share its keys in L2.
@@ -47,7 +48,7 @@ constexpr int kPfWaves = 8;
 constexpr int kPfThreads = kPfWaves * 64;
 constexpr int kPfRows = kPfWaves * 32;  // query rows (position, head) per workgroup
 constexpr int kPfKT = 64;               // keys per tile (4 pages)
-constexpr int kPfStages = 3;            // LDS ring depth
+constexpr int kPfStages = 4;            // LDS ring depth (a power of two)
 constexpr int kVRowW = kPfKT / 2 + 4;   // V^T tile row stride (32-bit words)
 // LDS geometry for head_dim D: 128, or 64 (the dense launchers only).
 template <int D>
@@ -55,7 +56,7 @@ struct PfGeom {
   static constexpr int kKRow = D + 8;            // K tile row stride (elements)
   static constexpr int kKStage = kPfKT * kKRow;  // elements per K stage
   static constexpr int kVStage = D * kVRowW;     // words per V^T stage
-  static constexpr size_t kLdsBytes = (size_t)kPfStages * (kKStage * 2 + kVStage * 4 + 2 * kPfKT * 4);
+  static constexpr size_t kLdsBytes = (size_t)kPfStages * (kKStage * 2 + kVStage * 4 + kPfKT * 4);
 };
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
@@ -117,7 +118,30 @@ __device__ __forceinline__ float max3(float a, float b, float c) {
   return r;
 }
 
-__device__ __forceinline__ bool page_ok(int pid, int num_pages) { return pid >= 0 && pid < num_pages; }
+// max over lanes l and l ^ 32: v_permlane32_swap exchanges the two halves of
+// the wave in registers (no LDS round trip).  Written as inline assembly: the
+// builtin, given one value for both operands, is folded as if both results
+// were that value, which drops the exchange.  (s_nop 1: the two wait states
+// the swap needs after a VALU write of its operands.)
+__device__ __forceinline__ float max_xor32(float x) {
+  float a = x, b = x;
+  asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  return max3(a, b, b);
+}
+
+// acc + lo + hi of two packed T values (one v_dot2 against (1, 1)).
+template <typename T>
+__device__ __forceinline__ float sum2(uint32_t w, float acc);
+template <>
+__device__ __forceinline__ float sum2<bf16_t>(uint32_t w, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), __builtin_bit_cast(bf16x2, 0x3f803f80u), acc,
+                                         false);
+}
+template <>
+__device__ __forceinline__ float sum2<f16_t>(uint32_t w, float acc) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), __builtin_bit_cast(f16x2, 0x3c003c00u), acc, false);
+}
+
 
 template <typename T, int G, bool kBias, bool kVs, bool kSplit, int kMode, int kD>
 __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
@@ -134,8 +158,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
   extern __shared__ __align__(16) unsigned char smem[];
   T* ks = reinterpret_cast<T*>(smem);                                                // [stage][64][kKRow]
   uint32_t* vts = reinterpret_cast<uint32_t*>(smem + (size_t)kPfStages * kKStage * 2);  // [stage][128][kVRowW]
-  float* fws = reinterpret_cast<float*>(vts + kPfStages * kVStage);                   // [stage][64] V weight
-  float* fbs = fws + kPfStages * kPfKT;                                               // [stage][64] bias*log2(e)
+  float* fbs = reinterpret_cast<float*>(vts + kPfStages * kVStage);                   // [stage][64] bias*log2(e)
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = uniform(tid >> 6);
@@ -250,20 +273,30 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
   const int kslot = kD == 128 ? wave >> 2 : wave >> 1;
   const int vslot = kD == 128 ? wave >> 1 : wave;
   const bool vload = kD == 128 || wave < 4;
+  const int vkey_off = 16 * vslot + ((2 * kr) & 15);  // this thread's first V key in a tile
 
-  // Page ids of a tile (4 uniform values; -1 past the end).
+  // Page ids of a tile (4 uniform values; -1 past the end).  The table index
+  // is clamped into the readable entries and the value replaced afterwards, so
+  // the four scalar loads issue back to back with no branch around them.
   auto fetch_ids = [&](int tile) {
     const int pg0 = (t_begin + tile * kPfKT) >> 4;
     i32x4 ids;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      ids[j] = (tile < n_tiles && pg0 + j < n_tab) ? (kDense ? dense0 + pg0 + j : table[pg0 + j]) : -1;
+    for (int j = 0; j < 4; ++j) {
+      const bool in = tile < n_tiles && pg0 + j < n_tab;
+      if (kDense) {
+        ids[j] = in ? dense0 + pg0 + j : -1;
+      } else {
+        const int e = table[min(pg0 + j, n_tab - 1)];
+        ids[j] = in ? e : -1;
+      }
+    }
     return ids;
   };
   auto valid_mask = [&](i32x4 ids) {
     int m = 0;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) m |= page_ok(uniform(ids[j]), p.num_pages) ? (1 << j) : 0;
+    for (int j = 0; j < 4; ++j) m |= (uint32_t)uniform(ids[j]) < (uint32_t)p.num_pages ? (1 << j) : 0;
     return m;
   };
 
@@ -272,16 +305,17 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
     return uniform(slot & 2 ? (slot & 1 ? ids[3] : ids[2]) : (slot & 1 ? ids[1] : ids[0]));
   };
   v8 kreg[kKL], vreg[2];
-  float fw_r = 1.0f, fb_r = 0.0f;
-  auto issue = [&](int tile, i32x4 ids) {
+  float fw0 = 1.0f, fw1 = 1.0f, fb_r = 0.0f;
+  auto issue = [&](int tile, i32x4 ids, int pm) {
     const int t0 = t_begin + tile * kPfKT;
 #pragma unroll
     for (int r = 0; r < kKL; ++r) {
-      const int pid = kD == 128 ? uniform(kslot ? ids[2 * r + 1] : ids[2 * r]) : slot_id(ids, kslot);
+      const int slot = kD == 128 ? 2 * r + kslot : kslot;
       // Dense pages may end inside the last one: tokens past the key range
       // are not read (past the tensor's end for its last head).
       const bool kin = !kDense || t0 + 32 * r + kr < hi;
-      if (page_ok(pid, p.num_pages) && kin) {
+      if (((pm >> slot) & 1) && kin) {
+        const int pid = slot_id(ids, slot);
         kreg[r] = *reinterpret_cast<const v8*>(kbase + (int64_t)pid * p.page_stride + (int64_t)(kr & 15) * p.tok_stride);
       } else {
 #pragma unroll
@@ -289,31 +323,40 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
       }
     }
     if (vload) {
-      const int pid = slot_id(ids, vslot);
-      if (page_ok(pid, p.num_pages)) {
+      const int vkey = t0 + vkey_off;
+      if ((pm >> vslot) & 1) {
+        const int pid = slot_id(ids, vslot);
         const T* vp = vbase + (int64_t)pid * p.page_stride + (int64_t)((2 * kr) & 15) * p.tok_stride;
-        if (kDense) {
-          const int vkey = t0 + 16 * vslot + ((2 * kr) & 15);
+        if (t0 + kPfKT <= hi) {
+          vreg[0] = *reinterpret_cast<const v8*>(vp);
+          vreg[1] = *reinterpret_cast<const v8*>(vp + p.tok_stride);
+        } else {
+          // The tile ends past the key range: V rows there are not read (past
+          // a dense tensor's end, or leftovers a zero weight would not cancel
+          // if they are not finite) but zero.
 #pragma unroll
           for (int e = 0; e < 8; ++e) vreg[0][e] = vreg[1][e] = static_cast<T>(0.0f);
           if (vkey < hi) vreg[0] = *reinterpret_cast<const v8*>(vp);
           if (vkey + 1 < hi) vreg[1] = *reinterpret_cast<const v8*>(vp + p.tok_stride);
-        } else {
-          vreg[0] = *reinterpret_cast<const v8*>(vp);
-          vreg[1] = *reinterpret_cast<const v8*>(vp + p.tok_stride);
         }
       } else {
 #pragma unroll
         for (int e = 0; e < 8; ++e) vreg[0][e] = vreg[1][e] = static_cast<T>(0.0f);
       }
+      if (kVs) {
+        const float* vs = p.vscale + (int64_t)b * p.vs_bs;
+        fw0 = vkey < hi ? vs[vkey] : 0.0f;
+        fw1 = vkey + 1 < hi ? vs[vkey + 1] : 0.0f;
+      }
     }
-    if ((kVs || kBias) && tid < kPfKT) {
+    if (kBias && tid < kPfKT) {
       const int key = t0 + tid;
-      const bool in = key < hi;
-      if (kVs) fw_r = in ? p.vscale[(int64_t)b * p.vs_bs + key] : 1.0f;
-      if (kBias) fb_r = in ? p.bias[(int64_t)b * p.bias_bs + key] * kLog2e : 0.0f;
+      fb_r = key < hi ? p.bias[(int64_t)b * p.bias_bs + key] * kLog2e : 0.0f;
     }
   };
+  // V-fog: V rows are scaled by their fog weights here, rounded to T, as the
+  // reference scales V before its product (v * fog_weights), so the
+  // probabilities stay unscaled and the softmax sum can be taken from them.
   auto store = [&](int stage) {
     T* kd = ks + stage * kKStage + 8 * kc;
 #pragma unroll
@@ -321,14 +364,29 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
     if (vload) {
       uint32_t* vd = vts + stage * kVStage + 4 * ((kr >> 2) ^ (kc >> 1)) + (kr & 3);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) vd[(8 * kc + e) * kVRowW] = bits16(vreg[0][e]) | (bits16(vreg[1][e]) << 16);
+      for (int e = 0; e < 8; ++e)
+        vd[(8 * kc + e) * kVRowW] = kVs ? pack2<T>(to_f32(vreg[0][e]) * fw0, to_f32(vreg[1][e]) * fw1)
+                                        : bits16(vreg[0][e]) | (bits16(vreg[1][e]) << 16);
     }
-    if ((kVs || kBias) && tid < kPfKT) {
-      if (kVs) fws[stage * kPfKT + tid] = fw_r;
-      if (kBias) fbs[stage * kPfKT + tid] = fb_r;
-    }
+    if (kBias && tid < kPfKT) fbs[stage * kPfKT + tid] = fb_r;
   };
 
+  // Slice i of n (n >= 8) of store(): V^T word i for i < 8, then the K rows
+  // and the bias at slice n-1 -- spread over the PV MFMAs.  With no tile
+  // t+2 it rewrites a stage that no later tile reads.
+  auto store_slice = [&](int stage, int i, int n) {
+    if (vload && i < 8) {
+      uint32_t* vd = vts + stage * kVStage + 4 * ((kr >> 2) ^ (kc >> 1)) + (kr & 3);
+      vd[(8 * kc + i) * kVRowW] = kVs ? pack2<T>(to_f32(vreg[0][i]) * fw0, to_f32(vreg[1][i]) * fw1)
+                                      : bits16(vreg[0][i]) | (bits16(vreg[1][i]) << 16);
+    }
+    if (i == n - 1) {
+      T* kd = ks + stage * kKStage + 8 * kc;
+#pragma unroll
+      for (int r = 0; r < kKL; ++r) *reinterpret_cast<v8*>(kd + (32 * r + swap23(kr)) * kKRow) = kreg[r];
+      if (kBias && tid < kPfKT) fbs[stage * kPfKT + tid] = fb_r;
+    }
+  };
   // S^T of the tile in a stage: lane (col, half) reads K row 32kb + col.
   const T* kread = ks + col * kKRow + 8 * half;
   auto qk = [&](int stage, f32x16 (&s)[2]) {
@@ -351,54 +409,58 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
   float m_run = kNegInf, l_half = 0.0f;
   const float c2 = p.sm_scale * kLog2e;
 
+  // Tiles whose 64 keys all lie in [lo, hi) and are visible to every row of
+  // the workgroup (causal: none after the first row's position; window: none
+  // before the last row's window start): [ti_lo, ti_hi), uniform.
+  int ti_lo, ti_hi;
+  {
+    const int klo = p.window > 0 ? max(lo, qmax - p.window + 1) : lo;
+    const int khi = min(hi, qmin + 1);
+    const int dlo = klo - t_begin, dhi = khi - t_begin;
+    ti_lo = dlo <= 0 ? 0 : (dlo + kPfKT - 1) / kPfKT;
+    ti_hi = dhi <= 0 ? 0 : dhi / kPfKT;
+  }
+
   i32x4 ids_a, ids_b;  // page ids of tiles t+2 and t+3
   int pm0 = 0, pm1 = 0;    // valid-page masks of tiles t and t+1
-  f32x16 s_cur[2], s_nxt[2];
-  if (n_tiles > 0) {
-    const i32x4 ids0 = fetch_ids(0);
-    ids_a = fetch_ids(1);
-    pm0 = valid_mask(ids0);
-    issue(0, ids0);
-    store(0);
-    pm1 = valid_mask(ids_a);
-    issue(1, ids_a);
-    store(1);
-    ids_a = fetch_ids(2);
-    ids_b = fetch_ids(3);
-    __syncthreads();
-    qk(0, s_cur);
-  }
-  // One tile: sc holds its scores, sn receives the next tile's.  Waves 0-3
-  // compute the next scores before this tile's softmax, waves 4-7 after it,
-  // so the two waves sharing a SIMD keep its MFMA and VALU pipes both busy.
-  const bool qk_first = (kBias && kVs) || wave < 4;  // both fog modes: no split (register budget)
+  f32x16 s_a[2], s_b[2];
+  // One tile: sc holds its scores, sn receives the next tile's.  The next
+  // tile's S^T MFMAs do not depend on this tile's softmax, so they share one
+  // scheduling region with its exponentials and are interleaved with them:
+  // the wave keeps the matrix pipe busy while its VALU works (and the other
+  // wave of the SIMD fills what is left of either).
   auto step = [&](int t, f32x16 (&sc)[2], f32x16 (&sn)[2]) {
     const int t0 = t_begin + t * kPfKT;
-    const int st_cur = t % kPfStages;
-    const int st_nxt = (t + 1) % kPfStages;
-    const int st_new = (t + 2) % kPfStages;
+    const int st_cur = t & (kPfStages - 1);
+    const int st_nxt = (t + 1) & (kPfStages - 1);
+    const int st_new = (t + 2) & (kPfStages - 1);
     const bool more = t + 2 < n_tiles;
-    if (qk_first) qk(st_nxt, sn);
+    // Tile t+2's global loads go out first and land during this tile's work.
     const int pm2 = valid_mask(ids_a);
-    if (more) issue(t + 2, ids_a);
+    if (more) issue(t + 2, ids_a, pm2);
     ids_a = ids_b;
     ids_b = fetch_ids(t + 4);
 
-    // Interior tile: every key present and visible to every row (uniform).
-    const bool interior = pm0 == 0xF && t0 >= lo && t0 + kPfKT <= hi && t0 + kPfKT - 1 <= qmin &&
-                          (p.window == 0 || t0 > qmax - p.window);
-    const float* fwt = fws + st_cur * kPfKT + 8 * half;
+    const bool interior = pm0 == 0xF && t >= ti_lo && t < ti_hi;
     const float* fbt = fbs + st_cur * kPfKT + 8 * half;
     // Base-2 logits y = x * c2 (+ bias * log2 e); the tile max of y.
     if (!interior) {
+      // This lane's keys of the tile form one interval of key offsets,
+      // [klo_r, khi_r) relative to this lane's first key, intersected with
+      // the valid pages: one unsigned compare per key.
+      const int kbase = t0 + 8 * half;
+      int klo_r = lo, khi_r = hi;
+      if (p.causal || p.window > 0) khi_r = min(khi_r, q_pos + 1);
+      if (p.window > 0) klo_r = max(klo_r, q_pos - p.window + 1);
+      if (!row_ok) khi_r = klo_r;
+      const int off = klo_r - kbase;
+      const uint32_t len = (uint32_t)max(khi_r - klo_r, 0);
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-          const int kl = 32 * kb + 16 * (v >> 3) + 8 * half + (v & 7);
-          const int key = t0 + kl;
-          const bool ok = row_ok && ((pm0 >> (2 * kb + (v >> 3))) & 1) && key >= lo && key < hi &&
-                          key_visible(q_pos, key, p.window, p.causal);
+          const int kl = 32 * kb + 16 * (v >> 3) + (v & 7);  // key offset minus 8 * half
+          const bool ok = ((uint32_t)(kl - off) < len) & (((pm0 >> (2 * kb + (v >> 3))) & 1) != 0);
           float y = kBias ? fmaf(sc[kb][v], c2, fbt[32 * kb + 16 * (v >> 3) + (v & 7)]) : sc[kb][v];
           sc[kb][v] = ok ? y : kNegInf;
         }
@@ -416,57 +478,94 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
         ma = max3(ma, sc[kb][v], sc[kb][v + 1]);
         mb = max3(mb, sc[kb][v + 2], sc[kb][v + 3]);
       }
-    float mloc = fmaxf(ma, mb);
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+    float mloc = max_xor32(fmaxf(ma, mb));
     if (!kBias) mloc *= c2;  // without a bias, y = x * c2 and c2 > 0
     const float mnew = fmaxf(m_run, mloc);
     const float muse = mnew == kNegInf ? 0.0f : mnew;
     const float alpha = mnew == kNegInf ? 1.0f : __builtin_amdgcn_exp2f(m_run - mnew);
-    float psum = 0.0f;
-    u32x4 pb[4];  // p as the PV B operand, two keys per dword
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int v = 0; v < 16; v += 2) {
-        const float y0 = sc[kb][v], y1 = sc[kb][v + 1];
-        float p0 = __builtin_amdgcn_exp2f(kBias ? y0 - muse : fmaf(y0, c2, -muse));
-        float p1 = __builtin_amdgcn_exp2f(kBias ? y1 - muse : fmaf(y1, c2, -muse));
-        psum += p0;
-        psum += p1;
-        if (kVs) {
-          p0 *= fwt[32 * kb + 16 * (v >> 3) + (v & 7)];
-          p1 *= fwt[32 * kb + 16 * (v >> 3) + (v & 7) + 1];
-        }
-        pb[2 * kb + (v >> 3)][(v & 7) >> 1] = pack2<T>(p0, p1);
-      }
-    if (!qk_first) qk(st_nxt, sn);
-    l_half = l_half * alpha + psum;
-    m_run = mnew;
+    // (Rescaled before the exponentials, so that they, the next scores and PV
+    // form one branch-free region.)
     if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
 #pragma unroll
       for (int i = 0; i < kDB; ++i) oacc[i] *= alpha;
     }
-    // O^T += V^T P^T over four 16-key steps.
+    // The next tile's scores, this tile's exponentials and PV, and the stage
+    // store of tile t+2 in one branch-free region, in a fixed order: step i
+    // issues MFMA i (QK steps first, then PV), the LDS operand read of MFMA
+    // i+2, and a share of the VALU work -- one or two exponential pairs per
+    // QK step, one slice of the stage store per PV step -- so the wave keeps
+    // the matrix pipe busy while its VALU works.
+    constexpr int kQ = 2 * kDS;   // S^T MFMAs
+    constexpr int kPV = 4 * kDB;  // O^T MFMAs
+    constexpr int kPairsPer = 16 / kQ;
+    const T* kb0 = kread + st_nxt * kKStage;
     const uint32_t* vr = vread + st_cur * kVStage;
+    auto op_read = [&](int i) {
+      if (i < kQ) return *reinterpret_cast<const v8*>(kb0 + 32 * (i & 1) * kKRow + 16 * (i >> 1));
+      const int s = (i - kQ) / kDB, db = (i - kQ) % kDB;
+      return *reinterpret_cast<const v8*>(vr + 32 * db * kVRowW + 8 * (s ^ db));
+    };
+    float ps0 = 0.0f, ps1 = 0.0f;  // the softmax sum, from p as rounded for PV
+    u32x4 pb[4];                   // p as the PV B operand, two keys per dword
+    auto exp_pair = [&](int j) {   // keys 2j, 2j+1 of this lane's 32
+      const int kb = j >> 3, v = 2 * (j & 7);
+      const float y0 = sc[kb][v], y1 = sc[kb][v + 1];
+      const float p0 = __builtin_amdgcn_exp2f(kBias ? y0 - muse : fmaf(y0, c2, -muse));
+      const float p1 = __builtin_amdgcn_exp2f(kBias ? y1 - muse : fmaf(y1, c2, -muse));
+      const uint32_t w = pack2<T>(p0, p1);
+      pb[j >> 2][j & 3] = w;
+      if (j & 1)
+        ps1 = sum2<T>(w, ps1);
+      else
+        ps0 = sum2<T>(w, ps0);
+    };
+    v8 op[3];
+    op[0] = op_read(0);
+    op[1] = op_read(1);
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
-#pragma unroll
-      for (int db = 0; db < kDB; ++db) {
-        const v8 a = *reinterpret_cast<const v8*>(vr + 32 * db * kVRowW + 8 * (s ^ db));
-        oacc[db] = Mma32<T>::mma(a, __builtin_bit_cast(v8, pb[s]), oacc[db]);
+    for (int i = 0; i < kQ + kPV; ++i) {
+      if (i < kQ) {
+        sn[i & 1] = Mma32<T>::mma(op[i % 3], qv[i >> 1], i < 2 ? f32x16{} : sn[i & 1]);
+      } else {
+        const int s = (i - kQ) / kDB, db = (i - kQ) % kDB;
+        oacc[db] = Mma32<T>::mma(op[i % 3], __builtin_bit_cast(v8, pb[s]), oacc[db]);
       }
-
-    if (more) store(st_new);
+      if (i + 2 < kQ + kPV) op[(i + 2) % 3] = op_read(i + 2);
+      if (i < kQ) {
+#pragma unroll
+        for (int j = 0; j < kPairsPer; ++j) exp_pair(i * kPairsPer + j);
+      } else {
+        store_slice(st_new, i - kQ, kPV);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    l_half = l_half * alpha + (ps0 + ps1);
+    m_run = mnew;
     pm0 = pm1;
     pm1 = pm2;
     __syncthreads();
   };
-  // (Unrolling by two to alternate sc/sn instead of copying them spills at
-  // 256 VGPRs, the budget of two waves per SIMD.)
-  for (int t = 0; t < n_tiles; ++t) {
-    step(t, s_cur, s_nxt);
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) s_cur[kb] = s_nxt[kb];
+  if (n_tiles > 0) {
+    const i32x4 ids0 = fetch_ids(0);
+    ids_a = fetch_ids(1);
+    pm0 = valid_mask(ids0);
+    issue(0, ids0, pm0);
+    store(0);
+    pm1 = valid_mask(ids_a);
+    issue(1, ids_a, pm1);
+    store(1);
+    ids_a = fetch_ids(2);
+    ids_b = fetch_ids(3);
+    __syncthreads();
+    qk(0, s_a);
+    // Unrolled by two so the score buffers alternate instead of being copied.
+    // (Inside the prologue's branch, so the wait for the query loads stays
+    // here and not in every iteration, where it would also wait for the
+    // tile loads just issued.)
+    for (int t = 0; t < n_tiles; t += 2) {
+      step(t, s_a, s_b);
+      if (t + 1 < n_tiles) step(t + 1, s_b, s_a);
+    }
   }
 
   // Lane (col, half) holds row frow at d = 32*db + 8*(v/4) + 4*half + (v%4).
