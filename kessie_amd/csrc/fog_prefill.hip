@@ -21,9 +21,10 @@
 // lane-local plus one half-wave swap, and p is already in the B-operand
 // layout of PV.  V is stored transposed ([d][key], key pairs packed into
 // 32-bit words, already scaled by the V-fog weights) with the 16-byte key
-// chunks XOR-swizzled by d/16, so both the transposing stores and the 16-byte
-// operand reads are free of bank conflicts; the K rows are padded to 68 words
-// for the same reason.  The softmax sum is taken from p as rounded for PV.
+// chunks XOR-swizzled by d/16 and rows of 40 words: of the row strides and
+// swizzles measured on gfx950 (LDS bank-conflict counters) this one leaves the
+// 16-byte operand reads without conflicts and the transposing 4-byte stores
+// with the fewest; the K rows are padded to 68 words, also conflict-free.  The softmax sum is taken from p as rounded for PV.
 // Grid index x = qtile * Hkv + g, so with 8 kv heads (and the hardware's
 // round-robin of workgroups over the 8 XCDs) every workgroup of kv head g
 // sits on one XCD and the query tiles of that head share its keys in L2.
@@ -49,7 +50,7 @@ constexpr int kPfThreads = kPfWaves * 64;
 constexpr int kPfRows = kPfWaves * 32;  // query rows (position, head) per workgroup
 constexpr int kPfKT = 64;               // keys per tile (4 pages)
 constexpr int kPfStages = 4;            // LDS ring depth (a power of two)
-constexpr int kVRowW = kPfKT / 2 + 4;   // V^T tile row stride (32-bit words)
+constexpr int kVRowW = kPfKT / 2 + 8;   // V^T tile row stride (32-bit words)
 // LDS geometry for head_dim D: 128, or 64 (the dense launchers only).
 template <int D>
 struct PfGeom {
@@ -259,21 +260,26 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
     }
   }
 
-  // Loader, head_dim 128: K keys kr and kr+32 (page slots kr/16 and 2+kr/16,
-  // both wave-uniform), V keys 2kr and 2kr+1 (page slot kr/8 = wave/2), 16-byte
-  // chunk kc of the 256-byte token row.  Head_dim 64: K key kr (page slot
-  // wave/2), V keys 2kr and 2kr+1 by waves 0-3 (page slot = wave), chunk kc of
-  // the 128-byte row.
+  // Loader.  Head_dim 128: wave w loads page slot w/2 of the tile, K and V
+  // alike (one page id per wave): K rows rr and rr+8 of the page and the V row
+  // pair (2rr, 2rr+1), rr = lane/16 + 4(w%2), 16-byte chunk kc = lane%16 of the
+  // 256-byte token row.  Head_dim 64: K row kr = tid/8 of the tile (page slot
+  // w/2), V rows 2kr and 2kr+1 by waves 0-3 (page slot w), chunk kc of the
+  // 128-byte row.
   constexpr int kCh = kD / 8;  // 16-byte chunks per token row
-  const int kc = tid & (kCh - 1), kr = tid / kCh;
+  const int kc = tid & (kCh - 1);
+  const int rr = kD == 128 ? (lane >> 4) + 4 * (wave & 1) : tid / kCh;
+  const int kslot = wave >> 1;                      // K page slot
+  const int vslot = kD == 128 ? wave >> 1 : wave;   // V page slot
+  const int kp = kD == 128 ? 8 * vslot + rr : rr;  // V key pair of the tile (keys 2kp, 2kp+1)
+  auto krow = [&](int r) { return kD == 128 ? 16 * kslot + rr + 8 * r : rr; };  // K key of the tile
+  auto krow_lds = [&](int r) { return (krow(r) & 32) | swap23(krow(r) & 31); };  // its LDS row
   const T* kbase = static_cast<const T*>(p.k) + (int64_t)g * p.head_stride + 8 * kc;
   const T* vbase = static_cast<const T*>(p.v) + (int64_t)g * p.head_stride + 8 * kc;
   const int32_t* table = kDense ? nullptr : p.page_table + (int64_t)b * p.table_stride;
   const int dense0 = kDense ? b * p.dense_ppb : 0;  // table-less pages: sequence b's first
-  const int kslot = kD == 128 ? wave >> 2 : wave >> 1;
-  const int vslot = kD == 128 ? wave >> 1 : wave;
   const bool vload = kD == 128 || wave < 4;
-  const int vkey_off = 16 * vslot + ((2 * kr) & 15);  // this thread's first V key in a tile
+  const int vkey_off = 2 * kp;  // this thread's first V key in a tile
 
   // Page ids of a tile (4 uniform values; -1 past the end).  The table index
   // is clamped into the readable entries and the value replaced afterwards, so
@@ -308,15 +314,16 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
   float fw0 = 1.0f, fw1 = 1.0f, fb_r = 0.0f;
   auto issue = [&](int tile, i32x4 ids, int pm) {
     const int t0 = t_begin + tile * kPfKT;
+    const int kpid = slot_id(ids, kslot);
+    const bool kok = (pm >> kslot) & 1;
 #pragma unroll
     for (int r = 0; r < kKL; ++r) {
-      const int slot = kD == 128 ? 2 * r + kslot : kslot;
       // Dense pages may end inside the last one: tokens past the key range
       // are not read (past the tensor's end for its last head).
-      const bool kin = !kDense || t0 + 32 * r + kr < hi;
-      if (((pm >> slot) & 1) && kin) {
-        const int pid = slot_id(ids, slot);
-        kreg[r] = *reinterpret_cast<const v8*>(kbase + (int64_t)pid * p.page_stride + (int64_t)(kr & 15) * p.tok_stride);
+      const bool kin = !kDense || t0 + krow(r) < hi;
+      if (kok && kin) {
+        kreg[r] = *reinterpret_cast<const v8*>(kbase + (int64_t)kpid * p.page_stride +
+                                               (int64_t)(krow(r) & 15) * p.tok_stride);
       } else {
 #pragma unroll
         for (int e = 0; e < 8; ++e) kreg[r][e] = static_cast<T>(0.0f);
@@ -325,8 +332,8 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
     if (vload) {
       const int vkey = t0 + vkey_off;
       if ((pm >> vslot) & 1) {
-        const int pid = slot_id(ids, vslot);
-        const T* vp = vbase + (int64_t)pid * p.page_stride + (int64_t)((2 * kr) & 15) * p.tok_stride;
+        const int pid = kD == 128 ? kpid : slot_id(ids, vslot);
+        const T* vp = vbase + (int64_t)pid * p.page_stride + (int64_t)(vkey_off & 15) * p.tok_stride;
         if (t0 + kPfKT <= hi) {
           vreg[0] = *reinterpret_cast<const v8*>(vp);
           vreg[1] = *reinterpret_cast<const v8*>(vp + p.tok_stride);
@@ -360,9 +367,9 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
   auto store = [&](int stage) {
     T* kd = ks + stage * kKStage + 8 * kc;
 #pragma unroll
-    for (int r = 0; r < kKL; ++r) *reinterpret_cast<v8*>(kd + (32 * r + swap23(kr)) * kKRow) = kreg[r];
+    for (int r = 0; r < kKL; ++r) *reinterpret_cast<v8*>(kd + krow_lds(r) * kKRow) = kreg[r];
     if (vload) {
-      uint32_t* vd = vts + stage * kVStage + 4 * ((kr >> 2) ^ (kc >> 1)) + (kr & 3);
+      uint32_t* vd = vts + stage * kVStage + 4 * ((kp >> 2) ^ (kc >> 1)) + (kp & 3);
 #pragma unroll
       for (int e = 0; e < 8; ++e)
         vd[(8 * kc + e) * kVRowW] = kVs ? pack2<T>(to_f32(vreg[0][e]) * fw0, to_f32(vreg[1][e]) * fw1)
@@ -373,17 +380,18 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
 
   // Slice i of n (n >= 8) of store(): V^T word i for i < 8, then the K rows
   // and the bias at slice n-1 -- spread over the PV MFMAs.  With no tile
-  // t+2 it rewrites a stage that no later tile reads.
+  // t+2 it rewrites a stage that no later tile reads.  (Moving the slices to
+  // the last PV steps, to give the tile's loads longer, measured slower.)
   auto store_slice = [&](int stage, int i, int n) {
     if (vload && i < 8) {
-      uint32_t* vd = vts + stage * kVStage + 4 * ((kr >> 2) ^ (kc >> 1)) + (kr & 3);
+      uint32_t* vd = vts + stage * kVStage + 4 * ((kp >> 2) ^ (kc >> 1)) + (kp & 3);
       vd[(8 * kc + i) * kVRowW] = kVs ? pack2<T>(to_f32(vreg[0][i]) * fw0, to_f32(vreg[1][i]) * fw1)
                                       : bits16(vreg[0][i]) | (bits16(vreg[1][i]) << 16);
     }
     if (i == n - 1) {
       T* kd = ks + stage * kKStage + 8 * kc;
 #pragma unroll
-      for (int r = 0; r < kKL; ++r) *reinterpret_cast<v8*>(kd + (32 * r + swap23(kr)) * kKRow) = kreg[r];
+      for (int r = 0; r < kKL; ++r) *reinterpret_cast<v8*>(kd + krow_lds(r) * kKRow) = kreg[r];
       if (kBias && tid < kPfKT) fbs[stage * kPfKT + tid] = fb_r;
     }
   };
