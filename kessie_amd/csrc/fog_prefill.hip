@@ -9,11 +9,12 @@
 // heads of one kv head) of one sequence; 8 waves x 32 rows.  The workgroup
 // streams its kv head's keys in tiles of 64 (4 pages) through a four-stage
 // LDS ring (stage = tile & 3), one barrier per tile:
-//   iteration t:  global loads of tile t+2 (page ids fetched two iterations
-//                 earlier, wave-uniform, so no load waits on another);
+//   iteration t:  buffer loads of tile t+3 into one of two register sets
+//                 (page ids fetched two iterations earlier, wave-uniform);
 //                 the softmax of tile t (VALU) interleaved with S^T(t+1) =
 //                 K Q^T on MFMA, which does not depend on it; O^T += V^T
-//                 P^T(t); tile t+2 to LDS; barrier.
+//                 P^T(t) interleaved with the store of tile t+2 (loaded one
+//                 iteration earlier) from the other set to LDS; barrier.
 // Per wave and tile: S^T (64 keys x 32 rows) on v_mfma_f32_32x32x16 (16
 // MFMAs) and O^T (128 d x 32 rows) likewise (16 MFMAs).  Key j of a 32-key
 // block sits in LDS row swap23(j), so register v of lane l of the S^T
@@ -60,6 +61,8 @@ struct PfGeom {
   static constexpr size_t kLdsBytes = (size_t)kPfStages * (kKStage * 2 + kVStage * 4 + kPfKT * 4);
 };
 constexpr float kLog2e = 1.4426950408889634f;
+// Word 3 of a raw (unformatted, stride 0) buffer resource on gfx9-family parts.
+constexpr int kRsrcWord3 = 0x00020000;
 constexpr float kLn2 = 0.6931471805599453f;
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -274,8 +277,6 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
   const int kp = kD == 128 ? 8 * vslot + rr : rr;  // V key pair of the tile (keys 2kp, 2kp+1)
   auto krow = [&](int r) { return kD == 128 ? 16 * kslot + rr + 8 * r : rr; };  // K key of the tile
   auto krow_lds = [&](int r) { return (krow(r) & 32) | swap23(krow(r) & 31); };  // its LDS row
-  const T* kbase = static_cast<const T*>(p.k) + (int64_t)g * p.head_stride + 8 * kc;
-  const T* vbase = static_cast<const T*>(p.v) + (int64_t)g * p.head_stride + 8 * kc;
   const int32_t* table = kDense ? nullptr : p.page_table + (int64_t)b * p.table_stride;
   const int dense0 = kDense ? b * p.dense_ppb : 0;  // table-less pages: sequence b's first
   const bool vload = kD == 128 || wave < 4;
@@ -305,94 +306,97 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
     for (int j = 0; j < 4; ++j) m |= (uint32_t)uniform(ids[j]) < (uint32_t)p.num_pages ? (1 << j) : 0;
     return m;
   };
-
-  constexpr int kKL = kD == 128 ? 2 : 1;  // K rows loaded per thread per tile
   auto slot_id = [&](i32x4 ids, int slot) {
     return uniform(slot & 2 ? (slot & 1 ? ids[3] : ids[2]) : (slot & 1 ? ids[1] : ids[0]));
   };
-  v8 kreg[kKL], vreg[2];
-  float fw0 = 1.0f, fw1 = 1.0f, fb_r = 0.0f;
-  auto issue = [&](int tile, i32x4 ids, int pm) {
+
+  // Global loads go through buffer resources whose record count covers only
+  // the page's rows inside the key range (none for an invalid page id), so
+  // rows past the range, past a dense tensor's end or of an invalid page read
+  // as zero with no branch: every tile issues the same loads, and the wait
+  // for one tile's data does not wait for the next tile's loads.  All
+  // offsets are in the per-lane offset, which the range check covers.
+  constexpr int kKL = kD == 128 ? 2 : 1;  // K rows loaded per thread per tile
+  const int ts_b = (int)p.tok_stride * (int)sizeof(T);
+  constexpr int kRowB = kD * (int)sizeof(T);
+  const char* kpool = static_cast<const char*>(p.k) + (int64_t)g * p.head_stride * (int64_t)sizeof(T);
+  const char* vpool = static_cast<const char*>(p.v) + (int64_t)g * p.head_stride * (int64_t)sizeof(T);
+  uint32_t koff[kKL];
+#pragma unroll
+  for (int r = 0; r < kKL; ++r) koff[r] = (uint32_t)((krow(r) & 15) * ts_b + 16 * kc);
+  const uint32_t voff0 = (uint32_t)((vkey_off & 15) * ts_b + 16 * kc), voff1 = voff0 + (uint32_t)ts_b;
+  auto page_rsrc = [&](const char* pool, int pid, int first_tok) {
+    const int nrows = min(max(hi - first_tok, 0), 16);
+    const bool ok = (uint32_t)pid < (uint32_t)p.num_pages && nrows > 0;
+    const char* base = ok ? pool + (int64_t)pid * p.page_stride * (int64_t)sizeof(T) : pool;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), (short)0, ok ? (nrows - 1) * ts_b + kRowB : 0,
+                                             kRsrcWord3);
+  };
+  // Rows of V weights and of the bias: keys past the range read as zero.
+  // (The second weight goes through a resource starting one key later, so the
+  // two loads are not merged into one 8-byte load, which would straddle the
+  // range's end for the last key.)
+  float* const fw_row = kVs ? const_cast<float*>(p.vscale + (int64_t)b * p.vs_bs) : nullptr;
+  const auto fw_rsrc = __builtin_amdgcn_make_buffer_rsrc(fw_row, (short)0, kVs ? hi * 4 : 0, kRsrcWord3);
+  const auto fw1_rsrc = __builtin_amdgcn_make_buffer_rsrc(kVs ? fw_row + 1 : nullptr, (short)0,
+                                                          kVs ? max(hi - 1, 0) * 4 : 0, kRsrcWord3);
+  const auto fb_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      kBias ? const_cast<float*>(p.bias + (int64_t)b * p.bias_bs) : nullptr, (short)0, kBias ? hi * 4 : 0, kRsrcWord3);
+
+  // Two register sets: the loads of tile t+3 go out in iteration t, one
+  // iteration before their stage store, and land behind a whole iteration.
+  v8 kreg[2][kKL], vreg[2][2];
+  float fw0[2] = {1.0f, 1.0f}, fw1[2] = {1.0f, 1.0f}, fb_r[2] = {0.0f, 0.0f};
+  auto issue = [&](int tile, i32x4 ids, int set) {
     const int t0 = t_begin + tile * kPfKT;
-    const int kpid = slot_id(ids, kslot);
-    const bool kok = (pm >> kslot) & 1;
+    const auto krs = page_rsrc(kpool, slot_id(ids, kslot), t0 + 16 * kslot);
 #pragma unroll
-    for (int r = 0; r < kKL; ++r) {
-      // Dense pages may end inside the last one: tokens past the key range
-      // are not read (past the tensor's end for its last head).
-      const bool kin = !kDense || t0 + krow(r) < hi;
-      if (kok && kin) {
-        kreg[r] = *reinterpret_cast<const v8*>(kbase + (int64_t)kpid * p.page_stride +
-                                               (int64_t)(krow(r) & 15) * p.tok_stride);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) kreg[r][e] = static_cast<T>(0.0f);
-      }
-    }
+    for (int r = 0; r < kKL; ++r)
+      kreg[set][r] = __builtin_bit_cast(v8, __builtin_amdgcn_raw_buffer_load_b128(krs, (int)koff[r], 0, 0));
     if (vload) {
-      const int vkey = t0 + vkey_off;
-      if ((pm >> vslot) & 1) {
-        const int pid = kD == 128 ? kpid : slot_id(ids, vslot);
-        const T* vp = vbase + (int64_t)pid * p.page_stride + (int64_t)(vkey_off & 15) * p.tok_stride;
-        if (t0 + kPfKT <= hi) {
-          vreg[0] = *reinterpret_cast<const v8*>(vp);
-          vreg[1] = *reinterpret_cast<const v8*>(vp + p.tok_stride);
-        } else {
-          // The tile ends past the key range: V rows there are not read (past
-          // a dense tensor's end, or leftovers a zero weight would not cancel
-          // if they are not finite) but zero.
-#pragma unroll
-          for (int e = 0; e < 8; ++e) vreg[0][e] = vreg[1][e] = static_cast<T>(0.0f);
-          if (vkey < hi) vreg[0] = *reinterpret_cast<const v8*>(vp);
-          if (vkey + 1 < hi) vreg[1] = *reinterpret_cast<const v8*>(vp + p.tok_stride);
-        }
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) vreg[0][e] = vreg[1][e] = static_cast<T>(0.0f);
-      }
+      const auto vrs = page_rsrc(vpool, slot_id(ids, vslot), t0 + 16 * vslot);
+      vreg[set][0] = __builtin_bit_cast(v8, __builtin_amdgcn_raw_buffer_load_b128(vrs, (int)voff0, 0, 0));
+      vreg[set][1] = __builtin_bit_cast(v8, __builtin_amdgcn_raw_buffer_load_b128(vrs, (int)voff1, 0, 0));
       if (kVs) {
-        const float* vs = p.vscale + (int64_t)b * p.vs_bs;
-        fw0 = vkey < hi ? vs[vkey] : 0.0f;
-        fw1 = vkey + 1 < hi ? vs[vkey + 1] : 0.0f;
+        const int o = (t0 + vkey_off) * 4;
+        fw0[set] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(fw_rsrc, o, 0, 0));
+        fw1[set] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(fw1_rsrc, o, 0, 0));
       }
     }
-    if (kBias && tid < kPfKT) {
-      const int key = t0 + tid;
-      fb_r = key < hi ? p.bias[(int64_t)b * p.bias_bs + key] * kLog2e : 0.0f;
-    }
+    if (kBias)
+      fb_r[set] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(fb_rsrc, (t0 + (tid & 63)) * 4, 0, 0));
   };
   // V-fog: V rows are scaled by their fog weights here, rounded to T, as the
   // reference scales V before its product (v * fog_weights), so the
   // probabilities stay unscaled and the softmax sum can be taken from them.
-  auto store = [&](int stage) {
+  auto store = [&](int stage, int set) {
     T* kd = ks + stage * kKStage + 8 * kc;
 #pragma unroll
-    for (int r = 0; r < kKL; ++r) *reinterpret_cast<v8*>(kd + krow_lds(r) * kKRow) = kreg[r];
+    for (int r = 0; r < kKL; ++r) *reinterpret_cast<v8*>(kd + krow_lds(r) * kKRow) = kreg[set][r];
     if (vload) {
       uint32_t* vd = vts + stage * kVStage + 4 * ((kp >> 2) ^ (kc >> 1)) + (kp & 3);
 #pragma unroll
       for (int e = 0; e < 8; ++e)
-        vd[(8 * kc + e) * kVRowW] = kVs ? pack2<T>(to_f32(vreg[0][e]) * fw0, to_f32(vreg[1][e]) * fw1)
-                                        : bits16(vreg[0][e]) | (bits16(vreg[1][e]) << 16);
+        vd[(8 * kc + e) * kVRowW] = kVs ? pack2<T>(to_f32(vreg[set][0][e]) * fw0[set], to_f32(vreg[set][1][e]) * fw1[set])
+                                        : bits16(vreg[set][0][e]) | (bits16(vreg[set][1][e]) << 16);
     }
-    if (kBias && tid < kPfKT) fbs[stage * kPfKT + tid] = fb_r;
+    if (kBias && tid < kPfKT) fbs[stage * kPfKT + tid] = fb_r[set] * kLog2e;
   };
 
   // Slice i of n (n >= 8) of store(): V^T word i for i < 8, then the K rows
   // and the bias at slice n-1 -- spread over the PV MFMAs.  With no tile
-  // t+2 it rewrites a stage that no later tile reads.  (Moving the slices to
-  // the last PV steps, to give the tile's loads longer, measured slower.)
-  auto store_slice = [&](int stage, int i, int n) {
+  // t+2 it rewrites a stage that no later tile reads.
+  auto store_slice = [&](int stage, int i, int n, int set) {
     if (vload && i < 8) {
       uint32_t* vd = vts + stage * kVStage + 4 * ((kp >> 2) ^ (kc >> 1)) + (kp & 3);
-      vd[(8 * kc + i) * kVRowW] = kVs ? pack2<T>(to_f32(vreg[0][i]) * fw0, to_f32(vreg[1][i]) * fw1)
-                                      : bits16(vreg[0][i]) | (bits16(vreg[1][i]) << 16);
+      vd[(8 * kc + i) * kVRowW] = kVs ? pack2<T>(to_f32(vreg[set][0][i]) * fw0[set], to_f32(vreg[set][1][i]) * fw1[set])
+                                      : bits16(vreg[set][0][i]) | (bits16(vreg[set][1][i]) << 16);
     }
     if (i == n - 1) {
       T* kd = ks + stage * kKStage + 8 * kc;
 #pragma unroll
-      for (int r = 0; r < kKL; ++r) *reinterpret_cast<v8*>(kd + krow_lds(r) * kKRow) = kreg[r];
-      if (kBias && tid < kPfKT) fbs[stage * kPfKT + tid] = fb_r;
+      for (int r = 0; r < kKL; ++r) *reinterpret_cast<v8*>(kd + krow_lds(r) * kKRow) = kreg[set][r];
+      if (kBias && tid < kPfKT) fbs[stage * kPfKT + tid] = fb_r[set] * kLog2e;
     }
   };
   // S^T of the tile in a stage: lane (col, half) reads K row 32kb + col.
@@ -429,25 +433,26 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
     ti_hi = dhi <= 0 ? 0 : dhi / kPfKT;
   }
 
-  i32x4 ids_a, ids_b;  // page ids of tiles t+2 and t+3
-  int pm0 = 0, pm1 = 0;    // valid-page masks of tiles t and t+1
+  i32x4 ids_a, ids_b;            // page ids of tiles t+3 and t+4
+  int pm0 = 0, pm1 = 0, pm2 = 0;  // valid-page masks of tiles t, t+1 and t+2
   f32x16 s_a[2], s_b[2];
   // One tile: sc holds its scores, sn receives the next tile's.  The next
   // tile's S^T MFMAs do not depend on this tile's softmax, so they share one
   // scheduling region with its exponentials and are interleaved with them:
   // the wave keeps the matrix pipe busy while its VALU works (and the other
   // wave of the SIMD fills what is left of either).
-  auto step = [&](int t, f32x16 (&sc)[2], f32x16 (&sn)[2]) {
+  // set: the register set receiving tile t+3 (= (t+1) & 1); the other one
+  // holds tile t+2, stored to its stage in this iteration.
+  auto step = [&](int t, f32x16 (&sc)[2], f32x16 (&sn)[2], int set) {
     const int t0 = t_begin + t * kPfKT;
     const int st_cur = t & (kPfStages - 1);
     const int st_nxt = (t + 1) & (kPfStages - 1);
     const int st_new = (t + 2) & (kPfStages - 1);
-    const bool more = t + 2 < n_tiles;
-    // Tile t+2's global loads go out first and land during this tile's work.
-    const int pm2 = valid_mask(ids_a);
-    if (more) issue(t + 2, ids_a, pm2);
+    // Tile t+3's global loads (none past the last tile: its ids are -1).
+    const int pm3 = valid_mask(ids_a);
+    issue(t + 3, ids_a, set);
     ids_a = ids_b;
-    ids_b = fetch_ids(t + 4);
+    ids_b = fetch_ids(t + 5);
 
     const bool interior = pm0 == 0xF && t >= ti_lo && t < ti_hi;
     const float* fbt = fbs + st_cur * kPfKT + 8 * half;
@@ -543,7 +548,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
 #pragma unroll
         for (int j = 0; j < kPairsPer; ++j) exp_pair(i * kPairsPer + j);
       } else {
-        store_slice(st_new, i - kQ, kPV);
+        store_slice(st_new, i - kQ, kPV, set ^ 1);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -551,19 +556,21 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
     m_run = mnew;
     pm0 = pm1;
     pm1 = pm2;
+    pm2 = pm3;
     __syncthreads();
   };
   if (n_tiles > 0) {
-    const i32x4 ids0 = fetch_ids(0);
-    ids_a = fetch_ids(1);
+    const i32x4 ids0 = fetch_ids(0), ids1 = fetch_ids(1), ids2 = fetch_ids(2);
     pm0 = valid_mask(ids0);
-    issue(0, ids0, pm0);
-    store(0);
-    pm1 = valid_mask(ids_a);
-    issue(1, ids_a, pm1);
-    store(1);
-    ids_a = fetch_ids(2);
-    ids_b = fetch_ids(3);
+    pm1 = valid_mask(ids1);
+    pm2 = valid_mask(ids2);
+    issue(0, ids0, 0);
+    store(0, 0);
+    issue(1, ids1, 1);
+    store(1, 1);
+    issue(2, ids2, 0);
+    ids_a = fetch_ids(3);
+    ids_b = fetch_ids(4);
     __syncthreads();
     qk(0, s_a);
     // Unrolled by two so the score buffers alternate instead of being copied.
@@ -571,8 +578,8 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
     // here and not in every iteration, where it would also wait for the
     // tile loads just issued.)
     for (int t = 0; t < n_tiles; t += 2) {
-      step(t, s_a, s_b);
-      if (t + 1 < n_tiles) step(t + 1, s_b, s_a);
+      step(t, s_a, s_b, 1);
+      if (t + 1 < n_tiles) step(t + 1, s_b, s_a, 0);
     }
   }
 
