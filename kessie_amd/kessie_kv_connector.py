@@ -201,6 +201,24 @@ _KESSIE_STORE: Optional[KeSSieCPUKVStore] = None
 _KESSIE_STORE_LOCK = threading.Lock()
 
 
+_HASH_TOKENS = None
+
+
+def recall_query_text(token_ids: List[int]) -> str:
+    """The semantic-search query for a prompt (kessie_kv_connector.py:335-344):
+    the md5 of the bytes of its last 128 token ids when transformers is
+    importable, of its last 64 otherwise.  The reference's ``bytes()`` raises
+    for an id above 255 (and the scheduler call with it); here such an id
+    contributes its low byte, so large vocabularies still get a query."""
+    global _HASH_TOKENS
+    if _HASH_TOKENS is None:
+        import importlib.util
+
+        _HASH_TOKENS = 128 if importlib.util.find_spec("transformers") is not None else 64
+    tail = token_ids[-_HASH_TOKENS:]
+    return f"tokens:{hashlib.md5(bytes(t & 0xFF for t in tail)).hexdigest()}"
+
+
 def get_kessie_store(max_cpu_bytes: int = 0) -> KeSSieCPUKVStore:
     """The process-wide store (created on first use)."""
     global _KESSIE_STORE
@@ -255,9 +273,14 @@ class KeSSieKVConnector(KVConnectorBase_v1):
     loads semantically recalled blocks back into the request's cache blocks
     (kessie_kv_connector.py:280-515).
 
-    kv_connector_extra_config keys: ``max_cpu_gb`` (default 64) and
+    kv_connector_extra_config keys: ``max_cpu_gb`` (default 64),
     ``rope_theta`` (default None: recalled K is copied unchanged; a value
-    re-rotates K from its original positions to its new ones while loading).
+    re-rotates K from its original positions to its new ones while loading)
+    and ``save_blocks``: ``"written"`` (default) saves the blocks this step's
+    slot_mapping touched; ``"all"`` re-saves every block of every sequence
+    each step, as the reference does (kessie_kv_connector.py:459-483), which
+    refreshes every block's timestamp and so reproduces its eviction order
+    under ``max_cpu_gb`` at the cost of copying the whole context per step.
     """
 
     def __init__(self, *args, **kwargs):
@@ -273,6 +296,10 @@ class KeSSieKVConnector(KVConnectorBase_v1):
         max_gb = float(extra.get("max_cpu_gb", 64))
         self.store = get_kessie_store(max_cpu_bytes=int(max_gb * 1073741824))
         self.rope_theta = extra.get("rope_theta")
+        mode = extra.get("save_blocks", "written")
+        if mode not in ("written", "all"):
+            raise ValueError(f"save_blocks must be 'written' or 'all', not {mode!r}")
+        self._save_all = mode == "all"
         self._kv_caches = []
         self._layer_names = []
         self._block_size = 16
@@ -306,9 +333,7 @@ class KeSSieKVConnector(KVConnectorBase_v1):
         with _RECALL_LOCK:
             if req_id in _RECALL_STATES:
                 return _RECALL_STATES[req_id].num_recalled_tokens
-        query_tokens = token_ids[-128:]
-        query_text = f"tokens:{hashlib.md5(bytes(t & 0xFF for t in query_tokens)).hexdigest()}"
-        results = self.store.semantic_search(query_text, top_k=3, exclude_positions=set())
+        results = self.store.semantic_search(recall_query_text(token_ids), top_k=3, exclude_positions=set())
         recalled, total = [], 0
         for pos_start, pos_end, sim in results:
             if sim < 0.3:
@@ -426,8 +451,8 @@ class KeSSieKVConnector(KVConnectorBase_v1):
 
     # -- worker side: save ------------------------------------------------------------
     def save_kv_layer(self, layer_name: str, kv_layer, attn_metadata, **kwargs):
-        """Copy the layer's blocks written this step (the blocks its
-        slot_mapping touches) to the CPU store: page gathers into a device
+        """Copy the layer's blocks of this step's save plan (by default those
+        its slot_mapping touches) to the CPU store: page gathers into a device
         staging buffer, then one async D2H copy into pinned memory."""
         from . import ops
 
@@ -465,10 +490,12 @@ class KeSSieKVConnector(KVConnectorBase_v1):
         self._pending_saves.append((ev, entries))
 
     def _save_plan(self, meta):
-        """[(block_id, position_start, tokens)] of the blocks written this step,
+        """[(block_id, position_start, tokens)] of the blocks to save this step
+        (those written this step, or every block with ``save_blocks="all"``),
         computed once per step and metadata object (all layers of the step
         share it; a runner that refills one metadata object in place is seen
-        again on the next step, which start_load_kv counts)."""
+        again on the next step, which start_load_kv counts).  Table entries
+        below zero (padding) are skipped."""
         if meta is None:
             return []
         key = (self._step, id(meta))
@@ -485,7 +512,7 @@ class KeSSieKVConnector(KVConnectorBase_v1):
             tables = block_tables.cpu() if isinstance(block_tables, torch.Tensor) else torch.tensor(block_tables)
             lens = seq_lens.tolist() if hasattr(seq_lens, "tolist") else list(seq_lens)
             touched = None
-            if slots is not None:
+            if slots is not None and not self._save_all:
                 sl = slots.cpu() if isinstance(slots, torch.Tensor) else torch.tensor(slots)
                 touched = set((sl[sl >= 0] // p).tolist())
             for si in range(min(len(lens), tables.shape[0])):

@@ -1,4 +1,5 @@
-"""CPU KV store bookkeeping oracle (test infrastructure only).
+"""CPU KV store bookkeeping oracle (test infrastructure only), and the
+reference connector's save plan and recall query.
 
 Restates KeSSieCPUKVStore.save_block / _evict_oldest
 (kessie_kv_connector.py:91-139, 203-215) as the reference does it: blocks in
@@ -40,3 +41,29 @@ class StoreModel:
         if oldest in keys:
             keys.remove(oldest)
         self.evicted.append(oldest)
+
+
+def reference_save_plan(block_tables, seq_lens, block_size: int):
+    """[(block_id, position_start, tokens)] in the order the reference's
+    save_kv_layer saves them (kessie_kv_connector.py:459-483): every block of
+    every sequence, sequence by sequence, ceil(seq_len / block_size) blocks
+    each, the last one partial."""
+    plan = []
+    n_rows = len(block_tables)
+    for si in range(min(len(seq_lens), n_rows)):
+        seq_len = int(seq_lens[si])
+        for b in range((seq_len + block_size - 1) // block_size):
+            pos = b * block_size
+            plan.append((int(block_tables[si][b]), pos, min(block_size, seq_len - pos)))
+    return plan
+
+
+def reference_query_text(token_ids, transformers_importable: bool = True) -> str:
+    """The reference's semantic-search query (kessie_kv_connector.py:335-344):
+    md5 over bytes() of the last 128 token ids when its transformers import
+    succeeds, of the last 64 otherwise; bytes() raises ValueError for an id
+    outside 0..255."""
+    import hashlib
+
+    tail = token_ids[-128:] if transformers_importable else token_ids[-64:]
+    return f"tokens:{hashlib.md5(bytes(tail)).hexdigest()}"

@@ -194,6 +194,75 @@ def test_connector_save_plan_follows_metadata_refilled_in_place():
     assert conn._save_plan(meta) == [(3, 32, 9)]
 
 
+def test_connector_save_all_blocks_matches_the_reference_plan():
+    """save_blocks="all" saves what the reference's save_kv_layer saves, in
+    its order: every block of every sequence, each step."""
+    from kessie_amd import kessie_kv_connector as kc
+    from oracle.store import reference_save_plan
+
+    class Meta:
+        block_table = torch.tensor([[5, 2, 9, 0], [7, 1, 0, 0], [3, 4, 6, 8]], dtype=torch.int32)
+        seq_lens = torch.tensor([40, 20, 64], dtype=torch.int32)
+        slot_mapping = torch.tensor([9 * 16 + 7, 1 * 16 + 3, 8 * 16 + 15], dtype=torch.int64)
+
+    conn = kc.KeSSieKVConnector(kv_connector_extra_config={"save_blocks": "all"})
+    meta = Meta()
+    want = reference_save_plan(Meta.block_table.tolist(), Meta.seq_lens.tolist(), 16)
+    assert want == [(5, 0, 16), (2, 16, 16), (9, 32, 8), (7, 0, 16), (1, 16, 4),
+                    (3, 0, 16), (4, 16, 16), (6, 32, 16), (8, 48, 16)]
+    assert conn._save_plan(meta) == want
+    # the default saves only the written blocks, in the same order
+    assert kc.KeSSieKVConnector()._save_plan(meta) == [(9, 32, 8), (1, 16, 4), (8, 48, 16)]
+    with pytest.raises(ValueError):
+        kc.KeSSieKVConnector(kv_connector_extra_config={"save_blocks": "some"})
+
+
+def test_connector_save_all_blocks_reproduces_the_reference_eviction_order():
+    """Under a byte budget, saving the reference's plan each step (every
+    block re-saved, so every timestamp refreshed) leaves the store holding
+    what the reference's store holds after every step."""
+    from kessie_amd import kessie_kv_connector as kc
+    from oracle.store import StoreModel, reference_save_plan
+
+    tables = [[5, 2, 9, 0], [7, 1, 0, 0]]
+    lens_by_step = [[40, 20], [41, 20], [42, 21]]
+    nbytes = 64
+    budget = 5 * nbytes
+    store = kc.KeSSieCPUKVStore(max_cpu_bytes=budget)
+    model = StoreModel(max_cpu_bytes=budget)
+    ts = 0.0
+    for lens in lens_by_step:
+        for bid, pos, tok in reference_save_plan(tables, lens, 16):
+            ts += 1.0
+            store._insert("layer.0", bid, torch.zeros(nbytes, dtype=torch.uint8), [], pos, timestamp=ts)
+            model.save(("layer.0", bid), nbytes, pos, ts)
+        assert sorted(store._blocks) == sorted(model.blocks)
+        assert store.total_bytes == model.total_bytes
+    assert model.evicted  # the budget was exceeded along the way
+
+
+def test_recall_query_text_matches_the_reference_for_byte_token_ids(monkeypatch):
+    """The semantic-search query equals the reference's for every prompt whose
+    token ids fit in a byte (the only prompts the reference handles); above
+    255 the reference's bytes() raises and this one takes the low byte."""
+    import random
+
+    from kessie_amd import kessie_kv_connector as kc
+    from oracle.store import reference_query_text
+
+    rng = random.Random(3)
+    for n in (1, 63, 64, 65, 127, 128, 129, 500):
+        ids = [rng.randrange(256) for _ in range(n)]
+        for importable in (True, False):
+            monkeypatch.setattr(kc, "_HASH_TOKENS", 128 if importable else 64)
+            assert kc.recall_query_text(ids) == reference_query_text(ids, importable)
+    big = [300, 70000, 5]
+    with pytest.raises(ValueError):
+        reference_query_text(big)
+    monkeypatch.setattr(kc, "_HASH_TOKENS", 128)
+    assert kc.recall_query_text(big) == reference_query_text([t & 0xFF for t in big])
+
+
 def test_attention_split_follows_metadata_refilled_in_place():
     """The decode / prefill split is keyed by the content of
     query_start_loc_cpu, not by the metadata object."""
