@@ -325,6 +325,30 @@ def test_connector_save_and_recall(dev, monkeypatch, remap):
         assert torch.equal(kf[:, mask].cpu(), bf[:, mask].cpu())
 
 
+@pytest.mark.parametrize("mode", ["written", "all"])
+def test_connector_save_blocks_modes(dev, monkeypatch, mode):
+    """A step that wrote only the last block: the default mode saves that
+    block, save_blocks="all" every block of the sequence (the reference's
+    plan), each with the cache's bytes."""
+    from kessie_amd import kessie_kv_connector as kc
+
+    monkeypatch.setattr(kc, "_KESSIE_STORE", None)
+    conn = kc.KeSSieKVConnector(kv_connector_extra_config={"max_cpu_gb": 1, "save_blocks": mode})
+    cache = randn((2, 32, 16, 8, 128), torch.bfloat16, dev, 5)
+    conn.register_kv_caches({"L0": cache})
+    table = torch.tensor([[3, 7, 1]], dtype=torch.int32, device=dev)
+    meta = _Meta(table, torch.tensor([40], dtype=torch.int32, device=dev),
+                 torch.tensor([1 * 16 + 7], device=dev))
+    conn.save_kv_layer("L0", cache, meta)
+    conn.wait_for_save()
+    want = [(1, 32, 8)] if mode == "written" else [(3, 0, 16), (7, 16, 16), (1, 32, 8)]
+    assert sorted(k[1] for k in conn.store._blocks) == sorted(b for b, _, _ in want)
+    for bid, pos, tok in want:
+        blk = conn.store.get_blocks_for_positions(pos, pos + tok, "L0")
+        assert blk is not None and blk.block_id == bid
+        assert torch.equal(blk.kv_data, cache[:, bid, :tok].cpu())
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_fog_bias_rows_match_the_reference_vector_per_sequence(dev, dtype):
     """Row b of the batched producer equals, bit for bit, the reference's op
