@@ -435,7 +435,11 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
 
   i32x4 ids_a, ids_b;            // page ids of tiles t+3 and t+4
   int pm0 = 0, pm1 = 0, pm2 = 0;  // valid-page masks of tiles t, t+1 and t+2
-  f32x16 s_a[2], s_b[2];
+  // Scores in three 16-register buffers: a tile's two 32-key blocks in two of
+  // them, the next tile's second block built in the third while the first
+  // is still read, its first block then built in the first buffer once that
+  // buffer's exponentials are done (16 registers fewer than two full sets).
+  f32x16 sA, sB, sC;
   // One tile: sc holds its scores, sn receives the next tile's.  The next
   // tile's S^T MFMAs do not depend on this tile's softmax, so they share one
   // scheduling region with its exponentials and are interleaved with them:
@@ -443,7 +447,8 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
   // wave of the SIMD fills what is left of either).
   // set: the register set receiving tile t+3 (= (t+1) & 1); the other one
   // holds tile t+2, stored to its stage in this iteration.
-  auto step = [&](int t, f32x16 (&sc)[2], f32x16 (&sn)[2], int set) {
+  auto step = [&](int t, f32x16& c0, f32x16& c1, f32x16& x, int set) {
+    auto sc = [&](int kb) -> f32x16& { return kb ? c1 : c0; };
     const int t0 = t_begin + t * kPfKT;
     const int st_cur = t & (kPfStages - 1);
     const int st_nxt = (t + 1) & (kPfStages - 1);
@@ -474,22 +479,22 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
         for (int v = 0; v < 16; ++v) {
           const int kl = 32 * kb + 16 * (v >> 3) + (v & 7);  // key offset minus 8 * half
           const bool ok = ((uint32_t)(kl - off) < len) & (((pm0 >> (2 * kb + (v >> 3))) & 1) != 0);
-          float y = kBias ? fmaf(sc[kb][v], c2, fbt[32 * kb + 16 * (v >> 3) + (v & 7)]) : sc[kb][v];
-          sc[kb][v] = ok ? y : kNegInf;
+          float y = kBias ? fmaf(sc(kb)[v], c2, fbt[32 * kb + 16 * (v >> 3) + (v & 7)]) : sc(kb)[v];
+          sc(kb)[v] = ok ? y : kNegInf;
         }
     } else if (kBias) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) sc[kb][v] = fmaf(sc[kb][v], c2, fbt[32 * kb + 16 * (v >> 3) + (v & 7)]);
+        for (int v = 0; v < 16; ++v) sc(kb)[v] = fmaf(sc(kb)[v], c2, fbt[32 * kb + 16 * (v >> 3) + (v & 7)]);
     }
     float ma = kNegInf, mb = kNegInf;  // two chains of max3
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int v = 0; v < 16; v += 4) {
-        ma = max3(ma, sc[kb][v], sc[kb][v + 1]);
-        mb = max3(mb, sc[kb][v + 2], sc[kb][v + 3]);
+        ma = max3(ma, sc(kb)[v], sc(kb)[v + 1]);
+        mb = max3(mb, sc(kb)[v + 2], sc(kb)[v + 3]);
       }
     float mloc = max_xor32(fmaxf(ma, mb));
     if (!kBias) mloc *= c2;  // without a bias, y = x * c2 and c2 > 0
@@ -514,7 +519,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
     const T* kb0 = kread + st_nxt * kKStage;
     const uint32_t* vr = vread + st_cur * kVStage;
     auto op_read = [&](int i) {
-      if (i < kQ) return *reinterpret_cast<const v8*>(kb0 + 32 * (i & 1) * kKRow + 16 * (i >> 1));
+      if (i < kQ) return *reinterpret_cast<const v8*>(kb0 + 32 * (i < kDS ? 1 : 0) * kKRow + 16 * (i % kDS));
       const int s = (i - kQ) / kDB, db = (i - kQ) % kDB;
       return *reinterpret_cast<const v8*>(vr + 32 * db * kVRowW + 8 * (s ^ db));
     };
@@ -522,7 +527,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
     u32x4 pb[4];                   // p as the PV B operand, two keys per dword
     auto exp_pair = [&](int j) {   // keys 2j, 2j+1 of this lane's 32
       const int kb = j >> 3, v = 2 * (j & 7);
-      const float y0 = sc[kb][v], y1 = sc[kb][v + 1];
+      const float y0 = sc(kb)[v], y1 = sc(kb)[v + 1];
       const float p0 = __builtin_amdgcn_exp2f(kBias ? y0 - muse : fmaf(y0, c2, -muse));
       const float p1 = __builtin_amdgcn_exp2f(kBias ? y1 - muse : fmaf(y1, c2, -muse));
       const uint32_t w = pack2<T>(p0, p1);
@@ -538,7 +543,12 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
 #pragma unroll
     for (int i = 0; i < kQ + kPV; ++i) {
       if (i < kQ) {
-        sn[i & 1] = Mma32<T>::mma(op[i % 3], qv[i >> 1], i < 2 ? f32x16{} : sn[i & 1]);
+        // The next tile's second block into x, then its first into c0
+        // (whose exponentials, the first eight pairs, are issued by then).
+        if (i < kDS)
+          x = Mma32<T>::mma(op[i % 3], qv[i], i == 0 ? f32x16{} : x);
+        else
+          c0 = Mma32<T>::mma(op[i % 3], qv[i - kDS], i == kDS ? f32x16{} : c0);
       } else {
         const int s = (i - kQ) / kDB, db = (i - kQ) % kDB;
         oacc[db] = Mma32<T>::mma(op[i % 3], __builtin_bit_cast(v8, pb[s]), oacc[db]);
@@ -572,14 +582,19 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
     ids_a = fetch_ids(3);
     ids_b = fetch_ids(4);
     __syncthreads();
-    qk(0, s_a);
+    {
+      f32x16 s0[2];
+      qk(0, s0);
+      sA = s0[0];
+      sB = s0[1];
+    }
     // Unrolled by two so the score buffers alternate instead of being copied.
     // (Inside the prologue's branch, so the wait for the query loads stays
     // here and not in every iteration, where it would also wait for the
     // tile loads just issued.)
     for (int t = 0; t < n_tiles; t += 2) {
-      step(t, s_a, s_b, 1);
-      if (t + 1 < n_tiles) step(t + 1, s_b, s_a, 0);
+      step(t, sA, sB, sC, 1);
+      if (t + 1 < n_tiles) step(t + 1, sA, sC, sB, 0);
     }
   }
 
