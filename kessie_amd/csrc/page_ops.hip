@@ -362,9 +362,20 @@ struct FusedArgs {
 constexpr int kFusedLdsWords = 2048 + 2 * kSelCap;
 static_assert(kFusedLdsWords >= kSelBins && kFusedLdsWords >= kFusedMaxRows, "fused LDS layout");
 
+// Buffer resources for the fused kernel's loads: dword-aligned raw buffers of
+// `bytes` bytes (loads past the end read 0).  Every range is below 2^31 bytes
+// (checked at the launch), so kOffNone, and any offset with bit 31 set, is
+// past all of them.
+constexpr int kRsrcWord3 = 0x00020000;
+constexpr int kOffNone = 0x7FFFFFF0;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t word_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, kRsrcWord3);
+}
+
 constexpr int kTileRegs = 4;  // key tiles per workgroup held in registers (4 keys per thread each)
 constexpr int kRowRegs = 4;   // 1,024-entry table-row chunks per workgroup held in registers
 
+template <int kTR>
 __global__ __launch_bounds__(kSelThreads) void sel_fused_kernel(FusedArgs a) {
   __shared__ uint32_t smem[kFusedLdsWords];
   __shared__ int sm[kSelWaves + 1];
@@ -418,18 +429,64 @@ __global__ __launch_bounds__(kSelThreads) void sel_fused_kernel(FusedArgs a) {
   };
 
   // P1: load this workgroup's keys (tiles and table entries) into registers;
-  // histogram the top 12 ordered-score bits of its valid pages.
-  uint32_t tk[kTileRegs][kSelPer];
+  // histogram the top 12 ordered-score bits of its valid pages.  The loads are
+  // straight-line code with no branch between them (a load under a condition
+  // turns the select on its value into a branch that waits for it): the
+  // tiles' flags and scores and the rows' lengths and entries in one round
+  // trip, then the flags and scores of the pages those entries name, which
+  // are only needed after the first grid barrier and stay in flight through
+  // the histogram.
+  uint32_t tk[kTR][kSelPer];
   uint32_t rk[kRowRegs];
   int rid[kRowRegs];
+  float rsc[kRowRegs];
+  int rv[kRowRegs];
+  {
+    // Range-limited buffer resources: a load past the end reads 0 instead of
+    // faulting, so absent tiles, rows and page ids need no clamp and no branch
+    // (an absent slot loads at kOffNone, past every range; a 0 flag is not 1,
+    // so its key is ~0).
+    const auto sc_rs = word_rsrc(a.scores, (uint32_t)a.n * 4u);
+    const auto va_rs = word_rsrc(a.valid, (uint32_t)a.n);
+    float tsc[kTR][kSelPer];
+    int tv[kTR][kSelPer];
 #pragma unroll
-  for (int u = 0; u < kTileRegs; ++u)
+    for (int u = 0; u < kTR; ++u)
 #pragma unroll
-    for (int j = 0; j < kSelPer; ++j) tk[u][j] = t_begin + u < t_end ? tile_key(t_begin + u, j) : 0xFFFFFFFFu;
+      for (int j = 0; j < kSelPer; ++j) {
+        const uint32_t i = (uint32_t)((t_begin + u) * kSelTile + tid * kSelPer + j);
+        const bool in = t_begin + u < t_end;
+        tsc[u][j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sc_rs, in ? (int)(i * 4u) : kOffNone, 0, 0));
+        tv[u][j] = __builtin_amdgcn_raw_buffer_load_b8(va_rs, in ? (int)i : kOffNone, 0, 0);
+      }
+    const auto ln_rs = word_rsrc(a.lens, tables ? (uint32_t)a.num_seqs * 4u : 0u);
+    int rlen[kRowRegs], rraw[kRowRegs];
 #pragma unroll
-  for (int u = 0; u < kRowRegs; ++u) {
-    rid[u] = -1;
-    rk[u] = u < my_chunks ? chunk_entry(u, &rid[u]) : 0xFFFFFFFFu;
+    for (int u = 0; u < kRowRegs; ++u) {
+      const int row = g + (u / cpr) * G;
+      const int j = (u % cpr) * kSelThreads + tid;
+      const bool in = u < my_chunks;
+      const auto tb_rs = word_rsrc(in ? a.tables + (int64_t)row * a.table_stride : nullptr,
+                                   in ? (uint32_t)a.table_stride * 4u : 0u);
+      rlen[u] = (int)__builtin_amdgcn_raw_buffer_load_b32(ln_rs, in ? row * 4 : kOffNone, 0, 0);
+      rraw[u] = (int)__builtin_amdgcn_raw_buffer_load_b32(tb_rs, in ? j * 4 : kOffNone, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < kRowRegs; ++u) {
+      const int j = (u % cpr) * kSelThreads + tid;
+      const int len = min(max(rlen[u], 0), a.table_stride);
+      rid[u] = u < my_chunks && j < len ? rraw[u] : -1;
+      // Out-of-range ids get bit 31 set: past every range (an offset select
+      // here is split into two loads of one register, which then wait on
+      // each other).
+      const uint32_t out = (uint32_t)rid[u] < (uint32_t)a.n ? 0u : 0x80000000u;
+      rsc[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sc_rs, (int)(((uint32_t)rid[u] * 4u) | out), 0, 0));
+      rv[u] = __builtin_amdgcn_raw_buffer_load_b8(va_rs, (int)((uint32_t)rid[u] | out), 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < kTR; ++u)
+#pragma unroll
+      for (int j = 0; j < kSelPer; ++j) tk[u][j] = tv[u][j] == 1 ? ordered_score(tsc[u][j]) : 0xFFFFFFFFu;
   }
   if (magic != kScratchMagic) {
     // The workspace was never initialised (kessie_page_workspace_init): touch
@@ -448,9 +505,9 @@ __global__ __launch_bounds__(kSelThreads) void sel_fused_kernel(FusedArgs a) {
     for (int j = 0; j < kSelPer; ++j) {
       uint32_t x = 0xFFFFFFFFu;
 #pragma unroll
-      for (int u = 0; u < kTileRegs; ++u)
+      for (int u = 0; u < kTR; ++u)
         if (t - t_begin == u) x = tk[u][j];
-      if (t - t_begin >= kTileRegs) x = tile_key(t, j);
+      if (t - t_begin >= kTR) x = tile_key(t, j);
       if (x != 0xFFFFFFFFu) {
         atomicAdd(&lhist[x >> 20], 1);
         ++c;
@@ -464,11 +521,23 @@ __global__ __launch_bounds__(kSelThreads) void sel_fused_kernel(FusedArgs a) {
     for (int e = tid; e < kSelBins; e += kSelThreads)
       if (lhist[e]) atomicAdd(&fs->hist[e], lhist[e]);
   grid_barrier(fs, (unsigned)G);
+#pragma unroll
+  for (int u = 0; u < kRowRegs; ++u)
+    rk[u] = rid[u] >= 0 && rid[u] < a.n && rv[u] == 1 ? ordered_score(rsc[u]) : 0xFFFFFFFFu;
 
-  // P2: k, the bin of rank k-1, and that bin's candidates.
-  for (int e = tid; e < kSelBins; e += kSelThreads)
-    lhist[e] = __hip_atomic_load(&fs->hist[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const int n_valid = __hip_atomic_load(&fs->n_valid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // P2: k, the bin of rank k-1, and that bin's candidates.  (The histogram and
+  // the valid count are read in one round trip: all loads, then the stores.)
+  int n_valid;
+  {
+    static_assert(kSelBins % kSelThreads == 0, "histogram bins per thread");
+    int hv[kSelBins / kSelThreads];
+#pragma unroll
+    for (int r = 0; r < kSelBins / kSelThreads; ++r)
+      hv[r] = __hip_atomic_load(&fs->hist[tid + r * kSelThreads], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    n_valid = __hip_atomic_load(&fs->n_valid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+    for (int r = 0; r < kSelBins / kSelThreads; ++r) lhist[tid + r * kSelThreads] = hv[r];
+  }
   long long kk;
   if (a.k_evict >= 0) {
     kk = min(a.k_evict, n_valid);
@@ -492,9 +561,9 @@ __global__ __launch_bounds__(kSelThreads) void sel_fused_kernel(FusedArgs a) {
       for (int j = 0; j < kSelPer; ++j) {
         uint32_t x = 0xFFFFFFFFu;
 #pragma unroll
-        for (int u = 0; u < kTileRegs; ++u)
+        for (int u = 0; u < kTR; ++u)
           if (t - t_begin == u) x = tk[u][j];
-        if (t - t_begin >= kTileRegs) x = tile_key(t, j);
+        if (t - t_begin >= kTR) x = tile_key(t, j);
         ks[j] = x;
         if (x != 0xFFFFFFFFu && (x >> 20) == top) {
           mbits |= 1 << j;
@@ -585,9 +654,9 @@ __global__ __launch_bounds__(kSelThreads) void sel_fused_kernel(FusedArgs a) {
   auto tile_key_at = [&](int t, int j) -> uint32_t {
     uint32_t x = 0xFFFFFFFFu;
 #pragma unroll
-    for (int u = 0; u < kTileRegs; ++u)
+    for (int u = 0; u < kTR; ++u)
       if (t - t_begin == u) x = tk[u][j];
-    if (t - t_begin >= kTileRegs) x = tile_key(t, j);
+    if (t - t_begin >= kTR) x = tile_key(t, j);
     return x;
   };
   // Table entry of chunk c: survives when it names a valid page that is not evicted.
@@ -1242,6 +1311,8 @@ int select_dispatch(const float* scores, int8_t* page_valid, int num_pages, int 
                     int32_t* gather_count, void* workspace, size_t workspace_bytes, hipStream_t s) {
   KESSIE_REQUIRE(num_pages >= 0, KESSIE_ERR_INVALID, "select evict: num_pages %d", num_pages);
   KESSIE_REQUIRE(scores && page_valid && evict_list && evict_count, KESSIE_ERR_INVALID, "select evict: null pointer");
+  KESSIE_REQUIRE(num_pages < (1 << 29) && table_stride < (1 << 29), KESSIE_ERR_UNSUPPORTED,
+                 "select evict: %d pages / %d table columns (at most 2^29 - 1 each)", num_pages, table_stride);
   KESSIE_REQUIRE(k_evict >= 0 || (evict_fraction >= 0.0f && evict_fraction <= 1.0f), KESSIE_ERR_INVALID,
                  "select evict: evict_fraction %g outside [0,1]", (double)evict_fraction);
   const int nws = max(num_pages, num_seqs);
@@ -1253,7 +1324,10 @@ int select_dispatch(const float* scores, int8_t* page_valid, int num_pages, int 
   FusedArgs a{scores,       page_valid, num_pages, k_evict,  evict_fraction, evict_list, evict_count,
               tables,       lens,       num_seqs,  table_stride, new_tables, new_lens,   gather_idx,
               gather_count, w.fs,       w.cand_s,  w.cand_i,   w.rows,       div_up(ntiles, G)};
-  hipLaunchKernelGGL(sel_fused_kernel, dim3(G), dim3(kSelThreads), 0, s, a);
+  if (a.tiles_per_wg == 1)
+    hipLaunchKernelGGL(sel_fused_kernel<1>, dim3(G), dim3(kSelThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL(sel_fused_kernel<kTileRegs>, dim3(G), dim3(kSelThreads), 0, s, a);
   return check_launch("select evict");
 }
 
