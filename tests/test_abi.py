@@ -125,6 +125,15 @@ def test_prefill_and_decode_argument_errors_without_gpu():
     st = lib.kessie_fog_decode_paged(fake, fake, 4096, 65536, 4096, 2048, 128, None, 4096, fake, None, 0,
                                      None, 0, fake, 1, 32, 8, 128, 16, 4096, 0, 0.088, bf16, None, 0, None)
     assert st == _lib.ERR_INVALID
+    # score eviction: every byte offset of its range-limited loads must stay below 2^31
+    st = lib.kessie_page_select_evict(fake, fake, 1 << 29, -1, 0.25, fake, fake, fake, 1 << 40, None)
+    assert st == _lib.ERR_UNSUPPORTED
+    other = C.c_void_p(1 << 21)  # new_tables must differ from tables
+    st = lib.kessie_page_evict_compact(fake, fake, 4096, -1, 0.25, fake, fake, fake, fake, 1, 1 << 29, other, fake,
+                                       fake, fake, fake, 1 << 40, None)
+    assert st == _lib.ERR_UNSUPPORTED
+    status, msg = _lib.last_error()
+    assert status == _lib.ERR_UNSUPPORTED and "2^29" in msg
 
 
 PROBES_HEADER = os.path.join(ROOT, "include", "kessie_probes.h")
