@@ -345,7 +345,7 @@ def bench_gather_evict(dev, reps=5, cpu=False):
         del pool_bytes
     return {
         "cpu_baseline": res_cpu,
-        "workload": "score evict 25% of 65,536 pages + compact 64x1024 tables (fused: 2 launches) + gather "
+        "workload": "score evict 25% of 65,536 pages + compact 64x1024 tables (fused: 1 launch) + gather "
                     "survivors (bf16 pages)",
         "pipeline_ms": round(tot, 4),
         "gather_kernel_ms": round(gat, 4),

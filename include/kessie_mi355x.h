@@ -326,9 +326,10 @@ int kessie_page_workspace_init(void* workspace, size_t workspace_bytes,
  * Deterministic: no order depends on atomics.  One launch whose workgroups
  * meet at bounded grid barriers (*evict_count reads -1 if the device could
  * not run them at once); the workspace must have been prepared by
- * kessie_page_workspace_init (-2 otherwise).  (The reference only has the
- * threshold predicate, kessie_kernels_v2.hip:393-407; this applies it with an
- * exact k-th-order-statistic threshold.) */
+ * kessie_page_workspace_init (-2 otherwise).  num_pages below 2^29 (else
+ * KESSIE_ERR_UNSUPPORTED).  (The reference only has the threshold predicate,
+ * kessie_kernels_v2.hip:393-407; this applies it with an exact
+ * k-th-order-statistic threshold.) */
 int kessie_page_select_evict(const float* scores, int8_t* page_valid,
                              int num_pages, int k_evict, float evict_fraction,
                              int32_t* evict_list, int32_t* evict_count,
@@ -349,10 +350,11 @@ int kessie_page_compact(const int32_t* tables, const int32_t* lens,
                         void* stream);
 
 /* kessie_page_select_evict followed by kessie_page_compact of the tables by
- * the post-eviction valid flags, in two launches instead of two calls' worth:
+ * the post-eviction valid flags, in one launch instead of two calls' worth:
  * every output equals what those two calls produce (evict_list / evict_count /
  * page_valid as select_evict; new_tables / new_lens / gather_idx /
- * gather_count as compact).  num_seqs <= 8192 (else KESSIE_ERR_UNSUPPORTED).
+ * gather_count as compact).  num_seqs <= 8192, num_pages and table_stride
+ * below 2^29 (else KESSIE_ERR_UNSUPPORTED).
  * Workspace: kessie_page_workspace_bytes(max(num_pages, num_seqs)), prepared
  * by kessie_page_workspace_init (else both counts read -2).  The launch's
  * workgroups (at most 64) wait for each other at bounded grid barriers; if

@@ -521,7 +521,7 @@ def page_evict_compact(scores: torch.Tensor, page_valid: torch.Tensor, tables: t
                        new_lens: Optional[torch.Tensor] = None, gather_idx: Optional[torch.Tensor] = None,
                        gather_count: Optional[torch.Tensor] = None, stream=None):
     """page_select_evict then page_compact by the post-eviction flags, fused
-    into two launches.  Returns (evict_list, evict_count, new_tables, new_lens,
+    into one launch.  Returns (evict_list, evict_count, new_tables, new_lens,
     gather_idx, gather_count), each equal to the two calls' outputs."""
     n = page_valid.numel()
     dev = page_valid.device

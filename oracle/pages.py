@@ -106,7 +106,7 @@ def compact(tables: np.ndarray, lens: np.ndarray, valid: np.ndarray):
     new_lens = np.zeros(s, dtype=np.int32)
     gather = []
     for i in range(s):
-        row = tables[i, : lens[i]]
+        row = tables[i, : min(max(int(lens[i]), 0), width)]  # a length outside [0, width] is clamped
         ok = (row >= 0) & (row < num_pages)
         ok[ok] = valid[row[ok]] == 1
         keep = row[ok]

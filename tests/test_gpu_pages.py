@@ -268,6 +268,44 @@ def test_evict_compact_matches_oracle(dev, n, s, w, frac, k, distinct):
     assert m == len(rg) and np.array_equal(_np(gi[:m]), rg)
 
 
+@pytest.mark.parametrize("n,s,w", [(4099, 3, 1500), (1, 2, 4), (4096, 5, 1024)])
+def test_evict_compact_edge_values(dev, n, s, w):
+    """Edge values through the fused call, against the oracle bit for bit:
+    lengths below 0 and past the row width (clamped), page ids at the int32
+    limits and just outside [0, n), valid flags other than 0 and 1 (only 1 is
+    valid), a page count one past a 4,096-key tile or a single page, and rows
+    wider than 1,024 entries (more than one chunk per row)."""
+    from kessie_amd import ops
+
+    g = torch.Generator().manual_seed(n * 7 + w)
+    scores = torch.rand(n, generator=g)
+    valid = torch.randint(-1, 3, (n,), generator=g, dtype=torch.int8)
+    valid[: max(1, n // 2)] = 1
+    tables = torch.randint(0, n, (s, w), generator=g, dtype=torch.int32)
+    specials = torch.tensor([-(2 ** 31), 2 ** 31 - 1, -1, n, n - 1, 0, 2 ** 30 + 1, -(2 ** 30)], dtype=torch.int32)
+    for r in range(s):
+        pos = torch.randint(0, w, (min(w, 8),), generator=g)
+        tables[r, pos] = specials[: len(pos)]
+    lens = torch.tensor([(-5, w + 7, w // 2, w, 0)[r % 5] for r in range(s)], dtype=torch.int32)
+    rv, rlist = P.select_evict(scores.numpy(), valid.numpy(), -1, 0.25)
+    rt, rl, rg = P.compact(tables.numpy(), lens.numpy(), rv)
+    dv = valid.to(dev)
+    lst, cnt, nt, nl, gi, gc = ops.page_evict_compact(scores.to(dev), dv, tables.to(dev), lens.to(dev), -1, 0.25)
+    torch.cuda.synchronize()
+    c = int(cnt.item())
+    assert c == len(rlist) and np.array_equal(_np(lst[:c]), rlist)
+    assert np.array_equal(_np(dv), rv)
+    assert np.array_equal(_np(nt), rt) and np.array_equal(_np(nl), rl)
+    m = int(gc.item())
+    assert m == len(rg) and np.array_equal(_np(gi[:m]), rg)
+    # the standalone compaction (look-back kernel) on the post-eviction flags
+    nt2, nl2, gi2, gc2 = ops.page_compact(tables.to(dev), lens.to(dev), dv)
+    torch.cuda.synchronize()
+    assert np.array_equal(_np(nt2), rt) and np.array_equal(_np(nl2), rl)
+    m2 = int(gc2.item())
+    assert m2 == len(rg) and np.array_equal(_np(gi2[:m2]), rg)
+
+
 def test_evict_compact_rejects_too_many_rows(dev):
     from kessie_amd import _lib, ops
 
