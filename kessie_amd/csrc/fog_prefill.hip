@@ -115,7 +115,12 @@ __device__ __forceinline__ uint32_t pack2<f16_t>(float a, float b) {
 
 // max(a, b, c) in one instruction.  fmaxf on MFMA results first quiets each
 // input (one extra v_max per score); scores hold no signalling NaN, so the
-// raw instruction gives the same result.
+// raw instruction gives the same result.  Being inline assembly, it gets no
+// wait states from the compiler's MFMA hazard checks: a VALU read of a 32x32
+// MFMA's result needs 18 (ISA), and every use here reads scores whose MFMAs
+// were issued in the previous iteration, hundreds of instructions earlier.
+// (Reading them right after their MFMAs returned stale registers, seen as
+// results that changed from run to run.)
 __device__ __forceinline__ float max3(float a, float b, float c) {
   float r;
   asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
