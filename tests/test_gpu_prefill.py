@@ -146,8 +146,8 @@ def test_prefill_varlen_matches_per_sequence(dev, fog, window, monkeypatch):
     """One varlen launch over sequences with different chunk lengths (incl. a
     one-token chunk and an empty one) equals the per-sequence launches bit for
     bit, and the oracle within tolerance; the query_start_loc slice may start
-    at a non-zero offset.  The per-sequence launches are held to one key split
-    (the varlen launch never splits), which makes the summation orders equal."""
+    at a non-zero offset.  Both forms are held to one key split
+    (KESSIE_PREFILL_SPLITS=1), which makes the summation orders equal."""
     from kessie_amd import ops
 
     monkeypatch.setenv("KESSIE_PREFILL_SPLITS", "1")
