@@ -260,6 +260,13 @@ def test_prefill_varlen_split_k(dev, chunks, ctxs, force, monkeypatch):
             ref = paged_prefill_ref(qq, pool.cpu(), table[i:i + 1].cpu(), lens[i:i + 1].cpu(), vs[i].cpu(), None, 0,
                                     rows=rows)
         _check(out[s:s + c][rows.long()].unsqueeze(0), ref, torch.bfloat16)
+        if force:
+            # at an equal (forced) split count the per-sequence launch sums the
+            # same partials in the same order
+            one = ops.fog_prefill(q[s:s + c].unsqueeze(0).contiguous(), pool, table[i:i + 1], lens[i:i + 1], mx,
+                                  fog_vscale=vs[i:i + 1])
+            torch.cuda.synchronize()
+            assert torch.equal(out[s:s + c], one[0]), f"sequence {i}"
 
 
 def test_prefill_varlen_many_sequences(dev):
