@@ -160,8 +160,9 @@ def _cpu_threads():
 
 
 def cpu_decode_baseline(s, budget_s=12.0):
-    """The CPU oracle (oracle.attention.paged_decode_blockwise) on the GPU box's
-    host cores: whole sequences of the same workload until ~budget_s seconds."""
+    """The CPU oracle (oracle.attention.paged_decode_blockwise) on the host
+    cores of the machine the bench runs on: whole sequences of the same
+    workload until ~budget_s seconds."""
     import torch
 
     from oracle.attention import paged_decode_blockwise

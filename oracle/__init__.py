@@ -14,8 +14,9 @@ the reference file:line it follows:
                     and the score-eviction / compaction rule built on them
 
 Who may use it: ``tests/``, ``__graft_entry__.smoke()`` and the
-``cpu_baseline`` leg of ``bench.py`` -- and only as the checker (or the timed
-CPU baseline), never as the thing measured or shipped.  The product package
+``cpu_baseline`` leg of ``bench.py`` -- and only as the reference the results
+are compared with (or the timed CPU baseline), never as the thing measured or
+shipped.  The product package
 ``kessie_amd`` never imports it.
 
 How it is pinned (tests/test_oracle_*.py): the reference ships no golden

@@ -1,6 +1,6 @@
 """GPU parity: paged fog decode vs the CPU oracle.
 
-Tolerances (north star): bf16/fp16 outputs with fp32 accumulation
+Tolerances (the path's parity requirement): bf16/fp16 outputs with fp32 accumulation
 |gpu - ref| <= 2e-2 + 1e-2*|ref|; fp32 configs 1e-5 (atol and rtol).
 """
 import math
