@@ -52,6 +52,7 @@ struct Params {
   int num_splits;
   int direct_out;      // 1: the main kernel writes the normalised output
   int launch_combine;  // host side: follow the main kernel with the combine
+  int balanced;        // decode split partials: units assigned by pages (decode_seq_of_unit)
   float* ws_o;  // [B*C*Hq][S][D]
   float* ws_m;  // [B*C*Hq][S]
   float* ws_l;  // [B*C*Hq][S]

@@ -24,6 +24,7 @@
 //                 MFMA kernels do not take (fp32 prefill, other head_dims,
 //                 page sizes and GQA ratios).
 //   combine       merges the per-split (m, l, o) partials of either kernel.
+#include <climits>
 #include <cmath>
 #include <cstdlib>
 
@@ -227,6 +228,123 @@ __global__ __launch_bounds__(kGenThreads) void attn_generic_kernel(Params p) {
 constexpr int kCombineThreads = 256;
 constexpr int kMaxSplits = 512;
 
+// ---------------------------------------------------------------------------
+// Balanced decode splits.  A decode launch has U = S * B workgroups per group
+// of kv heads; with every sequence split S ways, a batch of one long context
+// and many short ones leaves most of them idle while the long one streams.
+// Instead the U units go to the batch's pages: P, the pages per unit, is the
+// smallest value (at least ceil(max pages / kMaxSplits), so that no row has
+// more partials than the combine takes) with sum_b ceil(pages_b / P) <= U,
+// and sequence b gets ceil(pages_b / P) consecutive units.  A uniform batch
+// gets S units per sequence, the page ranges of the plain split.  Unit u's
+// partial of head h sits at slot u * Hq + h.  Each function is evaluated by a
+// whole wave and returns the same value in every lane.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int wave_sum_i(int v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ int wave_max_i(int v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = max(v, __shfl_xor(v, o, 64));
+  return v;
+}
+// Pages a decode over ctx tokens reads (16-token pages): those of its window.
+__device__ __forceinline__ int decode_pages(const Params& p, int ctx) {
+  const int lo = p.window > 0 ? max(0, ctx - p.window) : 0;
+  return ((ctx + 15) >> 4) - (lo >> 4);
+}
+constexpr int kBalSeqs = 256;  // batches the balanced split takes: 4 lengths per lane, read once
+struct BatchPages {
+  int ctx[kBalSeqs / 64];  // length of sequence lane + 64 j (0 past the batch)
+  int pg[kBalSeqs / 64];   // its pages
+  // Length of sequence b (uniform b), from the registers.
+  __device__ int seq_len(int b) const {
+    int v = ctx[0];
+#pragma unroll
+    for (int j = 1; j < kBalSeqs / 64; ++j)
+      if ((b >> 6) == j) v = ctx[j];
+    return __builtin_amdgcn_readlane(v, b & 63);
+  }
+};
+__device__ __forceinline__ BatchPages batch_pages(const Params& p) {
+  const int lane = threadIdx.x & 63;
+  BatchPages bp;
+#pragma unroll
+  for (int j = 0; j < kBalSeqs / 64; ++j) {
+    bp.ctx[j] = lane + 64 * j < p.B ? seq_ctx(p, lane + 64 * j) : 0;
+    bp.pg[j] = decode_pages(p, bp.ctx[j]);
+  }
+  return bp;
+}
+// P for S units per sequence of a B-sequence batch (U = S * B).
+__device__ int decode_unit_pages(const BatchPages& bp, int S, int B) {
+  const int lane = threadIdx.x & 63;
+  int mx = 0, mn = INT_MAX;
+#pragma unroll
+  for (int j = 0; j < kBalSeqs / 64; ++j)
+    if (lane + 64 * j < B) {
+      mx = max(mx, bp.pg[j]);
+      mn = min(mn, bp.pg[j]);
+    }
+  mx = wave_max_i(mx);
+  mn = -wave_max_i(-mn);
+  int lo = max(1, (mx + kMaxSplits - 1) / kMaxSplits), hi = max(lo, mx);  // P = mx fits: B <= U units
+  // Every sequence the same length: S units each, the plain split.
+  if (mn == mx) return max(lo, (mx + S - 1) / S);
+  const int U = S * B;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    int n = 0;
+#pragma unroll
+    for (int j = 0; j < kBalSeqs / 64; ++j)
+      if (64 * j < B) n += (bp.pg[j] + mid - 1) / mid;
+    if (wave_sum_i(n) <= U)
+      hi = mid;
+    else
+      lo = mid + 1;
+  }
+  return lo;
+}
+// The sequence and split of unit u; false when u is past the batch's units.
+__device__ bool decode_seq_of_unit(const BatchPages& bp, int P, int u, int* b_out, int* s_out) {
+  const int lane = threadIdx.x & 63;
+  int base = 0;
+#pragma unroll
+  for (int j = 0; j < kBalSeqs / 64; ++j) {
+    const int n = (bp.pg[j] + P - 1) / P;
+    int incl = n;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += y;
+    }
+    const int excl = incl - n;
+    const unsigned long long hit = __ballot(u >= base + excl && u < base + incl);
+    if (hit != 0) {
+      const int l = __ffsll((long long)hit) - 1;
+      *b_out = 64 * j + l;
+      *s_out = u - base - __shfl(excl, l, 64);
+      return true;
+    }
+    base += __shfl(incl, 63, 64);
+  }
+  return false;
+}
+// The first unit of sequence b and its number of units.
+__device__ void decode_units_of_seq(const BatchPages& bp, int P, int b, int* u0, int* n) {
+  const int lane = threadIdx.x & 63;
+  int before = 0, mine = 0;
+#pragma unroll
+  for (int j = 0; j < kBalSeqs / 64; ++j) {
+    const int c = lane + 64 * j, k = (bp.pg[j] + P - 1) / P;
+    before += c < b ? k : 0;
+    mine += c == b ? k : 0;
+  }
+  *u0 = wave_sum_i(before);
+  *n = wave_sum_i(mine);
+}
 // Workgroup (row, y) merges d in [y*D/Y, (y+1)*D/Y) of one row (Y =
 // gridDim.y, 1 unless rows are few).  With an even chunk its 256 lanes are
 // (split group, float2 column) pairs: each sums every groups-th split of its
@@ -252,18 +370,40 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(Params p) {
     b = 0;
   }
   const int tid = threadIdx.x, lane = tid & 63;
-  const float* m = p.ws_m + row * S;
-  const float* l = p.ws_l + row * S;
+  // The row's partials: S of them at row * S + s, or, with balanced decode
+  // splits, n_s at (u0 + s) * Hq + h (its sequence's units).
+  __shared__ int s_first, s_count;
+  int64_t first = row * S, stride = 1;
+  int n_s = S;
+  if (p.balanced) {
+    if (tid < 64) {
+      const BatchPages bp = batch_pages(p);
+      const int P = decode_unit_pages(bp, S, p.B);
+      int u0, n;
+      decode_units_of_seq(bp, P, b, &u0, &n);
+      if (tid == 0) {
+        s_first = u0;
+        s_count = n;
+      }
+    }
+    __syncthreads();
+    first = (int64_t)s_first * p.Hq + h;
+    stride = p.Hq;
+    n_s = s_count;
+  }
+  const float* m = p.ws_m + first;
+  const float* l = p.ws_l + first;
   if (tid < 64) {
     float mx = kNegInf;
-    for (int s = lane; s < S; s += 64) mx = fmaxf(mx, m[s]);
+    for (int s = lane; s < n_s; s += 64) mx = fmaxf(mx, m[s * stride]);
 #pragma unroll
     for (int w = 32; w >= 1; w >>= 1) mx = fmaxf(mx, __shfl_xor(mx, w, 64));
     float sum = 0.0f;
-    for (int s = lane; s < S; s += 64) {
-      const float e = (m[s] == kNegInf) ? 0.0f : expf(m[s] - mx);
+    for (int s = lane; s < n_s; s += 64) {
+      const float ms = m[s * stride];
+      const float e = (ms == kNegInf) ? 0.0f : expf(ms - mx);
       e_s[s] = e;
-      sum += e * l[s];
+      sum += e * l[s * stride];
     }
 #pragma unroll
     for (int w = 32; w >= 1; w >>= 1) sum += __shfl_xor(sum, w, 64);
@@ -273,16 +413,17 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(Params p) {
   const float il = inv_l;
   const int chunk = D / gridDim.y;
   const int d0 = blockIdx.y * chunk;
-  const float* o = p.ws_o + row * S * D + d0;
+  const float* o = p.ws_o + first * D + d0;
+  const int64_t ostride = stride * D;
   if ((chunk & 1) == 0 && kCombineThreads % (chunk / 2) == 0) {
     const int cols = chunk / 2;                // float2 columns
     const int groups = kCombineThreads / cols;
     const int col = tid % cols, grp = tid / cols;
     float ax = 0.0f, ay = 0.0f;
 #pragma unroll 4
-    for (int s = grp; s < S; s += groups) {
+    for (int s = grp; s < n_s; s += groups) {
       const float e = e_s[s];
-      const float2 v = *reinterpret_cast<const float2*>(o + (int64_t)s * D + 2 * col);
+      const float2 v = *reinterpret_cast<const float2*>(o + (int64_t)s * ostride + 2 * col);
       ax += e * v.x;
       ay += e * v.y;
     }
@@ -300,7 +441,7 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(Params p) {
   } else {
     for (int d = tid; d < chunk; d += kCombineThreads) {
       float acc = 0.0f;
-      for (int s = 0; s < S; ++s) acc += e_s[s] * o[(int64_t)s * D + d];
+      for (int s = 0; s < n_s; ++s) acc += e_s[s] * o[(int64_t)s * ostride + d];
       store_out<T>(p, b, i, h, d0 + d, acc * il);
     }
   }
@@ -393,17 +534,31 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) 
   if (g >= p.Hkv) return;  // no workgroup barriers below
   T* vtile = vtile_all[wave];
   T* qtile = qtile_all[wave];
-  const int b = blockIdx.y;
-  const int split = blockIdx.x;
   const int S = p.num_splits;
+  const int unit = blockIdx.y * S + blockIdx.x;  // balanced splits: this workgroup's unit
+  int b = blockIdx.y, split = blockIdx.x, per = 0;
+  int ctx;
+  if (p.balanced) {
+    const BatchPages bp = batch_pages(p);
+    per = decode_unit_pages(bp, S, p.B);
+    if (!decode_seq_of_unit(bp, per, unit, &b, &split)) return;  // past the batch's units: no partial to write
+    // Wave-uniform results, kept in scalar registers so that the page loop's
+    // bounds and page-table reads stay scalar (as vector loads they would
+    // queue behind the page prefetch).
+    per = __builtin_amdgcn_readfirstlane(per);
+    b = __builtin_amdgcn_readfirstlane(b);
+    split = __builtin_amdgcn_readfirstlane(split);
+    ctx = bp.seq_len(b);
+  } else {
+    ctx = seq_ctx(p, b);
+  }
   const int row = lane & 15;  // MFMA row / column index: token (K rows), head (scores), d (O^T)
   const int grp = lane >> 4;  // lane group: k-block slot, token quad
 
-  const int ctx = seq_ctx(p, b);
   const int lo = p.window > 0 ? max(0, ctx - p.window) : 0;
   const int pg_lo = lo >> 4;
   const int pg_hi = (ctx + 15) >> 4;
-  const int per = (pg_hi - pg_lo + S - 1) / S;
+  if (!p.balanced) per = (pg_hi - pg_lo + S - 1) / S;
   const int p0 = pg_lo + split * per;
   const int p1 = min(pg_hi, p0 + per);
 
@@ -573,13 +728,13 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) 
       *reinterpret_cast<vec4*>(dst + 16 * blk) = ov;
     }
   } else {
-    const int64_t r = row_id(p, b, 0, head);
-    float* dst = p.ws_o + (r * S + split) * 128 + 4 * grp;
+    const int64_t slot = p.balanced ? (int64_t)unit * p.Hq + head : row_id(p, b, 0, head) * S + split;
+    float* dst = p.ws_o + slot * 128 + 4 * grp;
 #pragma unroll
     for (int blk = 0; blk < 8; ++blk) *reinterpret_cast<f32x4*>(dst + 16 * blk) = oacc[blk];
     if (grp == 0) {
-      p.ws_m[r * S + split] = m_run;
-      p.ws_l[r * S + split] = l_run;
+      p.ws_m[slot] = m_run;
+      p.ws_l[slot] = l_run;
     }
   }
 }
@@ -610,17 +765,31 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) 
   const int g = blockIdx.z * W + wave;
   if (g >= p.Hkv) return;  // no workgroup barriers below
   float* vtile = vtile_all[wave];
-  const int b = blockIdx.y;
-  const int split = blockIdx.x;
   const int S = p.num_splits;
+  const int unit = blockIdx.y * S + blockIdx.x;  // balanced splits: this workgroup's unit
+  int b = blockIdx.y, split = blockIdx.x, per = 0;
+  int ctx;
+  if (p.balanced) {
+    const BatchPages bp = batch_pages(p);
+    per = decode_unit_pages(bp, S, p.B);
+    if (!decode_seq_of_unit(bp, per, unit, &b, &split)) return;  // past the batch's units: no partial to write
+    // Wave-uniform results, kept in scalar registers so that the page loop's
+    // bounds and page-table reads stay scalar (as vector loads they would
+    // queue behind the page prefetch).
+    per = __builtin_amdgcn_readfirstlane(per);
+    b = __builtin_amdgcn_readfirstlane(b);
+    split = __builtin_amdgcn_readfirstlane(split);
+    ctx = bp.seq_len(b);
+  } else {
+    ctx = seq_ctx(p, b);
+  }
   const int row = lane & 15;
   const int grp = lane >> 4;
 
-  const int ctx = seq_ctx(p, b);
   const int lo = p.window > 0 ? max(0, ctx - p.window) : 0;
   const int pg_lo = lo >> 4;
   const int pg_hi = (ctx + 15) >> 4;
-  const int per = (pg_hi - pg_lo + S - 1) / S;
+  if (!p.balanced) per = (pg_hi - pg_lo + S - 1) / S;
   const int p0 = pg_lo + split * per;
   const int p1 = min(pg_hi, p0 + per);
 
@@ -767,13 +936,13 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) 
 #pragma unroll
     for (int blk = 0; blk < 8; ++blk) *reinterpret_cast<f32x4*>(dst + 16 * blk) = oacc[blk] * il;
   } else {
-    const int64_t r = row_id(p, b, 0, head);
-    float* dst = p.ws_o + (r * S + split) * 128 + 4 * grp;
+    const int64_t slot = p.balanced ? (int64_t)unit * p.Hq + head : row_id(p, b, 0, head) * S + split;
+    float* dst = p.ws_o + slot * 128 + 4 * grp;
 #pragma unroll
     for (int blk = 0; blk < 8; ++blk) *reinterpret_cast<f32x4*>(dst + 16 * blk) = oacc[blk];
     if (grp == 0) {
-      p.ws_m[r * S + split] = m_run;
-      p.ws_l[r * S + split] = l_run;
+      p.ws_m[slot] = m_run;
+      p.ws_l[slot] = l_run;
     }
   }
 }
@@ -1063,6 +1232,9 @@ static int decode_entry(const void* q, const void* kv_pool, int num_pages, int64
   }
   hipStream_t s = as_stream(stream);
   if (decode_mfma_ok(p, dtype)) {
+    // Split partials merged here: assign the splits by pages across the batch
+    // (the partials-only form keeps the plain row * S + split layout).
+    p.balanced = (!partials_only && !p.direct_out && batch <= kBalSeqs) ? 1 : 0;
     if (dtype == KESSIE_DTYPE_F32) return run_decode_mfma_f32(p, s);
     return dtype == KESSIE_DTYPE_BF16 ? run_decode_mfma<bf16_t>(p, s) : run_decode_mfma<f16_t>(p, s);
   }
