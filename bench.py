@@ -204,10 +204,15 @@ def cpu_decode_baseline(s, budget_s=12.0):
 # ---------------------------------------------------------------------------
 # Secondary workloads
 # ---------------------------------------------------------------------------
-def bench_remap(dev, reps=20, sets=4, n_tok=65536, page_size=16, hkv=8, d=128, theta=500000.0, cpu=False):
-    """RoPE remap, bf16, 65,536 tokens in 16-token pages, 8 KV heads, D=128,
-    theta 5e5, only K rotated.  ``sets`` disjoint page sets rotate across reps
-    so the 256 MB MALL cannot serve the next rep."""
+def bench_remap(dev, reps=20, sets=4, n_tok=65536, page_size=16, hkv=8, d=128, theta=500000.0, cpu=False,
+                layout="native"):
+    """RoPE remap, bf16, 65,536 tokens, 8 KV heads, D=128, theta 5e5, only K
+    rotated.  ``layout``: "native" -- 16-token pages of interleaved K/V token
+    rows [pages][16][2][8][128] (K is the first half of every 4 KiB row);
+    "kv_first" -- 16-token K-only pages of vLLM's [2][blocks][16][8][128];
+    "dense" -- the reference operator's own K tensor [T][8][128]
+    (kessie_hip_kernels.py:443).  ``sets`` disjoint page sets (or tensors)
+    rotate across reps so the 256 MB MALL cannot serve the next rep."""
     import torch
 
     from kessie_amd import ops
@@ -215,7 +220,14 @@ def bench_remap(dev, reps=20, sets=4, n_tok=65536, page_size=16, hkv=8, d=128, t
     pages = n_tok // page_size
     g = torch.Generator(device=dev)
     g.manual_seed(0)
-    pool = torch.randn(pages * sets, page_size, 2, hkv, d, generator=g, device=dev).bfloat16()
+    if layout == "native":
+        pool = torch.randn(pages * sets, page_size, 2, hkv, d, generator=g, device=dev).bfloat16()
+    elif layout == "kv_first":
+        pool = torch.randn(2, pages * sets, page_size, hkv, d, generator=g, device=dev).bfloat16()
+    elif layout == "dense":
+        dense = [torch.randn(n_tok, hkv, d, generator=g, device=dev).bfloat16() for _ in range(sets)]
+    else:
+        raise ValueError(layout)
     g1 = torch.Generator(device=dev)
     g1.manual_seed(1)
     perm = torch.randperm(pages * sets, generator=g1, device=dev).to(torch.int32)
@@ -227,41 +239,58 @@ def bench_remap(dev, reps=20, sets=4, n_tok=65536, page_size=16, hkv=8, d=128, t
     g3.manual_seed(3)
     base = int(torch.randint(0, 1_000_000, (1,), generator=g3, device=dev).item())
     tgt = (base + torch.arange(n_tok, device=dev)).to(torch.int32)
+
+    def run(i):
+        if layout == "dense":
+            ops.rope_remap_paged(dense[i % sets], orig, tgt, theta)
+        else:
+            ops.rope_remap_paged(pool, orig, tgt, theta, page_list=lists[i % sets], layout=layout)
+
     for i in range(3):
-        ops.rope_remap_paged(pool, orig, tgt, theta, page_list=lists[i % sets])
+        run(i)
     torch.cuda.synchronize()
     e0, e1 = events(reps), events(reps)
     backlog()
     for i in range(reps):
         e0[i].record()
-        ops.rope_remap_paged(pool, orig, tgt, theta, page_list=lists[i % sets])
+        run(i)
         e1[i].record()
     torch.cuda.synchronize()
     ts = sorted(a.elapsed_time(b) for a, b in zip(e0, e1))
     mean_ms = sum(ts) / len(ts)
-    nbytes = 2 * n_tok * hkv * d * 2 + 2 * n_tok * 4 + pages * 4
+    nbytes = 2 * n_tok * hkv * d * 2 + 2 * n_tok * 4 + (0 if layout == "dense" else pages * 4)
     achieved = nbytes / (mean_ms * 1e-3) / 1e9
     res_cpu = None
     if cpu:
         from oracle.rope import rope_remap_ref
 
         cores = _cpu_threads()
-        k0 = pool[lists[0].long(), :, 0].cpu().reshape(n_tok, hkv, d)
+        if layout == "dense":
+            k0 = dense[0].cpu()
+        elif layout == "kv_first":
+            k0 = pool[0][lists[0].long()].cpu().reshape(n_tok, hkv, d)
+        else:
+            k0 = pool[lists[0].long(), :, 0].cpu().reshape(n_tok, hkv, d)
         o_c, t_c = orig.cpu(), tgt.cpu()
         k = k0.clone()
         sec = _cpu_median(lambda: rope_remap_ref(k, o_c, t_c, theta))
         res_cpu = {"value": round(n_tok / sec / 1e6, 2), "unit": "Mtok/s", "cores": cores, "kind": "port",
-                   "sample": f"the full workload ({n_tok} tokens, K [T, {hkv}, {d}] bf16 gathered from the "
-                             f"pages), torch {torch.__version__}, 1 warm-up + median of 3"}
+                   "sample": f"the full workload ({n_tok} tokens, K [T, {hkv}, {d}] bf16"
+                             + ("" if layout == "dense" else " gathered from the pages")
+                             + f"), torch {torch.__version__}, 1 warm-up + median of 3"}
+    where = {"native": f"in {page_size}-token pages of interleaved K/V rows",
+             "kv_first": f"in {page_size}-token K-only pages ([2][blocks][{page_size}][{hkv}][{d}])",
+             "dense": f"as one dense K tensor [{n_tok}][{hkv}][{d}]"}[layout]
     return {
         "cpu_baseline": res_cpu,
-        "workload": f"RoPE remap bf16, {n_tok} tokens in {page_size}-token pages, {hkv} KV heads, D={d}, "
-                    f"theta {theta:g}, K only, {sets} rotating page sets",
+        "workload": f"RoPE remap bf16, {n_tok} tokens {where}, {hkv} KV heads, D={d}, theta {theta:g}, K only, "
+                    f"{sets} rotating {'tensors' if layout == 'dense' else 'page sets'}",
         "mtok_s": round(n_tok / (mean_ms * 1e-3) / 1e6, 1),
         "kernel_ms_mean": round(mean_ms, 5),
         "kernel_ms_median": round(ts[len(ts) // 2], 5),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic("rope_remap_vec"),
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": read_traffic("rope_remap_vec") if layout == "native" else None,
                      "algorithmic_bytes": nbytes},
     }
 
@@ -507,6 +536,80 @@ def bench_decode_fp32(dev, reps=20, cpu=False):
                    "ms": round(1000 * sec, 3)}
     return {"workload": "fog decode fp32, B=1, 32q/8kv, D=128, 4096-token context",
             "ms": round(ms, 5), "gbs": round(s["bytes"] / (ms * 1e-3) / 1e9, 1), "cpu_baseline": res_cpu}
+
+
+def bench_decode_ragged(dev, reps=20, cpu=False, lens=None):
+    """Fog decode over a ragged batch through the fused entry point
+    (kessie_fog_decode_paged: split kernel + combine): B=16, 32q/8kv, D=128,
+    bf16, two 131,072-token and fourteen 4,096-token sequences in 16-token
+    pages, V-fog over the longest context.  Bytes: every sequence's K and V,
+    q and out, its page-table entries and the shared fog vector once."""
+    import torch
+
+    from kessie_amd import _lib, ops
+
+    lens = lens or [131072] * 2 + [4096] * 14
+    b, hq, hkv, d, ps = len(lens), 32, 8, 128, 16
+    max_ctx = max(lens)
+    width = (max_ctx + ps - 1) // ps
+    pages = [(c + ps - 1) // ps for c in lens]
+    n_pages = sum(pages)
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    q = torch.randn(b, hq, d, generator=g, device=dev).to(torch.bfloat16)
+    pool = torch.empty(n_pages, ps, 2, hkv, d, device=dev, dtype=torch.bfloat16)
+    for p0 in range(0, n_pages, 4096):
+        p1 = min(n_pages, p0 + 4096)
+        pool[p0:p1] = torch.randn(p1 - p0, ps, 2, hkv, d, generator=g, device=dev).to(torch.bfloat16)
+    perm = torch.randperm(n_pages, generator=g, device=dev).to(torch.int32)
+    table = torch.full((b, width), -1, dtype=torch.int32, device=dev)
+    off = 0
+    for i, n in enumerate(pages):
+        table[i, :n] = perm[off:off + n]
+        off += n
+    ctx_lens = torch.tensor(lens, dtype=torch.int32, device=dev)
+    c = int(max_ctx * 0.5)
+    fog = torch.ones(max_ctx, dtype=torch.float32, device=dev)
+    fog[:c] = (torch.arange(c, dtype=torch.float32, device=dev) / max(c - 1, 1)).pow(0.5)
+    out = torch.empty_like(q)
+    need = _lib.load().kessie_fog_decode_workspace_bytes(b, hq, hkv, d, max_ctx, ps, ops.dtype_code(q.dtype))
+    ws = torch.empty(need, dtype=torch.uint8, device=dev)
+    for _ in range(3):
+        ops.fog_decode(q, pool, table, ctx_lens, max_ctx, fog_vscale=fog, out=out, ws=ws)
+    torch.cuda.synchronize()
+    e0, e1 = events(reps), events(reps)
+    backlog()
+    for i in range(reps):
+        e0[i].record()
+        ops.fog_decode(q, pool, table, ctx_lens, max_ctx, fog_vscale=fog, out=out, ws=ws)
+        e1[i].record()
+    torch.cuda.synchronize()
+    ms = sum(a.elapsed_time(e) for a, e in zip(e0, e1)) / reps
+    nbytes = sum(lens) * hkv * d * 2 * 2 + 2 * b * hq * d * 2 + n_pages * 4 + max_ctx * 4
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    res_cpu = None
+    if cpu:
+        from oracle.attention import paged_decode_blockwise
+
+        cores = _cpu_threads()
+        q_c, fog_c = q.cpu(), fog.cpu()
+        sec = 0.0
+        for i in range(b):  # each sequence's pages gathered to host memory first, outside the timing
+            sub = pool[table[i, :pages[i]].long()].cpu()
+            sub_table = torch.arange(pages[i], dtype=torch.int32).view(1, -1)
+            t = time.perf_counter()
+            paged_decode_blockwise(q_c[i:i + 1], sub, sub_table, ctx_lens[i:i + 1].cpu(), fog_c)
+            sec += time.perf_counter() - t
+            del sub
+        res_cpu = {"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+                   "sample": "the full batch once (paged_decode_blockwise per sequence)", "seconds": round(sec, 2)}
+    return {"workload": f"fog decode bf16 ragged batch {b}: " + ", ".join(
+                f"{lens.count(v)} x {v}" for v in sorted(set(lens), reverse=True)) + " tokens, 32q/8kv, D=128",
+            "ms": round(ms, 5), "gbs": round(gbs, 1), "algorithmic_bytes": nbytes,
+            "roofline": {"bound": "hbm", "kernel": "decode_mfma_kernel + combine_kernel (step)",
+                         "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+            "cpu_baseline": res_cpu}
 
 
 def bench_fog_bias(dev, reps=50, kv_len=131072, n_recall=1000):
@@ -904,8 +1007,11 @@ def pmc_run(dev) -> None:
 # ---------------------------------------------------------------------------
 SECONDARY = {
     "remap": bench_remap,
+    "remap_dense": lambda dev, cpu=False: bench_remap(dev, cpu=cpu, layout="dense"),
+    "remap_kv_first": lambda dev, cpu=False: bench_remap(dev, cpu=cpu, layout="kv_first"),
     "gather": bench_gather_evict,
     "fp32": bench_decode_fp32,
+    "ragged": bench_decode_ragged,
     "prefill": bench_prefill,
     "dense": bench_dense,
     "dense64": lambda dev, cpu=False: bench_dense(dev, d=64, cpu=cpu),
@@ -1004,11 +1110,21 @@ def main():
         sec["rope_remap"] = bench_remap(dev, cpu=not args.no_cpu)
         result["rope_remap_mtok_s"] = sec["rope_remap"]["mtok_s"]
         torch.cuda.empty_cache()
+        log("secondary: RoPE remap, dense K tensor and K-only pages")
+        sec["rope_remap_dense_k"] = bench_remap(dev, cpu=False, layout="dense")
+        sec["rope_remap_dense_k"]["cpu_baseline"] = sec["rope_remap"]["cpu_baseline"]
+        torch.cuda.empty_cache()
+        sec["rope_remap_k_only_pages"] = bench_remap(dev, cpu=False, layout="kv_first")
+        sec["rope_remap_k_only_pages"]["cpu_baseline"] = sec["rope_remap"]["cpu_baseline"]
+        torch.cuda.empty_cache()
         log("secondary: gather + evict")
         sec["gather_evict"] = bench_gather_evict(dev, cpu=not args.no_cpu)
         torch.cuda.empty_cache()
         log("secondary: fp32 decode 4K")
         sec["decode_fp32_4k"] = bench_decode_fp32(dev, cpu=not args.no_cpu)
+        torch.cuda.empty_cache()
+        log("secondary: ragged-batch decode")
+        sec["decode_ragged_2x128k_14x4k"] = bench_decode_ragged(dev, cpu=not args.no_cpu)
         torch.cuda.empty_cache()
         log("secondary: chunked prefill 2048 x 1M")
         sec["prefill_1m"] = bench_prefill(dev, cpu=not args.no_cpu)

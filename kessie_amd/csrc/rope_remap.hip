@@ -16,11 +16,14 @@
 // with 16-byte loads: each lane owns one chunk pair (8 elements of the first
 // half of a head and the matching 8 of the second half), so a wave's loads
 // cover whole 128-byte segments of a token's K row.
-// The access pattern, not the arithmetic, bounds it: the K half (2 KiB) of
-// every 4 KiB token row of random 64 KiB pages.  Measured on MI355X with the
-// measurement probes (bytes read + written per second): that half-row pattern
-// reaches 4.8 TB/s updated in place and the same out of place, 5.9 TB/s when
-// only read; whole rows 5.6 TB/s updated and 6.8 TB/s read.
+// The access pattern, not the arithmetic, bounds it.  In interleaved K/V
+// pages K is the first 2 KiB of every 4 KiB token row of random 64 KiB pages:
+// measured on MI355X with the measurement probes (bytes read + written per
+// second), that half-row pattern reaches 4.8 TB/s updated in place and the
+// same out of place, 5.9 TB/s when only read; whole rows 5.6 TB/s updated and
+// 6.8 TB/s read.  A dense K tensor updated in place by this kernel with the
+// rotation replaced by the identity reaches 6.0 TB/s; random 32 KiB K-only
+// pages 4.7 TB/s.
 #include "common.h"
 
 namespace kessie {
@@ -69,11 +72,14 @@ struct Vec16<float> {
 // before the cos/sin phase, so HBM latency overlaps the trigonometry; the
 // workgroup barrier that publishes cos/sin keeps those loads ahead of it.
 // One chunk pair (two 16-byte loads) per thread per round.  Tile shape
-// (measured, 65,536 bf16 tokens of 8 heads x 128 in random 16-token pages):
-// one page's 16 tokens per 1,024-thread workgroup 52.1-52.7 us; 8 tokens per
-// 512 threads 54.3; 4 per 256 55.0-55.2; 1 per 64 53.7; 16 tokens with 2 or 4
-// pairs per thread 58.6-58.7; 32 tokens 57.4-59.7.  Exchanging chunk halves
-// by lane shuffle (each wave reading 1 KiB contiguous) measured the same.
+// (measured, 65,536 bf16 tokens of 8 heads x 128 in random interleaved K/V
+// 16-token pages): one page's 16 tokens per 1,024-thread workgroup
+// 52.1-52.7 us; 8 tokens per 512 threads 54.3; 4 per 256 55.0-55.2; 1 per 64
+// 53.7; 16 tokens with 2 or 4 pairs per thread 58.6-58.7; 32 tokens
+// 57.4-59.7.  Exchanging chunk halves by lane shuffle (each wave reading 1 KiB
+// contiguous) measured the same, and so did (or worse) persistent workgroups
+// that load their next tile before rotating this one, and plain instead of
+// non-temporal loads and stores (8-10 % slower), on every layout.
 constexpr int kRemapItems = 1;  // chunk pairs per thread per round
 
 // kHalf / kHeads / kPage > 0 fix head_dim/2, the head count and the page size
@@ -208,11 +214,21 @@ int launch_remap(void* pool, int64_t page_stride, int64_t tok_stride, int64_t he
                       head_stride % N == 0;
   T* p = static_cast<T*>(pool);
   if (vec_ok) {
-    // Specialised instance for the Llama-style K layout (8 kv heads x 128,
-    // 16-token pages or dense rows): one page's 16 tokens per 1,024-thread
-    // workgroup, one chunk pair per thread (bf16/fp16; fp32 rows hold twice
-    // the chunks and take two rounds).
-    if (half == 64 && num_heads == 8 && (page_list == nullptr || page_size == 16))
+    // Specialised instances for the Llama-style K shape (8 kv heads x 128,
+    // 16-token pages or dense rows), one chunk pair per thread (bf16/fp16;
+    // fp32 rows hold twice the chunks and take two rounds).  The tile follows
+    // the row layout (65,536 bf16 tokens, one MI355X): K rows that are the
+    // first half of interleaved K/V token rows run best as one page's 16
+    // tokens per 1,024-thread workgroup (54 us; 8 tokens per 512 threads 56);
+    // contiguous K rows (a dense [T][H][D] tensor, K-only pages) as 8 tokens
+    // per 512 threads (dense 45.5-46 us against 47 for the 16-token shape;
+    // K-only pages 57 either way).
+    const bool k_rows_contiguous = tok_stride == (int64_t)num_heads * head_stride;
+    if (half == 64 && num_heads == 8 && (page_list == nullptr || page_size == 16) && k_rows_contiguous)
+      hipLaunchKernelGGL((rope_remap_vec<T, 64, 8, 16, 8, 512>), dim3(div_up(num_tokens, 8)), dim3(512), 0,
+                         stream, p, page_stride, tok_stride, head_stride, page_list, num_pages, orig_pos, tgt_pos,
+                         inv_freq, theta, num_tokens, num_heads, half, page_size);
+    else if (half == 64 && num_heads == 8 && (page_list == nullptr || page_size == 16))
       hipLaunchKernelGGL((rope_remap_vec<T, 64, 8, 16, 16, 1024>), dim3(div_up(num_tokens, 16)), dim3(1024), 0,
                          stream, p, page_stride, tok_stride, head_stride, page_list, num_pages, orig_pos, tgt_pos,
                          inv_freq, theta, num_tokens, num_heads, half, page_size);

@@ -87,6 +87,52 @@ def test_remap_full_size_every_token(dev):
     assert (k2 - k0).abs().max().item() < 0.1
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("layout", ["kv_first", "block_kv"])
+def test_remap_k_only_page_layouts(dev, layout, dtype):
+    """Pools whose pages hold K rows contiguously (vLLM's [2][blocks][P][H][D]
+    and [blocks][2][P][H][D]) take the contiguous-row tile; 2,003 tokens leave
+    a partial last page and a partial last tile.  Checked through a native
+    view of the same storage against the oracle; V untouched."""
+    from kessie_amd import ops
+
+    n_tok, p, num_pages = 2003, 16, 160
+    g = gen(dev, 21)
+    if layout == "kv_first":
+        pool = torch.randn(2, num_pages, p, 8, 128, generator=g, device=dev).to(dtype)
+        native = lambda t: t.permute(1, 2, 0, 3, 4)  # noqa: E731
+    else:
+        pool = torch.randn(num_pages, 2, p, 8, 128, generator=g, device=dev).to(dtype)
+        native = lambda t: t.permute(0, 2, 1, 3, 4)  # noqa: E731
+    page_list = randperm(num_pages, dev, 22)[: (n_tok + p - 1) // p].contiguous()
+    orig = torch.randint(0, 1_000_000, (n_tok,), generator=gen(dev, 23), device=dev, dtype=torch.int32)
+    tgt = (777 + torch.arange(n_tok, device=dev)).to(torch.int32)
+    before = pool.clone()
+    ref = pool.cpu()
+    rope_remap_pages_ref(native(ref), page_list.cpu(), orig.cpu(), tgt.cpu(), 500000.0)
+    ops.rope_remap_paged(pool, orig, tgt, 500000.0, page_list=page_list, layout=layout)
+    torch.cuda.synchronize()
+    _assert_close_rare(native(pool)[:, :, 0], native(ref)[:, :, 0])
+    assert torch.equal(native(pool)[:, :, 1], native(before)[:, :, 1])
+
+
+@pytest.mark.parametrize("n_tok", [65536, 1005])
+def test_remap_dense_k_tensor(dev, n_tok):
+    """The reference operator's own form, K [T, 8, 128] bf16 (kessie_hip_kernels.py:443-476),
+    at the full 65,536 tokens and at a count that leaves a partial tile: every
+    element against the oracle."""
+    from kessie_amd import ops
+
+    k = torch.randn(n_tok, 8, 128, generator=gen(dev, 31), device=dev).bfloat16()
+    orig = torch.randint(0, 1_000_000, (n_tok,), generator=gen(dev, 32), device=dev, dtype=torch.int32)
+    base = int(torch.randint(0, 1_000_000, (1,), generator=gen(dev, 33), device=dev).item())
+    tgt = (base + torch.arange(n_tok, device=dev)).to(torch.int32)
+    ref = rope_remap_ref(k.cpu().clone(), orig.cpu(), tgt.cpu(), 500000.0)
+    ops.rope_remap_paged(k, orig, tgt, 500000.0)
+    torch.cuda.synchronize()
+    _assert_close_rare(k, ref)
+
+
 def test_remap_identity_is_bit_exact(dev):
     from kessie_amd import ops
 
