@@ -41,6 +41,48 @@ def test_graph_decode(dev):
         assert torch.equal(got, want), f"replay {i}"
 
 
+def test_graph_decode_lengths_change_between_replays(dev):
+    """A serving loop's decode graph: captured once for a batch of 16 with a
+    host bound on the context, replayed while the sequence lengths change on
+    the device (uniform, ragged, spread, empty sequences).  The split
+    workgroups are dealt out from the lengths the kernels read at run time,
+    so each replay equals an eager call on the same lengths bit for bit, and
+    the ragged replay matches the oracle."""
+    from oracle.attention import paged_decode_blockwise
+
+    from kessie_amd import ops
+
+    b, max_ctx = 16, 8192
+    q, pool, table, lens = decode_case(b, 32, 8, 128, max_ctx, 16, torch.bfloat16, dev, seed=13)
+    vs = torch.rand(max_ctx, generator=torch.Generator(device=dev).manual_seed(14), device=dev)
+    out = torch.empty_like(q)
+    g = _capture(lambda: ops.fog_decode(q, pool, table, lens, max_ctx=max_ctx, fog_vscale=vs, out=out))
+    schedules = {
+        "uniform": [max_ctx] * b,
+        "ragged": [max_ctx, max_ctx] + [512] * 14,
+        "spread": [512 * (i + 1) for i in range(b)],
+        "empty": [0, max_ctx, 0, 1, 17, 0, 4096, 0] * 2,
+    }
+    for name, new_lens in schedules.items():
+        lens.copy_(torch.tensor(new_lens, dtype=torch.int32))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got = out.clone()
+        want = ops.fog_decode(q, pool, table, lens, max_ctx=max_ctx, fog_vscale=vs)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), name
+        if name == "ragged":
+            for i in (0, 1, 2, 15):
+                sub_pool = pool[table[i].long()].cpu()
+                sub_table = torch.arange(table.shape[1], dtype=torch.int32).view(1, -1)
+                ref = paged_decode_blockwise(q[i:i + 1].cpu(), sub_pool, sub_table, lens[i:i + 1].cpu(), vs.cpu())
+                diff = (got[i:i + 1].float().cpu() - ref).abs()
+                assert (diff <= 2e-2 + 1e-2 * ref.abs()).all(), (name, i, diff.max().item())
+        if name == "empty":
+            assert not got[torch.tensor(new_lens, device=dev) == 0].any()
+
+
 def test_graph_evict_pipeline(dev):
     from kessie_amd import ops
 
