@@ -71,6 +71,40 @@ def test_decode_fp32_cpu_path_shape(dev):
     _check(out, ref, torch.float32)
 
 
+def test_decode_fp32_config_inputs_with_rope(dev):
+    """The configuration's inputs as specified: fp32, B=1, 32q/8kv, D=128,
+    4,096 tokens in 16-token pages (table randperm(256), seed 1), Q, K, V ~
+    N(0,1) from seed 0 in that order, K stored after rotate-half RoPE (theta
+    1e4) at positions 0..4095 and q rotated at position 4095, fog weights
+    build_fog_weights(4096, 0.5, 0.5), window 0: within 1e-5 of the oracle."""
+    from kessie_amd import ops
+
+    n, hq, hkv, d, p = 4096, 32, 8, 128, 16
+    g = gen(dev, 0)
+    q = torch.randn(1, hq, d, generator=g, device=dev)
+    k = torch.randn(n, hkv, d, generator=g, device=dev)
+    v = torch.randn(n, hkv, d, generator=g, device=dev)
+
+    def rope(x, pos):  # rotate-half RoPE in float64; x [T, H, D], pos [T]
+        inv = 1.0 / (1e4 ** (torch.arange(d // 2, dtype=torch.float64, device=dev) / (d // 2)))
+        ang = pos.double()[:, None] * inv[None, :]
+        c, s = ang.cos()[:, None, :], ang.sin()[:, None, :]
+        x1, x2 = x[..., :d // 2].double(), x[..., d // 2:].double()
+        return torch.cat([x1 * c - x2 * s, x1 * s + x2 * c], -1).float()
+
+    k = rope(k, torch.arange(n, device=dev))
+    q = rope(q, torch.tensor([n - 1], device=dev))
+    table = torch.randperm(n // p, generator=gen(dev, 1), device=dev).to(torch.int32).view(1, -1)
+    pool = torch.empty(n // p, p, 2, hkv, d, device=dev)
+    pool[table[0].long()] = torch.stack([k, v], 1).view(n // p, p, 2, hkv, d)
+    lens = torch.tensor([n], dtype=torch.int32, device=dev)
+    vs = build_fog_weights(n, 0.5, 0.5).to(dev)
+    out = ops.fog_decode(q, pool, table, lens, max_ctx=n, fog_vscale=vs)
+    torch.cuda.synchronize()
+    ref = paged_decode_ref(q.cpu(), pool.cpu(), table.cpu(), lens.cpu(), vs.cpu(), None, 0)
+    _check(out, ref, torch.float32)
+
+
 @pytest.mark.parametrize("fog", ["none", "bias", "vscale_batched", "both"])
 def test_decode_fog_modes(dev, fog):
     out, ref = _run(dev, 3, 32, 8, 530, torch.bfloat16, fog=fog)
