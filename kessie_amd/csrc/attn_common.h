@@ -58,14 +58,18 @@ struct Params {
   float* ws_l;  // [B*C*Hq][S]
 };
 
-__device__ __forceinline__ int seq_ctx(const Params& p, int b) {
-  int ctx = p.ctx_lens ? p.ctx_lens[b] : p.ctx_const;
+// A sequence length as the kernels use it: at most max_ctx and the page
+// table's capacity, at least 0.
+__device__ __forceinline__ int clamp_ctx(const Params& p, int ctx) {
   ctx = min(ctx, p.max_ctx);
   if (p.page_table) {
     const int64_t cap = p.table_stride * (int64_t)p.page_size;
     if ((int64_t)ctx > cap) ctx = (int)cap;
   }
   return max(ctx, 0);
+}
+__device__ __forceinline__ int seq_ctx(const Params& p, int b) {
+  return clamp_ctx(p, p.ctx_lens ? p.ctx_lens[b] : p.ctx_const);
 }
 
 // Element offset of token t of sequence b, or -1 when its page id is invalid.

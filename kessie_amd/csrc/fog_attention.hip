@@ -237,113 +237,85 @@ constexpr int kMaxSplits = 512;
 // more partials than the combine takes) with sum_b ceil(pages_b / P) <= U,
 // and sequence b gets ceil(pages_b / P) consecutive units.  A uniform batch
 // gets S units per sequence, the page ranges of the plain split.  Unit u's
-// partial of head h sits at slot u * Hq + h.  Each function is evaluated by a
-// whole wave and returns the same value in every lane.
+// partial of head h sits at slot h * U + u, so a row's partials are
+// consecutive, as in the plain layout.  Each function is evaluated by a
+// whole wave (lane b holds sequence b: batches of up to kBalSeqs) and returns
+// the same value in every lane.
+//
+// Every wave of the launch runs this before its first page load, and its
+// cost is mostly the fetch of its code (the caches hold none of it at the
+// start of a launch): an unrolled form with four lengths per lane took
+// 6-8 us per wave before the first page load, and a 4K-token decode ran 2.8
+// times slower than with the plain split; a second pass over the same code in
+// the same wave took 0.2 us.  So the code is kept short (one length per lane,
+// reductions and the scan on the device library's DPP path), and
+// decode_entry only chooses it for batches whose streaming time makes the
+// rest negligible.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ int wave_sum_i(int v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
-__device__ __forceinline__ int wave_max_i(int v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = max(v, __shfl_xor(v, o, 64));
-  return v;
-}
+extern "C" __device__ int __ockl_wfscan_add_i32(int, bool);  // inclusive when the flag is set
+
+constexpr int kBalSeqs = 64;  // batches the balanced split takes: one length per lane
+
 // Pages a decode over ctx tokens reads (16-token pages): those of its window.
 __device__ __forceinline__ int decode_pages(const Params& p, int ctx) {
   const int lo = p.window > 0 ? max(0, ctx - p.window) : 0;
   return ((ctx + 15) >> 4) - (lo >> 4);
 }
-constexpr int kBalSeqs = 256;  // batches the balanced split takes: 4 lengths per lane, read once
 struct BatchPages {
-  int ctx[kBalSeqs / 64];  // length of sequence lane + 64 j (0 past the batch)
-  int pg[kBalSeqs / 64];   // its pages
-  // Length of sequence b (uniform b), from the registers.
-  __device__ int seq_len(int b) const {
-    int v = ctx[0];
-#pragma unroll
-    for (int j = 1; j < kBalSeqs / 64; ++j)
-      if ((b >> 6) == j) v = ctx[j];
-    return __builtin_amdgcn_readlane(v, b & 63);
-  }
+  int ctx;  // length of sequence `lane` (0 past the batch)
+  int pg;   // its pages
+  __device__ int seq_len(int b) const { return __builtin_amdgcn_readlane(ctx, b); }  // uniform b
+  __device__ int seq_pages(int b) const { return __builtin_amdgcn_readlane(pg, b); }
 };
 __device__ __forceinline__ BatchPages batch_pages(const Params& p) {
   const int lane = threadIdx.x & 63;
   BatchPages bp;
-#pragma unroll
-  for (int j = 0; j < kBalSeqs / 64; ++j) {
-    bp.ctx[j] = lane + 64 * j < p.B ? seq_ctx(p, lane + 64 * j) : 0;
-    bp.pg[j] = decode_pages(p, bp.ctx[j]);
-  }
+  bp.ctx = lane < p.B ? clamp_ctx(p, p.ctx_lens ? p.ctx_lens[lane] : p.ctx_const) : 0;
+  bp.pg = decode_pages(p, bp.ctx);
   return bp;
 }
 // P for S units per sequence of a B-sequence batch (U = S * B).
 __device__ int decode_unit_pages(const BatchPages& bp, int S, int B) {
   const int lane = threadIdx.x & 63;
-  int mx = 0, mn = INT_MAX;
-#pragma unroll
-  for (int j = 0; j < kBalSeqs / 64; ++j)
-    if (lane + 64 * j < B) {
-      mx = max(mx, bp.pg[j]);
-      mn = min(mn, bp.pg[j]);
-    }
-  mx = wave_max_i(mx);
-  mn = -wave_max_i(-mn);
-  int lo = max(1, (mx + kMaxSplits - 1) / kMaxSplits), hi = max(lo, mx);  // P = mx fits: B <= U units
+  const int mx = __ockl_wfred_max_i32(bp.pg);
+  const int mn = __ockl_wfred_min_i32(lane < B ? bp.pg : INT_MAX);
+  int lo = max(1, (mx + kMaxSplits - 1) / kMaxSplits);
   // Every sequence the same length: S units each, the plain split.
   if (mn == mx) return max(lo, (mx + S - 1) / S);
+  const int tot = __ockl_wfred_add_i32(bp.pg);
+  const int nz = __ockl_wfred_add_i32(bp.pg > 0 ? 1 : 0);
   const int U = S * B;
+  // Bounds on the answer: a P that fits has tot / P <= U, so P >= ceil(tot / U);
+  // P = mx fits (at most B <= U units), and so does ceil(tot / (U - nz)) when
+  // U > nz, since sum ceil(pages / P) <= tot / P + nz.
+  lo = max(lo, (tot + U - 1) / U);
+  int hi = max(lo, mx);
+  if (U > nz) hi = min(hi, max(lo, (tot + (U - nz) - 1) / (U - nz)));
   while (lo < hi) {
     const int mid = (lo + hi) >> 1;
-    int n = 0;
-#pragma unroll
-    for (int j = 0; j < kBalSeqs / 64; ++j)
-      if (64 * j < B) n += (bp.pg[j] + mid - 1) / mid;
-    if (wave_sum_i(n) <= U)
+    if (__ockl_wfred_add_i32((bp.pg + mid - 1) / mid) <= U)
       hi = mid;
     else
       lo = mid + 1;
   }
   return lo;
 }
-// The sequence and split of unit u; false when u is past the batch's units.
+// The sequence and split of unit u (uniform u); false when u is past the
+// batch's units.
 __device__ bool decode_seq_of_unit(const BatchPages& bp, int P, int u, int* b_out, int* s_out) {
-  const int lane = threadIdx.x & 63;
-  int base = 0;
-#pragma unroll
-  for (int j = 0; j < kBalSeqs / 64; ++j) {
-    const int n = (bp.pg[j] + P - 1) / P;
-    int incl = n;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int y = __shfl_up(incl, o, 64);
-      if (lane >= o) incl += y;
-    }
-    const int excl = incl - n;
-    const unsigned long long hit = __ballot(u >= base + excl && u < base + incl);
-    if (hit != 0) {
-      const int l = __ffsll((long long)hit) - 1;
-      *b_out = 64 * j + l;
-      *s_out = u - base - __shfl(excl, l, 64);
-      return true;
-    }
-    base += __shfl(incl, 63, 64);
-  }
-  return false;
+  const int n = (bp.pg + P - 1) / P;
+  const int incl = __ockl_wfscan_add_i32(n, true);
+  if (u >= __builtin_amdgcn_readlane(incl, 63)) return false;
+  const int b = __ffsll((long long)__ballot(u < incl)) - 1;  // the first lane whose units reach past u
+  *b_out = b;
+  *s_out = u - __builtin_amdgcn_readlane(incl - n, b);
+  return true;
 }
-// The first unit of sequence b and its number of units.
+// The first unit of sequence b (uniform b) and its number of units.
 __device__ void decode_units_of_seq(const BatchPages& bp, int P, int b, int* u0, int* n) {
   const int lane = threadIdx.x & 63;
-  int before = 0, mine = 0;
-#pragma unroll
-  for (int j = 0; j < kBalSeqs / 64; ++j) {
-    const int c = lane + 64 * j, k = (bp.pg[j] + P - 1) / P;
-    before += c < b ? k : 0;
-    mine += c == b ? k : 0;
-  }
-  *u0 = wave_sum_i(before);
-  *n = wave_sum_i(mine);
+  *u0 = __ockl_wfred_add_i32(lane < b ? (bp.pg + P - 1) / P : 0);
+  *n = (bp.seq_pages(b) + P - 1) / P;
 }
 // Workgroup (row, y) merges d in [y*D/Y, (y+1)*D/Y) of one row (Y =
 // gridDim.y, 1 unless rows are few).  With an even chunk its 256 lanes are
@@ -371,9 +343,9 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(Params p) {
   }
   const int tid = threadIdx.x, lane = tid & 63;
   // The row's partials: S of them at row * S + s, or, with balanced decode
-  // splits, n_s at (u0 + s) * Hq + h (its sequence's units).
+  // splits, n_s at h * S * B + u0 + s (its sequence's units).
   __shared__ int s_first, s_count;
-  int64_t first = row * S, stride = 1;
+  int64_t first = row * S;
   int n_s = S;
   if (p.balanced) {
     if (tid < 64) {
@@ -387,23 +359,22 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(Params p) {
       }
     }
     __syncthreads();
-    first = (int64_t)s_first * p.Hq + h;
-    stride = p.Hq;
+    first = (int64_t)h * S * p.B + s_first;
     n_s = s_count;
   }
   const float* m = p.ws_m + first;
   const float* l = p.ws_l + first;
   if (tid < 64) {
     float mx = kNegInf;
-    for (int s = lane; s < n_s; s += 64) mx = fmaxf(mx, m[s * stride]);
+    for (int s = lane; s < n_s; s += 64) mx = fmaxf(mx, m[s]);
 #pragma unroll
     for (int w = 32; w >= 1; w >>= 1) mx = fmaxf(mx, __shfl_xor(mx, w, 64));
     float sum = 0.0f;
     for (int s = lane; s < n_s; s += 64) {
-      const float ms = m[s * stride];
+      const float ms = m[s];
       const float e = (ms == kNegInf) ? 0.0f : expf(ms - mx);
       e_s[s] = e;
-      sum += e * l[s * stride];
+      sum += e * l[s];
     }
 #pragma unroll
     for (int w = 32; w >= 1; w >>= 1) sum += __shfl_xor(sum, w, 64);
@@ -414,7 +385,6 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(Params p) {
   const int chunk = D / gridDim.y;
   const int d0 = blockIdx.y * chunk;
   const float* o = p.ws_o + first * D + d0;
-  const int64_t ostride = stride * D;
   if ((chunk & 1) == 0 && kCombineThreads % (chunk / 2) == 0) {
     const int cols = chunk / 2;                // float2 columns
     const int groups = kCombineThreads / cols;
@@ -423,7 +393,7 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(Params p) {
 #pragma unroll 4
     for (int s = grp; s < n_s; s += groups) {
       const float e = e_s[s];
-      const float2 v = *reinterpret_cast<const float2*>(o + (int64_t)s * ostride + 2 * col);
+      const float2 v = *reinterpret_cast<const float2*>(o + (int64_t)s * D + 2 * col);
       ax += e * v.x;
       ay += e * v.y;
     }
@@ -441,7 +411,7 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(Params p) {
   } else {
     for (int d = tid; d < chunk; d += kCombineThreads) {
       float acc = 0.0f;
-      for (int s = 0; s < n_s; ++s) acc += e_s[s] * o[(int64_t)s * ostride + d];
+      for (int s = 0; s < n_s; ++s) acc += e_s[s] * o[(int64_t)s * D + d];
       store_out<T>(p, b, i, h, d0 + d, acc * il);
     }
   }
@@ -728,7 +698,7 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) 
       *reinterpret_cast<vec4*>(dst + 16 * blk) = ov;
     }
   } else {
-    const int64_t slot = p.balanced ? (int64_t)unit * p.Hq + head : row_id(p, b, 0, head) * S + split;
+    const int64_t slot = p.balanced ? (int64_t)head * S * p.B + unit : row_id(p, b, 0, head) * S + split;
     float* dst = p.ws_o + slot * 128 + 4 * grp;
 #pragma unroll
     for (int blk = 0; blk < 8; ++blk) *reinterpret_cast<f32x4*>(dst + 16 * blk) = oacc[blk];
@@ -936,7 +906,7 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) 
 #pragma unroll
     for (int blk = 0; blk < 8; ++blk) *reinterpret_cast<f32x4*>(dst + 16 * blk) = oacc[blk] * il;
   } else {
-    const int64_t slot = p.balanced ? (int64_t)unit * p.Hq + head : row_id(p, b, 0, head) * S + split;
+    const int64_t slot = p.balanced ? (int64_t)head * S * p.B + unit : row_id(p, b, 0, head) * S + split;
     float* dst = p.ws_o + slot * 128 + 4 * grp;
 #pragma unroll
     for (int blk = 0; blk < 8; ++blk) *reinterpret_cast<f32x4*>(dst + 16 * blk) = oacc[blk];
@@ -1233,8 +1203,14 @@ static int decode_entry(const void* q, const void* kv_pool, int num_pages, int64
   hipStream_t s = as_stream(stream);
   if (decode_mfma_ok(p, dtype)) {
     // Split partials merged here: assign the splits by pages across the batch
-    // (the partials-only form keeps the plain row * S + split layout).
-    p.balanced = (!partials_only && !p.direct_out && batch <= kBalSeqs) ? 1 : 0;
+    // (the partials-only form keeps the plain row * S + split layout).  Its
+    // set-up costs each wave ~1 us before the first page load, so it is taken
+    // for batches of 2..kBalSeqs sequences whose bound on the K/V bytes (B *
+    // max_ctx tokens) streams for at least ~40 us, 256 MiB; one sequence, or a
+    // batch that small, gets the plain split.
+    const double kv_bound = (double)batch * max_ctx * num_kv_heads * head_dim * 2.0 * dtype_size(dtype);
+    p.balanced = (!partials_only && !p.direct_out && batch >= 2 && batch <= kBalSeqs &&
+                  kv_bound >= 256.0 * 1024 * 1024) ? 1 : 0;
     if (dtype == KESSIE_DTYPE_F32) return run_decode_mfma_f32(p, s);
     return dtype == KESSIE_DTYPE_BF16 ? run_decode_mfma<bf16_t>(p, s) : run_decode_mfma<f16_t>(p, s);
   }
