@@ -223,6 +223,30 @@ def test_decode_ragged_batch(dev, dtype, kind):
         _check(out[i:i + 1], ref, dtype)
 
 
+@pytest.mark.parametrize("b", [64, 65])
+def test_decode_ragged_batch_at_the_balanced_limit(dev, b):
+    """64 sequences (the most the balanced split takes: one per lane) and 65
+    (the plain split), lengths spread over 0..4096 with empty ones among them;
+    every sequence against the oracle."""
+    from kessie_amd import ops
+
+    ctx = 4096
+    ctx_lens = [(i * 997) % (ctx + 1) if i % 9 else 0 for i in range(b)]
+    ctx_lens[b - 1] = ctx  # the last lane holds a full-length sequence
+    q, pool, table, lens = decode_case(b, 32, 8, 128, ctx, 16, torch.bfloat16, dev, seed=93, ctx_lens=ctx_lens)
+    vs = build_fog_weights(ctx).to(dev)
+    out = ops.fog_decode(q, pool, table, lens, ctx, fog_vscale=vs)
+    torch.cuda.synchronize()
+    for i in range(b):
+        if ctx_lens[i] == 0:
+            assert not out[i].any()
+            continue
+        sub_pool = pool[table[i].long()].cpu()
+        sub_table = torch.arange(table.shape[1], dtype=torch.int32).view(1, -1)
+        ref = paged_decode_blockwise(q[i:i + 1].cpu(), sub_pool, sub_table, lens[i:i + 1].cpu(), vs.cpu())
+        _check(out[i:i + 1], ref, torch.bfloat16)
+
+
 @pytest.mark.parametrize("hq,hkv,fog,window,ctx_lens", [
     (32, 8, "vscale", 0, None),
     (32, 8, "both", 100, [4096, 1000, 17]),
