@@ -298,7 +298,8 @@ def bench_remap(dev, reps=20, sets=4, n_tok=65536, page_size=16, hkv=8, d=128, t
         "timing": f"{reps} launches back to back between two events",
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": read_traffic("rope_remap_vec") if layout == "native" else None,
+                     "traffic": {"native": read_traffic("rope_remap_vec"),
+                                 "dense": read_traffic("rope_remap_vec_dense_k")}.get(layout),
                      "algorithmic_bytes": nbytes},
     }
 
@@ -964,9 +965,10 @@ def bench_hbm_ceilings(dev, reps=10):
 def pmc_run(dev) -> None:
     """A short fixed sequence of launches for hardware-counter passes
     (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE): a 1 GiB device copy of
-    known size (the calibration kernel), then one decode, one remap, one
-    gather + evict pipeline, one recall-inject, one index query, one HF
-    append + fog launch and one chunked prefill of the bench workloads."""
+    known size (the calibration kernel), then one decode, one remap in
+    interleaved pages and one on a dense K tensor, one gather + evict
+    pipeline, one recall-inject, one index query, one HF append + fog launch
+    and one chunked prefill of the bench workloads."""
     import torch
 
     src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
@@ -981,6 +983,8 @@ def pmc_run(dev) -> None:
     del s
     torch.cuda.empty_cache()
     bench_remap(dev, reps=1, sets=1)
+    torch.cuda.empty_cache()
+    bench_remap(dev, reps=1, sets=1, layout="dense")
     torch.cuda.empty_cache()
     bench_gather_evict(dev, reps=1)
     torch.cuda.empty_cache()
