@@ -223,6 +223,28 @@ def test_decode_ragged_batch(dev, dtype, kind):
         _check(out[i:i + 1], ref, dtype)
 
 
+@pytest.mark.parametrize("hq,hkv,ctx", [(16, 1, 65536), (64, 8, 32768)])
+def test_decode_ragged_batch_gqa(dev, hq, hkv, ctx):
+    """Ragged batches through the balanced split at other GQA shapes (MQA and
+    8 q heads per kv head): every sequence against the oracle."""
+    from kessie_amd import ops
+
+    ctx_lens = [ctx, 17, ctx // 3, 0, 4097, ctx - 5, 1, 2048]
+    b = len(ctx_lens)
+    q, pool, table, lens = decode_case(b, hq, hkv, 128, ctx, 16, torch.bfloat16, dev, seed=95, ctx_lens=ctx_lens)
+    vs = build_fog_weights(ctx).to(dev)
+    out = ops.fog_decode(q, pool, table, lens, ctx, fog_vscale=vs)
+    torch.cuda.synchronize()
+    for i in range(b):
+        if ctx_lens[i] == 0:
+            assert not out[i].any()
+            continue
+        sub_pool = pool[table[i].long()].cpu()
+        sub_table = torch.arange(table.shape[1], dtype=torch.int32).view(1, -1)
+        ref = paged_decode_blockwise(q[i:i + 1].cpu(), sub_pool, sub_table, lens[i:i + 1].cpu(), vs.cpu())
+        _check(out[i:i + 1], ref, torch.bfloat16)
+
+
 @pytest.mark.parametrize("b", [64, 65])
 def test_decode_ragged_batch_at_the_balanced_limit(dev, b):
     """64 sequences (the most the balanced split takes: one per lane) and 65
