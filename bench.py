@@ -140,18 +140,27 @@ def time_decode(s, steps, warmup):
     for _ in range(warmup):
         run_decode_step(s)
     torch.cuda.synchronize()
-    e0, e1 = events(steps), events(steps)
+    # The steps: K decodes back to back between two events, nothing else in
+    # the stream (an event pair around each launch would add its dispatch and
+    # completion, ~2-3 us, to every step).
     start, end = events(2)
     backlog()
     start.record()
+    for _ in range(steps):
+        run_decode_step(s)
+    end.record()
+    torch.cuda.synchronize()
+    total_ms = start.elapsed_time(end)
+    # The streaming kernel alone: the same K steps again, with an event pair
+    # around each partials launch.
+    e0, e1 = events(steps), events(steps)
+    backlog()
     for i in range(steps):
         e0[i].record()
         ops.fog_decode_partials(s["q"], s["pool"], s["table"], s["lens"], s["ctx"], s["ws"], fog_vscale=s["fog"])
         e1[i].record()
         ops.fog_decode_combine(s["ws"], s["out"], s["hkv"], s["ctx"], s["page_size"])
-    end.record()
     torch.cuda.synchronize()
-    total_ms = start.elapsed_time(end)
     kern = [a.elapsed_time(b) for a, b in zip(e0, e1)]
     return total_ms / steps, sum(kern) / len(kern)
 
