@@ -533,14 +533,7 @@ def bench_decode_fp32(dev, reps=20, cpu=False):
     for _ in range(3):
         run_decode_step(s)
     torch.cuda.synchronize()
-    e0, e1 = events(reps), events(reps)
-    backlog()
-    for i in range(reps):
-        e0[i].record()
-        run_decode_step(s)
-        e1[i].record()
-    torch.cuda.synchronize()
-    ms = sum(a.elapsed_time(b) for a, b in zip(e0, e1)) / reps
+    ms = time_back_to_back(lambda i: run_decode_step(s), reps)  # steps back to back, as the headline's
     res_cpu = None
     if cpu:
         from oracle.attention import paged_decode_ref
@@ -595,14 +588,9 @@ def bench_decode_ragged(dev, reps=20, cpu=False, lens=None):
     for _ in range(3):
         ops.fog_decode(q, pool, table, ctx_lens, max_ctx, fog_vscale=fog, out=out, ws=ws)
     torch.cuda.synchronize()
-    e0, e1 = events(reps), events(reps)
-    backlog()
-    for i in range(reps):
-        e0[i].record()
-        ops.fog_decode(q, pool, table, ctx_lens, max_ctx, fog_vscale=fog, out=out, ws=ws)
-        e1[i].record()
-    torch.cuda.synchronize()
-    ms = sum(a.elapsed_time(e) for a, e in zip(e0, e1)) / reps
+    # steps back to back, as the headline's
+    ms = time_back_to_back(lambda i: ops.fog_decode(q, pool, table, ctx_lens, max_ctx, fog_vscale=fog, out=out, ws=ws),
+                           reps)
     nbytes = sum(lens) * hkv * d * 2 * 2 + 2 * b * hq * d * 2 + n_pages * 4 + max_ctx * 4
     gbs = nbytes / (ms * 1e-3) / 1e9
     res_cpu = None
