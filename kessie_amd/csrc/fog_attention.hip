@@ -12,7 +12,8 @@
 //
 // Kernels:
 //   decode_mfma   bf16/f16 (fp32: decode_mfma_f32 on v_mfma_f32_16x16x4_f32,
-//                 same decomposition), head_dim 128, 16-token pages.  One workgroup =
+//                 same decomposition), head_dim 128, pages of 16 * 2^k tokens
+//                 (read as 16-token blocks).  One workgroup =
 //                 one (sequence, split) x 2 kv heads, one wave per kv head; a
 //                 wave streams its kv head's 256-byte K and V rows of every
 //                 page in its split with 16-byte loads (register prefetch of
@@ -256,7 +257,7 @@ extern "C" __device__ int __ockl_wfscan_add_i32(int, bool);  // inclusive when t
 
 constexpr int kBalSeqs = 64;  // batches the balanced split takes: one length per lane
 
-// Pages a decode over ctx tokens reads (16-token pages): those of its window.
+// 16-token blocks a decode over ctx tokens reads: those of its window.
 __device__ __forceinline__ int decode_pages(const Params& p, int ctx) {
   const int lo = p.window > 0 ? max(0, ctx - p.window) : 0;
   return ((ctx + 15) >> 4) - (lo >> 4);
@@ -426,7 +427,7 @@ inline int combine_dsplit(int64_t rows, int D) {
 }
 
 // ---------------------------------------------------------------------------
-// MFMA decode (bf16 / f16, head_dim 128, 16-token pages)
+// MFMA decode (bf16 / f16, head_dim 128, pages of 16 * 2^k tokens)
 //
 // One workgroup = (split of one sequence's pages) x kDecWaves kv heads, one
 // wave per kv head, no workgroup barriers.  Per page a wave:
@@ -536,6 +537,10 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) 
   const T* vbase = static_cast<const T*>(p.v) + (int64_t)g * p.head_stride;
   const int32_t* table = p.page_table + (int64_t)b * p.table_stride;
   const int64_t ts = p.tok_stride;
+  // The loop runs over 16-token blocks; a page of 16 * 2^psh tokens holds
+  // 2^psh of them, block lp at rows 16 * (lp & pmask) of page table[lp >> psh].
+  const int psh = __builtin_ctz((unsigned)p.page_size) - 4;
+  const int pmask = (1 << psh) - 1;
   const int64_t koff = (int64_t)row * ts + 8 * grp;        // + 32*kb
   const int64_t voff = (int64_t)(4 * grp) * ts + 8 * row;  // + i*ts
 
@@ -581,11 +586,12 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) 
   };
 
   auto issue = [&](int st, int lp) {
-    const int pid = table[lp];
+    const int pid = table[lp >> psh];
     pid_s[st] = pid;
     if (pid >= 0 && pid < p.num_pages) {
-      const T* kp = kbase + (int64_t)pid * p.page_stride;
-      const T* vp = vbase + (int64_t)pid * p.page_stride;
+      const int64_t at = (int64_t)pid * p.page_stride + (int64_t)((lp & pmask) << 4) * ts;
+      const T* kp = kbase + at;
+      const T* vp = vbase + at;
       // Non-temporal: each K/V byte is read once per launch (measured 9 % faster
       // than plain loads for this access pattern).
 #pragma unroll
@@ -710,7 +716,7 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) 
 }
 
 // ---------------------------------------------------------------------------
-// fp32 decode on MFMA (head_dim 128, 16-token pages): the bf16 kernel's
+// fp32 decode on MFMA (head_dim 128, pages of 16 * 2^k tokens): the bf16 kernel's
 // decomposition with v_mfma_f32_16x16x4_f32 and the probabilities kept in
 // fp32 (no rounding of p, so fp32 inputs meet a 1e-5 tolerance).
 //   * K: lane (grp, row) loads token `row`'s d = 32*grp .. 32*grp+31 (128
@@ -767,6 +773,10 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) 
   const float* vbase = static_cast<const float*>(p.v) + (int64_t)g * p.head_stride;
   const int32_t* table = p.page_table + (int64_t)b * p.table_stride;
   const int64_t ts = p.tok_stride;
+  // The loop runs over 16-token blocks; a page of 16 * 2^psh tokens holds
+  // 2^psh of them, block lp at rows 16 * (lp & pmask) of page table[lp >> psh].
+  const int psh = __builtin_ctz((unsigned)p.page_size) - 4;
+  const int pmask = (1 << psh) - 1;
   const int64_t koff = (int64_t)row * ts + 32 * grp;
   const int64_t voff = (int64_t)(4 * grp) * ts + 8 * row;  // + i*ts, +4
 
@@ -796,11 +806,12 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     if (FOG & kFogVs) fv_cur = in ? fog_v[tl] : 0.0f;
   };
   auto issue = [&](int st, int lp) {
-    const int pid = table[lp];
+    const int pid = table[lp >> psh];
     pid_s[st] = pid;
     if (pid >= 0 && pid < p.num_pages) {
-      const float* kp = kbase + (int64_t)pid * p.page_stride;
-      const float* vp = vbase + (int64_t)pid * p.page_stride;
+      const int64_t at = (int64_t)pid * p.page_stride + (int64_t)((lp & pmask) << 4) * ts;
+      const float* kp = kbase + at;
+      const float* vp = vbase + at;
 #pragma unroll
       for (int j = 0; j < 8; ++j)
         kreg[st][j] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(kp + koff + 4 * j));
@@ -1081,7 +1092,9 @@ int run_generic(int dtype, Params& p, hipStream_t s) {
 bool decode_mfma_ok(const Params& p, int dtype) {
   if (env_int("KESSIE_FORCE_GENERIC", 0)) return false;
   if (dtype != KESSIE_DTYPE_BF16 && dtype != KESSIE_DTYPE_F16 && dtype != KESSIE_DTYPE_F32) return false;
-  if (p.D != 128 || p.page_size != 16 || p.page_table == nullptr) return false;
+  // Pages of 16 * 2^k tokens (vLLM's 16, 32, 64, ... token blocks).
+  if (p.D != 128 || p.page_size < 16 || (p.page_size & (p.page_size - 1)) != 0 || p.page_table == nullptr)
+    return false;
   if (!(p.G == 1 || p.G == 2 || p.G == 4 || p.G == 8 || p.G == 16)) return false;
   if (!aligned16(p.q) || !aligned16(p.k) || !aligned16(p.v) || !aligned16(p.out)) return false;
   // 16-byte rows: 8 elements of bf16/fp16, 4 of fp32.

@@ -25,10 +25,10 @@ def _check(got, ref, dtype):
     assert not bad.any(), f"{int(bad.sum())}/{bad.numel()} outside tol, max diff {diff.max().item():.3e}"
 
 
-def _run(dev, b, hq, hkv, ctx, dtype, fog="vscale", window=0, ctx_lens=None, layout="native", seed=0):
+def _run(dev, b, hq, hkv, ctx, dtype, fog="vscale", window=0, ctx_lens=None, layout="native", seed=0, page_size=16):
     from kessie_amd import ops
 
-    d, p = 128, 16
+    d, p = 128, page_size
     q, pool, table, lens = decode_case(b, hq, hkv, d, ctx, p, dtype, dev, seed=seed, ctx_lens=ctx_lens)
     vs = bias = None
     if fog == "vscale":
@@ -58,6 +58,47 @@ def _run(dev, b, hq, hkv, ctx, dtype, fog="vscale", window=0, ctx_lens=None, lay
 def test_decode_bf16_gqa(dev, hq, hkv):
     out, ref = _run(dev, 2, hq, hkv, 1000, torch.bfloat16)
     _check(out, ref, torch.bfloat16)
+
+
+@pytest.mark.parametrize("page_size,dtype,fog,window,ctx_lens,layout", [
+    (32, torch.bfloat16, "vscale", 0, [1000, 37, 777], "native"),
+    (64, torch.bfloat16, "both", 100, [530, 301, 17], "native"),
+    (32, torch.float32, "vscale", 0, [1000, 0, 513], "native"),
+    (32, torch.bfloat16, "bias", 0, [640, 33, 1], "kv_first"),
+    (128, torch.bfloat16, "vscale", 0, [1000, 129, 128], "native"),
+])
+def test_decode_larger_pages(dev, page_size, dtype, fog, window, ctx_lens, layout):
+    """Pages of 32, 64 and 128 tokens (vLLM block sizes) on the MFMA kernels,
+    which read them as 16-token blocks: against the oracle, ragged and empty
+    sequences, windows and vLLM's K/V-first layout included."""
+    out, ref = _run(dev, len(ctx_lens), 32, 8, max(ctx_lens), dtype, fog=fog, window=window, ctx_lens=ctx_lens,
+                    layout=layout, page_size=page_size)
+    _check(out, ref, dtype)
+    for i, n in enumerate(ctx_lens):
+        if n == 0:
+            assert not out[i].any()
+
+
+def test_decode_larger_pages_balanced(dev):
+    """32-token pages through the balanced split (a ragged batch whose K/V
+    bound passes its threshold): every sequence against the oracle."""
+    from kessie_amd import ops
+
+    ctx, p = 32768, 32
+    ctx_lens = [ctx, 5, 20000, 0]
+    q, pool, table, lens = decode_case(len(ctx_lens), 32, 8, 128, ctx, p, torch.bfloat16, dev, seed=97,
+                                       ctx_lens=ctx_lens)
+    vs = build_fog_weights(ctx).to(dev)
+    out = ops.fog_decode(q, pool, table, lens, ctx, fog_vscale=vs)
+    torch.cuda.synchronize()
+    for i, n in enumerate(ctx_lens):
+        if n == 0:
+            assert not out[i].any()
+            continue
+        sub_pool = pool[table[i].long()].cpu()
+        sub_table = torch.arange(table.shape[1], dtype=torch.int32).view(1, -1)
+        ref = paged_decode_blockwise(q[i:i + 1].cpu(), sub_pool, sub_table, lens[i:i + 1].cpu(), vs.cpu())
+        _check(out[i:i + 1], ref, torch.bfloat16)
 
 
 def test_decode_fp16(dev):
