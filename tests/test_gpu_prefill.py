@@ -21,8 +21,8 @@ def _check(got, ref, dtype):
     assert not bad.any(), f"{int(bad.sum())}/{bad.numel()} outside tol, max diff {diff.max().item():.3e}"
 
 
-def _case(dev, b, c, ctxs, hq, hkv, dtype, seed=0):
-    p, d = 16, 128
+def _case(dev, b, c, ctxs, hq, hkv, dtype, seed=0, page_size=16):
+    p, d = page_size, 128
     pages_per = max((x + p - 1) // p for x in ctxs)
     num_pages = b * pages_per + 3
     pool = paged_pool(num_pages, p, hkv, d, dtype, dev, seed)
@@ -102,6 +102,58 @@ def test_prefill_fp32_generic(dev):
     torch.cuda.synchronize()
     ref = paged_prefill_ref(q.cpu(), pool.cpu(), table.cpu(), lens.cpu(), fog.cpu())
     _check(out, ref, torch.float32)
+
+
+@pytest.mark.parametrize("page_size,dtype,fog,window", [(32, torch.bfloat16, "vscale", 0),
+                                                         (64, torch.float16, "bias", 37),
+                                                         (128, torch.bfloat16, "vscale", 0)])
+def test_prefill_larger_pages(dev, page_size, dtype, fog, window):
+    """Pages of 32, 64 and 128 tokens (the generic kernel: the MFMA prefill
+    takes 16-token pages), ragged contexts: against the oracle."""
+    from kessie_amd import ops
+
+    q, pool, table, lens = _case(dev, 2, 100, [1000, 777], 32, 8, dtype, seed=31, page_size=page_size)
+    vs = build_fog_weights(1000).to(dev) if fog == "vscale" else None
+    bias = fog_bias(1000, 0.5, 0.5, {3, 500}, 0.1).to(dev) if fog == "bias" else None
+    out = ops.fog_prefill(q, pool, table, lens, 1000, fog_vscale=vs, fog_bias=bias, window=window)
+    torch.cuda.synchronize()
+    ref = paged_prefill_ref(q.cpu(), pool.cpu(), table.cpu(), lens.cpu(), None if vs is None else vs.cpu(),
+                            None if bias is None else bias.cpu(), window)
+    _check(out, ref, dtype)
+
+
+def test_prefill_larger_pages_bad_page(dev):
+    """An invalid page id in a table of 32-token pages masks all 32 of its
+    tokens: non-causal, so the oracle is the same context without that page."""
+    from kessie_amd import ops
+
+    q, pool, table, lens = _case(dev, 1, 40, [400], 32, 8, torch.bfloat16, seed=7, page_size=32)
+    table[0, 3] = -1
+    out = ops.fog_prefill(q, pool, table, lens, 400, causal=False)
+    torch.cuda.synchronize()
+    keep = [i for i in range(table.shape[1]) if i != 3]
+    ref = paged_prefill_ref(q.cpu(), pool.cpu(), table.cpu()[:, keep].contiguous(), torch.tensor([400 - 32]),
+                            causal=False)
+    _check(out, ref, torch.bfloat16)
+
+
+def test_prefill_larger_pages_varlen_declined(dev):
+    """The varlen entry runs only on the MFMA kernel, which takes 16-token
+    pages: with 32-token pages it launches nothing and reports it, and the
+    per-sequence call (generic kernel) matches the oracle."""
+    from kessie_amd import ops
+
+    _, pool, table, lens = _case(dev, 2, 1, [300, 200], 32, 8, torch.bfloat16, seed=33, page_size=32)
+    qsl = torch.tensor([0, 24, 40], dtype=torch.int32, device=dev)
+    q = torch.randn(40, 32, 128, generator=gen(dev, 34), device=dev).bfloat16()
+    out = torch.full_like(q, 7.0)
+    assert not ops.fog_prefill_varlen(q, qsl, 24, pool, table, lens, 300, out=out)
+    torch.cuda.synchronize()
+    assert torch.all(out == 7.0)
+    qi = q[:24].unsqueeze(0).contiguous()
+    one = ops.fog_prefill(qi, pool, table[:1].contiguous(), lens[:1], 300)
+    torch.cuda.synchronize()
+    _check(one, paged_prefill_ref(qi.cpu(), pool.cpu(), table[:1].cpu(), lens[:1].cpu()), torch.bfloat16)
 
 
 def test_prefill_mfma_matches_generic(dev, monkeypatch):
