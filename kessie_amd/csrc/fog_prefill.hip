@@ -1,5 +1,5 @@
 // Chunked-prefill fog attention on MFMA for gfx950 (bf16 / f16, head_dim 128,
-// 16-token pages, GQA ratio 1/2/4/8/16, sm_scale > 0).
+// pages of 16 * 2^k tokens, GQA ratio 1/2/4/8/16, sm_scale > 0).
 //
 // Math: the last C rows of kessie_hip_kernels.py:577-593 over ctx = L + C
 // tokens (query i at position ctx-C+i, causal, window, fog weights scaling V
@@ -39,7 +39,8 @@
 //   kMode    0 paged; 1 table-less pages (page b * dense_ppb + j) for the
 //            reference's dense [B][H][N][D] launchers, query tiles longest
 //            first; 2 paged with query tiles longest first (a causal chunk
-//            that is most of its context and takes several grid rounds).
+//            that is most of its context and takes several grid rounds); 3
+//            paged with pages of 32, 64, ... tokens, read as 16-token blocks.
 #include "attn_common.h"
 
 namespace kessie {
@@ -156,6 +157,7 @@ template <typename T, int G, bool kBias, bool kVs, bool kSplit, int kMode, int k
 __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
   static_assert(kD == 128 || kD == 64, "head_dim 128, or 64 on table-less pages");
   constexpr bool kDense = kMode == 1;
+  constexpr bool kBig = kMode == 3;  // pages of 16 * 2^k tokens, k >= 1
   constexpr int kKRow = PfGeom<kD>::kKRow;
   constexpr int kKStage = PfGeom<kD>::kKStage;
   constexpr int kVStage = PfGeom<kD>::kVStage;
@@ -287,6 +289,14 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
   const bool vload = kD == 128 || wave < 4;
   const int vkey_off = 2 * kp;  // this thread's first V key in a tile
 
+  // The loop runs over 16-token blocks.  With pages of 16 * 2^psh tokens
+  // (kBig), block j is rows 16 * (j & pmask) of page table[j >> psh], and its
+  // id is (page << psh) | (j & pmask), or -1 for an invalid page; otherwise the
+  // id is the page id.  (A separate instance: the extra scalar work per tile
+  // cost the 16-token instances 3-4.5 %.)
+  const int psh = kBig ? __builtin_ctz((unsigned)p.page_size) - 4 : 0;
+  const int pmask = (1 << psh) - 1;
+  const uint32_t n_ids = kBig ? (uint32_t)p.num_pages << psh : (uint32_t)p.num_pages;
   // Page ids of a tile (4 uniform values; -1 past the end).  The table index
   // is clamped into the readable entries and the value replaced afterwards, so
   // the four scalar loads issue back to back with no branch around them.
@@ -296,8 +306,11 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const bool in = tile < n_tiles && pg0 + j < n_tab;
-      if (kDense) {
+      if constexpr (kDense) {
         ids[j] = in ? dense0 + pg0 + j : -1;
+      } else if constexpr (kBig) {
+        const int e = table[min(pg0 + j, n_tab - 1) >> psh];
+        ids[j] = in && (uint32_t)e < (uint32_t)p.num_pages ? (e << psh) | ((pg0 + j) & pmask) : -1;
       } else {
         const int e = table[min(pg0 + j, n_tab - 1)];
         ids[j] = in ? e : -1;
@@ -308,7 +321,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
   auto valid_mask = [&](i32x4 ids) {
     int m = 0;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) m |= (uint32_t)uniform(ids[j]) < (uint32_t)p.num_pages ? (1 << j) : 0;
+    for (int j = 0; j < 4; ++j) m |= (uint32_t)uniform(ids[j]) < n_ids ? (1 << j) : 0;
     return m;
   };
   auto slot_id = [&](i32x4 ids, int slot) {
@@ -332,8 +345,10 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
   const uint32_t voff0 = (uint32_t)((vkey_off & 15) * ts_b + 16 * kc), voff1 = voff0 + (uint32_t)ts_b;
   auto page_rsrc = [&](const char* pool, int pid, int first_tok) {
     const int nrows = min(max(hi - first_tok, 0), 16);
-    const bool ok = (uint32_t)pid < (uint32_t)p.num_pages && nrows > 0;
-    const char* base = ok ? pool + (int64_t)pid * p.page_stride * (int64_t)sizeof(T) : pool;
+    const bool ok = (uint32_t)pid < n_ids && nrows > 0;
+    int64_t at = (int64_t)pid * p.page_stride;
+    if constexpr (kBig) at = (int64_t)(pid >> psh) * p.page_stride + (int64_t)((pid & pmask) << 4) * p.tok_stride;
+    const char* base = ok ? pool + at * (int64_t)sizeof(T) : pool;
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), (short)0, ok ? (nrows - 1) * ts_b + kRowB : 0,
                                              kRsrcWord3);
   };
@@ -669,6 +684,8 @@ int launch_fog(const Params& p, dim3 grid, hipStream_t stream) {
 // V-fog long-context shape 1-6 %).
 template <typename T, int G>
 int launch_split(const Params& p, dim3 grid, hipStream_t stream) {
+  if (p.page_size > 16)  // pages of 16 * 2^k tokens (in query order)
+    return p.direct_out ? launch_fog<T, G, false, 3>(p, grid, stream) : launch_fog<T, G, true, 3>(p, grid, stream);
   if (!p.direct_out) return launch_fog<T, G, true>(p, grid, stream);
   return p.reverse_q ? launch_fog<T, G, false, 2>(p, grid, stream) : launch_fog<T, G, false>(p, grid, stream);
 }
@@ -703,7 +720,11 @@ bool prefill_mfma_ok(const Params& p, int dtype) {
   if (env_int("KESSIE_FORCE_GENERIC", 0)) return false;
   if (dtype != KESSIE_DTYPE_BF16 && dtype != KESSIE_DTYPE_F16) return false;
   // Head_dim 64 only on table-less pages (the dense launchers).
-  if (!(p.D == 128 || (p.D == 64 && p.page_table == nullptr)) || p.page_size != 16) return false;
+  if (!(p.D == 128 || (p.D == 64 && p.page_table == nullptr))) return false;
+  // Pages of 16 * 2^k tokens (table-less pages: 16), block ids (page << k) below 2^31.
+  if (p.page_size < 16 || (p.page_size & (p.page_size - 1)) != 0 || (p.page_table == nullptr && p.page_size != 16))
+    return false;
+  if (((int64_t)p.num_pages << (__builtin_ctz((unsigned)p.page_size) - 4)) >= (int64_t)1 << 31) return false;
   // Table-less pages: instantiated for the dense launchers' form only.
   if (p.page_table == nullptr && (p.dense_ppb <= 0 || p.G != 1 || p.bias || p.num_splits > 1)) return false;
   if (!(p.G == 1 || p.G == 2 || p.G == 4 || p.G == 8 || p.G == 16)) return false;

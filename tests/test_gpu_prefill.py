@@ -108,8 +108,8 @@ def test_prefill_fp32_generic(dev):
                                                          (64, torch.float16, "bias", 37),
                                                          (128, torch.bfloat16, "vscale", 0)])
 def test_prefill_larger_pages(dev, page_size, dtype, fog, window):
-    """Pages of 32, 64 and 128 tokens (the generic kernel: the MFMA prefill
-    takes 16-token pages), ragged contexts: against the oracle."""
+    """Pages of 32, 64 and 128 tokens on the MFMA kernel (read as 16-token
+    blocks), ragged contexts: against the oracle."""
     from kessie_amd import ops
 
     q, pool, table, lens = _case(dev, 2, 100, [1000, 777], 32, 8, dtype, seed=31, page_size=page_size)
@@ -137,23 +137,43 @@ def test_prefill_larger_pages_bad_page(dev):
     _check(out, ref, torch.bfloat16)
 
 
-def test_prefill_larger_pages_varlen_declined(dev):
-    """The varlen entry runs only on the MFMA kernel, which takes 16-token
-    pages: with 32-token pages it launches nothing and reports it, and the
-    per-sequence call (generic kernel) matches the oracle."""
+def test_prefill_larger_pages_varlen_and_split(dev, monkeypatch):
+    """32-token pages: the varlen entry takes them (it launches only on the
+    MFMA kernel) and matches per-sequence launches bit for bit at a forced key
+    split, and both match the oracle."""
     from kessie_amd import ops
 
-    _, pool, table, lens = _case(dev, 2, 1, [300, 200], 32, 8, torch.bfloat16, seed=33, page_size=32)
-    qsl = torch.tensor([0, 24, 40], dtype=torch.int32, device=dev)
-    q = torch.randn(40, 32, 128, generator=gen(dev, 34), device=dev).bfloat16()
-    out = torch.full_like(q, 7.0)
-    assert not ops.fog_prefill_varlen(q, qsl, 24, pool, table, lens, 300, out=out)
+    p, c = 32, 64
+    ctxs = [3000, 1500]
+    _, pool, table, lens = _case(dev, 2, 1, ctxs, 32, 8, torch.bfloat16, seed=33, page_size=p)
+    chunks = [c, 40]
+    qsl = torch.tensor([0, chunks[0], chunks[0] + chunks[1]], dtype=torch.int32, device=dev)
+    q = torch.randn(sum(chunks), 32, 128, generator=gen(dev, 34), device=dev).bfloat16()
+    monkeypatch.setenv("KESSIE_PREFILL_SPLITS", "3")
+    out = torch.zeros_like(q)
+    assert ops.fog_prefill_varlen(q, qsl, c, pool, table, lens, max(ctxs), out=out)
     torch.cuda.synchronize()
-    assert torch.all(out == 7.0)
-    qi = q[:24].unsqueeze(0).contiguous()
-    one = ops.fog_prefill(qi, pool, table[:1].contiguous(), lens[:1], 300)
+    for i in range(2):
+        qi = q[qsl[i]:qsl[i + 1]].unsqueeze(0).contiguous()
+        one = ops.fog_prefill(qi, pool, table[i:i + 1].contiguous(), lens[i:i + 1], ctxs[i])
+        torch.cuda.synchronize()
+        assert torch.equal(out[qsl[i]:qsl[i + 1]], one[0])
+        ref = paged_prefill_ref(qi.cpu(), pool.cpu(), table[i:i + 1].cpu(), lens[i:i + 1].cpu())
+        _check(one, ref, torch.bfloat16)
+
+
+def test_prefill_larger_pages_match_generic(dev, monkeypatch):
+    """The MFMA kernel on 64-token pages against the generic kernel on the same
+    inputs (the generic one takes any page size)."""
+    from kessie_amd import ops
+
+    q, pool, table, lens = _case(dev, 2, 150, [2000, 1500], 32, 8, torch.bfloat16, seed=35, page_size=64)
+    fog = build_fog_weights(2000).to(dev)
+    a = ops.fog_prefill(q, pool, table, lens, 2000, fog_vscale=fog)
+    monkeypatch.setenv("KESSIE_FORCE_GENERIC", "1")
+    b = ops.fog_prefill(q, pool, table, lens, 2000, fog_vscale=fog)
     torch.cuda.synchronize()
-    _check(one, paged_prefill_ref(qi.cpu(), pool.cpu(), table[:1].cpu(), lens[:1].cpu()), torch.bfloat16)
+    assert (a.float() - b.float()).abs().max().item() < 2e-2
 
 
 def test_prefill_mfma_matches_generic(dev, monkeypatch):
