@@ -139,9 +139,9 @@ def test_fog_cache_generations(dev, dtype):
     assert f32.dtype == torch.float32 and torch.equal(f32, b4.view(-1).float())
 
 
-def _mixed_batch(dev, order, seed=0):
-    """Sequences (query_len, ctx) in ``order``; blocks drawn at random."""
-    hq, hkv, d, p, nb = 32, 8, 128, 16, 96
+def _mixed_batch(dev, order, seed=0, p=16):
+    """Sequences (query_len, ctx) in ``order``; blocks of ``p`` tokens drawn at random."""
+    hq, hkv, d, nb = 32, 8, 128, 96
     spec = {"d0": (1, 300), "pf": (37, 500), "d1": (1, 77)}
     seqs = [spec[k] for k in order]
     width = 32
@@ -174,13 +174,16 @@ def _mixed_batch(dev, order, seed=0):
     return seqs, qsl, kv_cache, query, key, value, meta
 
 
-@pytest.mark.parametrize("order,fog", [(("d0", "pf", "d1"), True), (("d0", "d1", "pf"), True),
-                                       (("pf", "d0"), False)])
-def test_attention_impl_forward(dev, monkeypatch, order, fog):
+@pytest.mark.parametrize("order,fog,p", [(("d0", "pf", "d1"), True, 16), (("d0", "d1", "pf"), True, 16),
+                                         (("pf", "d0"), False, 16), (("d0", "pf", "d1"), True, 32)])
+def test_attention_impl_forward(dev, monkeypatch, order, fog, p):
+    """A mixed batch through KeSSieAttentionImpl.forward: slot-mapped cache
+    write, decode rows and one varlen prefill launch, against the oracle
+    (16- and 32-token blocks)."""
     from kessie_amd import kessie_attention as ka
 
     hq, hkv, d = 32, 8, 128
-    seqs, qsl, kv_cache, query, key, value, meta = _mixed_batch(dev, order)
+    seqs, qsl, kv_cache, query, key, value, meta = _mixed_batch(dev, order, p=p)
     state = ka.KeSSieAttentionState()
     state.update(prompt_len=100 if fog else 0, recall_positions={5, 250})
     monkeypatch.setattr(ka, "KESSIE_STATE", state)
@@ -194,8 +197,8 @@ def test_attention_impl_forward(dev, monkeypatch, order, fog):
     # The new rows landed in their slots and nothing else changed.
     ref_cache = before.cpu()
     sl = meta.slot_mapping.cpu()
-    ref_cache[0, sl // 16, sl % 16] = key.cpu()
-    ref_cache[1, sl // 16, sl % 16] = value.cpu()
+    ref_cache[0, sl // p, sl % p] = key.cpu()
+    ref_cache[1, sl // p, sl % p] = value.cpu()
     assert torch.equal(kv_cache.cpu(), ref_cache)
 
     pool = ref_cache.permute(1, 2, 0, 3, 4).contiguous()  # native [pages, P, 2, H, D]
