@@ -328,6 +328,63 @@ def test_connector_save_and_recall(dev, monkeypatch, remap):
         assert torch.equal(kf[:, mask].cpu(), bf[:, mask].cpu())
 
 
+@pytest.mark.parametrize("remap", [False, True])
+def test_connector_save_and_recall_32_token_blocks(dev, monkeypatch, remap):
+    """The save and recall-inject path with 32-token blocks (both vLLM cache
+    layouts): a 72-token sequence saved block by block, positions 32..71 recalled
+    into two fresh blocks at positions 0..39 (K re-rotated by -32 when remapping)."""
+    from kessie_amd import kessie_kv_connector as kc
+
+    monkeypatch.setattr(kc, "_KESSIE_STORE", None)
+    monkeypatch.setattr(kc, "_RECALL_STATES", {})
+    theta, p = 10000.0, 32
+    extra = {"max_cpu_gb": 1}
+    if remap:
+        extra["rope_theta"] = theta
+    conn = kc.KeSSieKVConnector(kv_connector_extra_config=extra)
+    kv = {"L0": randn((2, 16, p, 8, 128), torch.bfloat16, dev, 11),
+          "L1": randn((16, 2, p, 8, 128), torch.bfloat16, dev, 12)}
+    conn.register_kv_caches(kv)
+    table = torch.tensor([[3, 7, 1]], dtype=torch.int32, device=dev)
+    meta = _Meta(table, torch.tensor([72], dtype=torch.int32, device=dev),
+                 torch.tensor([table[0, t // p].item() * p + t % p for t in range(72)], device=dev))
+    for name, cache in kv.items():
+        conn.save_kv_layer(name, cache, meta)
+    conn.wait_for_save()
+    for name, cache in kv.items():
+        kf = cache if name == "L0" else cache.transpose(0, 1)
+        for bid, pos, tok in [(3, 0, 32), (7, 32, 32), (1, 64, 8)]:
+            blk = conn.store.get_blocks_for_positions(pos, pos + tok, name)
+            assert blk is not None and blk.block_id == bid
+            assert torch.equal(blk.kv_data, kf[:, bid, :tok].cpu())
+    saved = {name: [conn.store.get_blocks_for_positions(pos, 0, name).kv_data.clone() for pos in (32, 64)]
+             for name in kv}
+
+    kc._RECALL_STATES["r"] = kc.RecallState(request_id="r", recalled_positions=[(32, 64), (64, 96)],
+                                            num_recalled_tokens=40, load_pending=True, target_block_ids=[10, 11])
+    before = {n: c.clone() for n, c in kv.items()}
+    conn.start_load_kv()
+    for name in kv:
+        conn.wait_for_layer_load(name)
+    torch.cuda.synchronize()
+    assert not kc._RECALL_STATES["r"].load_pending
+    for name, cache in kv.items():
+        kf = cache if name == "L0" else cache.transpose(0, 1)
+        bf = before[name] if name == "L0" else before[name].transpose(0, 1)
+        want = torch.cat(saved[name], dim=1)  # [2, 40, H, D]
+        got = torch.cat([kf[:, 10, :32], kf[:, 11, :8]], dim=1).cpu()
+        assert torch.equal(got[1], want[1])  # V is copied unchanged
+        if not remap:
+            assert torch.equal(got[0], want[0])
+        else:
+            k_ref = want[0].clone()
+            rope_remap_ref(k_ref, torch.arange(32, 72, dtype=torch.int32), torch.arange(40, dtype=torch.int32), theta)
+            assert (got[0].float() - k_ref.float()).abs().max().item() <= 2e-2
+        mask = torch.ones(16, dtype=torch.bool)
+        mask[[10, 11]] = False
+        assert torch.equal(kf[:, mask].cpu(), bf[:, mask].cpu())
+
+
 @pytest.mark.parametrize("mode", ["written", "all"])
 def test_connector_save_blocks_modes(dev, monkeypatch, mode):
     """A step that wrote only the last block: the default mode saves that
