@@ -953,7 +953,9 @@ int device_cus() {
 int decode_splits(int B, int Hkv, int max_ctx, int page_size) {
   const int target = env_int("KESSIE_DECODE_WGS", kDecWgsPerCu * device_cus());
   const int units = B * div_up(Hkv, kDecWaves);
-  const int pages = div_up(max(max_ctx, 1), max(page_size, 1));
+  // Counted in 16-token blocks, the unit the MFMA decode streams (pages of
+  // 16 * 2^k tokens hold 2^k of them); smaller pages count as they are.
+  const int pages = div_up(max(max_ctx, 1), max(min(page_size, 16), 1));
   int s = div_up(target, max(units, 1));
   // At least 2 pages per split: short contexts are latency-bound, so more,
   // shorter splits win (one 4K sequence: bf16 step 23.0 -> 17.8 us, fp32
