@@ -985,7 +985,7 @@ int prefill_mfma_splits(int B, int C, int Hkv, int G, int max_ctx) {
 int prefill_splits(int B, int C, int Hkv, int G, int max_ctx, int page_size) {
   const int target = env_int("KESSIE_PREFILL_WGS", 1024);
   const int units = B * Hkv * div_up(C * G, kGenRT);
-  const int pages = div_up(max(max_ctx, 1), max(page_size, 1));
+  const int pages = div_up(max(max_ctx, 1), max(min(page_size, 16), 1));  // 16-token blocks, as in decode_splits
   int s = div_up(target, max(units, 1));
   s = min(s, max(1, pages / 8));
   s = min(s, kMaxSplits);
