@@ -23,11 +23,17 @@ def _check(got, ref):
     assert not bad.any(), f"{int(bad.sum())}/{bad.numel()} outside tol, max diff {diff.max().item():.3e}"
 
 
-def _setup(dev, rng, b, ctxs, hkv, dtype, seed):
-    pages = [max(1, -(-c // 16)) for c in ctxs]
+def _page_size(seed):
+    """16, 32 or 64-token pages, drawn apart from the other shape choices so
+    that a seed's other draws do not depend on it."""
+    return random.Random(5000 + seed).choice([16, 16, 32, 64])
+
+
+def _setup(dev, rng, b, ctxs, hkv, dtype, seed, p=16):
+    pages = [max(1, -(-c // p)) for c in ctxs]
     w = max(pages)
     num_pages = sum(pages) + rng.randint(0, 5)
-    pool = paged_pool(num_pages, 16, hkv, 128, dtype, dev, seed)
+    pool = paged_pool(num_pages, p, hkv, 128, dtype, dev, seed)
     perm = randperm(num_pages, dev, seed + 1)
     table = torch.full((b, w), -1, dtype=torch.int32, device=dev)
     at = 0
@@ -55,7 +61,7 @@ def test_random_decode(dev, seed):
     ctxs = [rng.choice([0, 1, 15, 16, 17, rng.randint(2, 3000)]) for _ in range(b)]
     mx = max(max(ctxs), 1)
     window = rng.choice([0, 0, 1, 16, rng.randint(2, 2000)])
-    pool, table, lens = _setup(dev, rng, b, ctxs, hkv, dtype, seed)
+    pool, table, lens = _setup(dev, rng, b, ctxs, hkv, dtype, seed, _page_size(seed))
     mode, vs, bias = _fog(dev, rng, b, mx, seed)
     q = torch.randn(b, hq, 128, generator=gen(dev, seed + 9), device=dev).to(dtype)
     out = ops.fog_decode(q, pool, table, lens, max_ctx=mx, fog_vscale=vs, fog_bias=bias, window=window)
@@ -78,7 +84,7 @@ def test_random_prefill(dev, seed):
     mx = max(ctxs)
     window = rng.choice([0, 0, 1, 33, rng.randint(2, 1500)])
     causal = rng.random() < 0.85
-    pool, table, lens = _setup(dev, rng, b, ctxs, hkv, dtype, seed)
+    pool, table, lens = _setup(dev, rng, b, ctxs, hkv, dtype, seed, _page_size(seed))
     mode, vs, bias = _fog(dev, rng, b, mx, seed)
     q = torch.randn(b, c, hq, 128, generator=gen(dev, seed + 9), device=dev).to(dtype)
     out = ops.fog_prefill(q, pool, table, lens, mx, fog_vscale=vs, fog_bias=bias, window=window, causal=causal)
