@@ -81,6 +81,23 @@ def test_loads_and_reports_errors_without_gpu():
     assert lib.kessie_page_workspace_bytes(65536) >= 65536 * 4
 
 
+def test_decode_splits_counted_in_16_token_blocks():
+    """The decode's split count (and so its workspace) is taken in 16-token
+    blocks, so pages of 32 or 64 tokens split a context as 16-token pages do;
+    smaller pages count as they are.  Host computation (the CU count falls back
+    to 256 without a device)."""
+    from kessie_amd import _lib
+
+    lib = _lib.load()
+    for b, ctx in [(1, 4096), (1, 16384), (16, 131072), (3, 1000)]:
+        s16 = lib.kessie_fog_decode_num_splits(b, 8, ctx, 16)
+        assert lib.kessie_fog_decode_num_splits(b, 8, ctx, 32) == s16
+        assert lib.kessie_fog_decode_num_splits(b, 8, ctx, 64) == s16
+        assert (lib.kessie_fog_decode_workspace_bytes(b, 32, 8, 128, ctx, 32, 1)
+                == lib.kessie_fog_decode_workspace_bytes(b, 32, 8, 128, ctx, 16, 1))
+    assert lib.kessie_fog_decode_num_splits(1, 8, 64, 8) == 4  # 8 pages of 8 tokens: at least 2 per split
+
+
 def test_ctypes_class_mirrors_reference_surface():
     from kessie_amd.kessie_hip_ctypes import KeSSieKernels
 
