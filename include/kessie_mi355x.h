@@ -324,8 +324,10 @@ int kessie_page_workspace_init(void* workspace, size_t workspace_bytes,
  * else floor(evict_fraction * n_valid) computed in double.  Evicted pages get
  * page_valid=0; their ids go to evict_list ascending; k to *evict_count.
  * Deterministic: no order depends on atomics.  One launch whose workgroups
- * meet at bounded grid barriers (*evict_count reads -1 if the device could
- * not run them at once); the workspace must have been prepared by
+ * meet at bounded grid barriers: if the device could not run them at once,
+ * *evict_count reads -1 and nothing else is written (page_valid and
+ * evict_list are left as they were, so the call can be retried); the
+ * workspace must have been prepared by
  * kessie_page_workspace_init (-2 otherwise).  num_pages below 2^29 (else
  * KESSIE_ERR_UNSUPPORTED).  (The reference only has the threshold predicate,
  * kessie_kernels_v2.hip:393-407; this applies it with an exact
@@ -358,8 +360,10 @@ int kessie_page_compact(const int32_t* tables, const int32_t* lens,
  * Workspace: kessie_page_workspace_bytes(max(num_pages, num_seqs)), prepared
  * by kessie_page_workspace_init (else both counts read -2).  The launch's
  * workgroups (at most 64) wait for each other at bounded grid barriers; if
- * the device cannot run them at once the wait runs out (~0.1 s each), the
- * outputs are undefined and *evict_count and *gather_count read -1.  (The reference evicts by threshold only and compacts nothing,
+ * the device cannot run them at once the wait runs out (~0.1 s each),
+ * *evict_count and *gather_count read -1 and no other output is written
+ * (page_valid, evict_list, new_tables, new_lens and gather_idx are left as
+ * they were, so the call can be retried).  (The reference evicts by threshold only and compacts nothing,
  * kessie_hip_kernels.py:526-564; the caller this serves is the page
  * manager's evict-then-gather step.) */
 int kessie_page_evict_compact(const float* scores, int8_t* page_valid,

@@ -174,7 +174,13 @@ __global__ __launch_bounds__(kThreads) void compact_write_kernel(PredArgs a, int
 // histogram and candidate atomics only count: no result depends on their
 // order.  Each barrier wait is bounded (~0.1 s); a wait that runs out (only
 // possible if the device could not hold the G workgroups at once) marks the
-// call failed and the evict count reads -1.
+// call failed and the evict count reads -1.  The mark is a bit of the barrier
+// word itself, set by compare-and-swap only while the barrier is incomplete,
+// so it precedes the last arrival in that word's modification order and every
+// workgroup reads it after its last barrier: all of them see the failure, or
+// none.  A failed call writes none of its outputs (page_valid, the evict
+// list, the tables, the gather indices), so page_valid is left as it was and
+// the call can be retried.
 // Every workgroup loads its keys once, in P1 -- the 4,096 keys of its tile
 // (4 per thread) and the page keys of its table-row entries (one 1,024-entry
 // chunk per thread per row) -- and keeps them in registers, so P2-P4 touch
@@ -196,6 +202,7 @@ constexpr int kSelTile = kSelThreads * kSelPer;
 constexpr int kFusedMaxG = 64;                // workgroups of the fused launch
 constexpr int kFusedMaxRows = 8192;           // table rows whose offsets fit in LDS
 constexpr int kSpinLimit = 1 << 21;           // barrier polls (s_sleep 2 each: ~0.1 s)
+constexpr unsigned kBarFail = 0x80000000u;    // bit of FusedScratch::bar: a barrier wait ran out
 
 // Scratch of the fused launch, at the start of the page workspace.  It is
 // zero apart from `magic` between calls: kessie_page_workspace_init writes
@@ -204,9 +211,9 @@ constexpr int kSpinLimit = 1 << 21;           // barrier polls (s_sleep 2 each: 
 constexpr unsigned kScratchMagic = 0x4b535331u;
 struct FusedScratch {
   unsigned magic;  // kScratchMagic once initialised
-  unsigned bar;    // grid-barrier arrivals
+  unsigned bar;    // grid-barrier arrivals (| kBarFail once a wait ran out)
   unsigned done;   // workgroups past their last read of this scratch
-  int timed_out;
+  int unused;
   int n_valid;
   int ncand;
   int hist[kSelBins];
@@ -303,26 +310,38 @@ __global__ __launch_bounds__(kThreads) void scratch_init_kernel(FusedScratch* fs
   if (threadIdx.x == 0) {
     fs->bar = 0;
     fs->done = 0;
-    fs->timed_out = 0;
+    fs->unused = 0;
     fs->n_valid = 0;
     fs->ncand = 0;
     fs->magic = kScratchMagic;
   }
 }
 
-// All G workgroups arrive; returns once arrivals reach `target` or the bounded
-// wait runs out (then fs->timed_out is set).  Release/acquire at agent scope
-// make every write before the barrier visible to every workgroup after it.
-__device__ __forceinline__ void grid_barrier(FusedScratch* fs, unsigned target) {
+// All G workgroups arrive; returns once arrivals reach `target`, or once the
+// bounded wait (`spin_limit` polls) has run out and the failure is recorded in
+// fs->bar (or another workgroup recorded one).  The failure bit is set by
+// compare-and-swap only on a value whose count is below `target`, so it is
+// ordered before the barrier's last arrival: a workgroup that passes any later
+// barrier, or reads fs->bar after its own last arrival, sees it.
+// Release/acquire at agent scope make every write before the barrier visible
+// to every workgroup after it.
+__device__ __forceinline__ void grid_barrier(FusedScratch* fs, unsigned target, int spin_limit) {
   __syncthreads();
   if (threadIdx.x == 0) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
     __hip_atomic_fetch_add(&fs->bar, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     int spins = 0;
-    while (__hip_atomic_load(&fs->bar, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-      __builtin_amdgcn_s_sleep(2);
-      if (++spins > kSpinLimit) {
-        __hip_atomic_store(&fs->timed_out, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    unsigned v = __hip_atomic_load(&fs->bar, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // Every pass either polls (at most spin_limit times), or attempts the
+    // swap, which fails only when another arrival or failure changed fs->bar
+    // (finitely many per call): the loop always ends.
+    while ((v & ~kBarFail) < target && (v & kBarFail) == 0) {
+      if (spins < spin_limit) {
+        ++spins;
+        __builtin_amdgcn_s_sleep(2);
+        v = __hip_atomic_load(&fs->bar, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      } else if (__hip_atomic_compare_exchange_strong(&fs->bar, &v, v | kBarFail, __ATOMIC_RELAXED,
+                                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
         break;
       }
     }
@@ -354,6 +373,8 @@ struct FusedArgs {
   uint32_t* cand_i;
   int* row_count;
   int tiles_per_wg;
+  int spin_limit;     // polls per barrier wait before the call is marked failed
+  int extra_arrival;  // 1: the first barrier waits for one arrival more than the grid has (test hook)
 };
 
 // LDS of the fused kernel, in 32-bit words: P1/P2 use the first kSelBins as
@@ -379,7 +400,7 @@ template <int kTR>
 __global__ __launch_bounds__(kSelThreads) void sel_fused_kernel(FusedArgs a) {
   __shared__ uint32_t smem[kFusedLdsWords];
   __shared__ int sm[kSelWaves + 1];
-  __shared__ int s_digit, s_rank, s_id, s_base;
+  __shared__ int s_digit, s_rank, s_id, s_base, s_fail;
   FusedScratch* fs = a.fs;
   const int tid = threadIdx.x;
   const int G = gridDim.x;
@@ -498,6 +519,12 @@ __global__ __launch_bounds__(kSelThreads) void sel_fused_kernel(FusedArgs a) {
     return;
   }
   for (int e = tid; e < kSelBins; e += kSelThreads) lhist[e] = 0;
+  // (A call that has failed at a barrier may pick from incomplete counts, where
+  // no bin holds the rank: the picks then keep these in-range values.)
+  if (tid == 0) {
+    s_digit = 0;
+    s_rank = 0;
+  }
   __syncthreads();
   int c = 0;
   for (int t = t_begin; t < t_end; ++t) {
@@ -520,7 +547,7 @@ __global__ __launch_bounds__(kSelThreads) void sel_fused_kernel(FusedArgs a) {
   if (t_end > t_begin)
     for (int e = tid; e < kSelBins; e += kSelThreads)
       if (lhist[e]) atomicAdd(&fs->hist[e], lhist[e]);
-  grid_barrier(fs, (unsigned)G);
+  grid_barrier(fs, (unsigned)(G + a.extra_arrival), a.spin_limit);
 #pragma unroll
   for (int u = 0; u < kRowRegs; ++u)
     rk[u] = rid[u] >= 0 && rid[u] < a.n && rv[u] == 1 ? ordered_score(rsc[u]) : 0xFFFFFFFFu;
@@ -584,7 +611,7 @@ __global__ __launch_bounds__(kSelThreads) void sel_fused_kernel(FusedArgs a) {
       __syncthreads();  // s_base and sm are reused by the next tile
     }
   }
-  grid_barrier(fs, 2u * G);
+  grid_barrier(fs, 2u * G, a.spin_limit);
 
   // P3: the threshold key (identical in every workgroup), then the counts.
   unsigned long long key_thr = 0;
@@ -727,12 +754,16 @@ __global__ __launch_bounds__(kSelThreads) void sel_fused_kernel(FusedArgs a) {
       __syncthreads();
     }
   }
-  grid_barrier(fs, 3u * G);
+  grid_barrier(fs, 3u * G, a.spin_limit);
 
   // P4: read what the other workgroups published, leave the scratch, then
   // write the evict list (ascending ids, clearing the pages' valid flags) and
   // the compacted tables.
-  const bool failed = __hip_atomic_load(&fs->timed_out, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+  // (Read by one thread: every workgroup reads fs->bar here after its own last
+  // arrival, so all of them get the same answer.)
+  if (tid == 0) s_fail = (__hip_atomic_load(&fs->bar, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & kBarFail) != 0;
+  __syncthreads();
+  const bool failed = s_fail != 0;
   if (tid < 64) {
     int v = 0;
     if (tid < g) v = __hip_atomic_load(&fs->wg_evict[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -762,10 +793,17 @@ __global__ __launch_bounds__(kSelThreads) void sel_fused_kernel(FusedArgs a) {
     if (tid == 0) {
       __hip_atomic_store(&fs->bar, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(&fs->done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(&fs->timed_out, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(&fs->n_valid, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(&fs->ncand, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+  }
+  if (failed) {
+    // Outputs untouched: only the counts report the failure.
+    if (g == 0 && tid == 0) {
+      if (tables) *a.gather_count = -1;
+      *a.evict_count = -1;
+    }
+    return;
   }
   int carry = s_base;
   for (int t = t_begin; t < t_end; ++t) {
@@ -827,9 +865,9 @@ __global__ __launch_bounds__(kSelThreads) void sel_fused_kernel(FusedArgs a) {
         if (tid == 0) a.new_lens[row] = rc;
       }
     }
-    if (g == 0 && tid == 0) *a.gather_count = failed ? -1 : run;
+    if (g == 0 && tid == 0) *a.gather_count = run;
   }
-  if (g == 0 && tid == 0) *a.evict_count = failed ? -1 : k;
+  if (g == 0 && tid == 0) *a.evict_count = k;
 }
 
 // ---------------------------------------------------------------------------
@@ -1303,8 +1341,22 @@ int insert_dispatch(InsertArgs& a, int dtype, hipStream_t s) {
   return KESSIE_ERR_UNSUPPORTED;
 }
 
-// Score eviction (+ table compaction when tables != nullptr): the clear launch
-// and the fused launch.
+// Test hook: KESSIE_GRID_TEST_TIMEOUT=<polls> makes the fused launch's first
+// grid barrier wait for one arrival more than the grid has, giving up after
+// <polls> polls, so a test drives the failure path deterministically while
+// every workgroup still exits normally.  Unset: the full bounded wait.
+void grid_test_hook(int* spin_limit, int* extra_arrival) {
+  const char* v = getenv("KESSIE_GRID_TEST_TIMEOUT");
+  if (v == nullptr || *v == '\0') {
+    *spin_limit = kSpinLimit;
+    *extra_arrival = 0;
+    return;
+  }
+  *spin_limit = min(max(0, atoi(v)), kSpinLimit);
+  *extra_arrival = 1;
+}
+
+// Score eviction (+ table compaction when tables != nullptr): the fused launch.
 int select_dispatch(const float* scores, int8_t* page_valid, int num_pages, int k_evict, float evict_fraction,
                     int32_t* evict_list, int32_t* evict_count, const int32_t* tables, const int32_t* lens,
                     int num_seqs, int table_stride, int32_t* new_tables, int32_t* new_lens, int32_t* gather_idx,
@@ -1323,7 +1375,9 @@ int select_dispatch(const float* scores, int8_t* page_valid, int num_pages, int 
   const int G = max(1, min(kFusedMaxG, ntiles));
   FusedArgs a{scores,       page_valid, num_pages, k_evict,  evict_fraction, evict_list, evict_count,
               tables,       lens,       num_seqs,  table_stride, new_tables, new_lens,   gather_idx,
-              gather_count, w.fs,       w.cand_s,  w.cand_i,   w.rows,       div_up(ntiles, G)};
+              gather_count, w.fs,       w.cand_s,  w.cand_i,   w.rows,       div_up(ntiles, G),
+              kSpinLimit,   0};
+  grid_test_hook(&a.spin_limit, &a.extra_arrival);
   if (a.tiles_per_wg == 1)
     hipLaunchKernelGGL(sel_fused_kernel<1>, dim3(G), dim3(kSelThreads), 0, s, a);
   else

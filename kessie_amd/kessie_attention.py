@@ -111,6 +111,10 @@ class _FogCache:
         self._compute_lock = threading.Lock()
         self._recall_key = None
         self._recall_dev = None
+        self._rows_cache = None  # (key, view) of get_fog_bias_rows
+        self._rows_buf = None
+        self._rows_graph_buf = None
+        self._rows_retired = []
 
     def _ensure_alloc(self, kv_len, device, dtype):
         if self._alloc_len >= kv_len and self._device == device and self._dtype == dtype:
@@ -211,27 +215,42 @@ class _FogCache:
         seq_lens[b], zero past it.  One launch on the current stream, no host
         synchronisation.  Shared by the layers of a step when the lengths are
         known on the host (``seq_lens_host``): cached per generation and length
-        tuple; without them it is recomputed on every call."""
+        tuple; without them it is recomputed on every call.
+
+        Under HIP graph capture the fill is always recorded (a cached view
+        would leave the graph without it, replaying whatever an eager call
+        left there) into a buffer of its own that is never freed, so replays
+        neither read stale rows nor write into memory handed out again."""
         from . import ops
 
         b = int(seq_lens.numel())
+        capturing = torch.device(device).type == "cuda" and torch.cuda.is_current_stream_capturing()
         key = None
-        if seq_lens_host is not None:
+        if seq_lens_host is not None and not capturing:
             key = (state["generation"], kv_len, str(device), dtype, tuple(int(x) for x in seq_lens_host.tolist()))
-            if key == getattr(self, "_rows_key", None):
-                return self._rows_view
-        rows_buf = getattr(self, "_rows_buf", None)
-        if (rows_buf is None or rows_buf.shape[0] < b or rows_buf.shape[1] < kv_len
-                or rows_buf.device != torch.device(device)):
-            cols = (max(kv_len, 2048) + 255) & ~255
-            self._rows_buf = rows_buf = torch.empty(max(b, 16), cols, dtype=torch.float32, device=device)
-        view = rows_buf[:b, :kv_len]
-        lens = seq_lens if seq_lens.dtype == torch.int32 else seq_lens.to(torch.int32)
-        recall = self._recall_for(frozenset(state["recall_positions"]), device)
-        ops.fog_bias_rows(view, lens, dtype, state["fog_alpha"], state["fog_start"], recall,
-                          state.get("recall_boost", 0.1))
-        self._rows_key, self._rows_view = key, view
-        return view
+            cached = self._rows_cache  # (key, view), replaced as one attribute
+            if cached is not None and cached[0] == key:
+                return cached[1]
+        with self._compute_lock:
+            attr = "_rows_graph_buf" if capturing else "_rows_buf"
+            rows_buf = getattr(self, attr, None)
+            if (rows_buf is None or rows_buf.shape[0] < b or rows_buf.shape[1] < kv_len
+                    or rows_buf.device != torch.device(device)):
+                if rows_buf is not None:
+                    # A graph captured with it (or a stream still reading it)
+                    # may use it later: keep it alive.
+                    self._rows_retired.append(rows_buf)
+                cols = (max(kv_len, 2048) + 255) & ~255
+                rows_buf = torch.empty(max(b, 16), cols, dtype=torch.float32, device=device)
+                setattr(self, attr, rows_buf)
+            view = rows_buf[:b, :kv_len]
+            lens = seq_lens if seq_lens.dtype == torch.int32 else seq_lens.to(torch.int32)
+            recall = self._recall_for(frozenset(state["recall_positions"]), device)
+            ops.fog_bias_rows(view, lens, dtype, state["fog_alpha"], state["fog_start"], recall,
+                              state.get("recall_boost", 0.1))
+            if not capturing:
+                self._rows_cache = (key, view) if key is not None else None
+            return view
 
     def get_fog_bias_f32(self, kv_len, device, dtype, state):
         """The current generation's bias (computed in ``dtype`` as above)
@@ -414,8 +433,9 @@ class KeSSieAttentionImpl:
         return getattr(inner, name)
 
     # -- the kernels --------------------------------------------------------------
-    _split_key = None
-    _split_val = None
+    # (key, value) of the last split, replaced as one attribute so a reader
+    # never pairs one call's key with another call's split.
+    _split_cache = None
 
     @classmethod
     def _split(cls, meta):
@@ -428,8 +448,9 @@ class KeSSieAttentionImpl:
         host = getattr(meta, "query_start_loc_cpu", None)
         if host is not None:
             key = tuple(int(x) for x in host.tolist())
-            if key == cls._split_key:
-                return cls._split_val
+            cached = cls._split_cache
+            if cached is not None and cached[0] == key:
+                return cached[1]
             qsl = list(key)
         else:
             key = None
@@ -437,8 +458,10 @@ class KeSSieAttentionImpl:
         nseq = len(qsl) - 1
         decode = [i for i in range(nseq) if qsl[i + 1] - qsl[i] == 1]
         prefill = [i for i in range(nseq) if qsl[i + 1] - qsl[i] > 1]
-        cls._split_key, cls._split_val = key, (qsl, decode, prefill)
-        return cls._split_val
+        val = (qsl, decode, prefill)
+        if key is not None:
+            cls._split_cache = (key, val)
+        return val
 
     def _attend(self, args, kwargs, state):
         from . import ops

@@ -378,3 +378,51 @@ def test_select_evict_needs_an_initialised_workspace(dev):
         c = int(cnt.item())
         assert c == len(ref_list) and np.array_equal(_np(lst[:c]), ref_list)
         assert np.array_equal(_np(valid), ref_valid)
+
+
+def test_evict_compact_barrier_failure_leaves_outputs_untouched(dev, monkeypatch):
+    """A grid-barrier wait that runs out fails the whole call: both counts read
+    -1 and page_valid, the evict list, the tables and the gather indices keep
+    their previous contents.  The condition is forced from the host
+    (KESSIE_GRID_TEST_TIMEOUT: the first barrier waits for one arrival more
+    than the grid has and gives up after a few polls, so every workgroup still
+    exits normally).  The scratch is restored, so the next call on the same
+    workspace matches the oracle bit for bit."""
+    from kessie_amd import ops
+
+    for n, s, w in [(262144, 64, 4096), (65536, 64, 1024), (5000, 3, 700)]:  # 64, 16 and 2 workgroups
+        g = torch.Generator().manual_seed(n)
+        scores = torch.rand(n, generator=g)
+        valid = (torch.rand(n, generator=g) < 0.9).to(torch.int8)
+        tables = torch.randint(0, n, (s, w), generator=g, dtype=torch.int32)
+        lens = torch.randint(0, w + 1, (s,), generator=g, dtype=torch.int32)
+        dsc, dtab, dlens = scores.to(dev), tables.to(dev), lens.to(dev)
+        sentinel = -7
+        for polls in ("0", "100"):
+            dv = valid.to(dev)
+            lst = torch.full((n,), sentinel, dtype=torch.int32, device=dev)
+            nt = torch.full((s, w), sentinel, dtype=torch.int32, device=dev)
+            nl = torch.full((s,), sentinel, dtype=torch.int32, device=dev)
+            gi = torch.full((s * w,), sentinel, dtype=torch.int32, device=dev)
+            cnt = torch.zeros(1, dtype=torch.int32, device=dev)
+            gc = torch.zeros(1, dtype=torch.int32, device=dev)
+            monkeypatch.setenv("KESSIE_GRID_TEST_TIMEOUT", polls)
+            ops.page_evict_compact(dsc, dv, dtab, dlens, -1, 0.25, evict_list=lst, evict_count=cnt,
+                                   new_tables=nt, new_lens=nl, gather_idx=gi, gather_count=gc)
+            torch.cuda.synchronize()
+            monkeypatch.delenv("KESSIE_GRID_TEST_TIMEOUT")
+            assert int(cnt.item()) == -1 and int(gc.item()) == -1, (n, polls)
+            assert torch.equal(dv.cpu(), valid)
+            for t in (lst, nt, nl, gi):
+                assert bool((t == sentinel).all())
+        rv, rlist = P.select_evict(scores.numpy(), valid.numpy(), -1, 0.25)
+        rt, rl, rg = P.compact(tables.numpy(), lens.numpy(), rv)
+        dv = valid.to(dev)
+        lst, cnt, nt, nl, gi, gc = ops.page_evict_compact(dsc, dv, dtab, dlens, -1, 0.25)
+        torch.cuda.synchronize()
+        c = int(cnt.item())
+        assert c == len(rlist) and np.array_equal(_np(lst[:c]), rlist)
+        assert np.array_equal(_np(dv), rv)
+        assert np.array_equal(_np(nt), rt) and np.array_equal(_np(nl), rl)
+        m = int(gc.item())
+        assert m == len(rg) and np.array_equal(_np(gi[:m]), rg)

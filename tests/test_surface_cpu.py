@@ -277,3 +277,74 @@ def test_attention_split_follows_metadata_refilled_in_place():
     meta.query_start_loc_cpu[1:] = torch.tensor([3, 4, 5], dtype=torch.int32)
     qsl, dec, pre = ka.KeSSieAttentionImpl._split(meta)
     assert (qsl, dec, pre) == ([0, 3, 4, 5], [1, 2], [0])
+
+
+def test_attention_split_is_consistent_under_concurrent_callers():
+    """Two threads alternating metadata of different decode / prefill splits
+    always get the split of their own metadata (the cached key and value are
+    one attribute, never paired across calls)."""
+    import threading
+
+    from kessie_amd import kessie_attention as ka
+
+    class Meta:
+        def __init__(self, qsl):
+            self.query_start_loc_cpu = torch.tensor(qsl, dtype=torch.int32)
+
+    cases = [([0, 1, 5, 6], [0, 2], [1]), ([0, 4, 5, 6, 9], [1, 2], [0, 3]), ([0, 1, 2], [0, 1], [])]
+    errors = []
+
+    def worker(order):
+        metas = [(Meta(q), (q, d, p)) for q, d, p in cases]
+        for i in range(4000):
+            meta, want = metas[order[i % len(order)]]
+            got = ka.KeSSieAttentionImpl._split(meta)
+            if got != want:
+                errors.append((got, want))
+                return
+
+    threads = [threading.Thread(target=worker, args=(o,)) for o in ([0, 1, 2], [2, 1, 0], [1, 0, 2, 2])]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors[:3]
+
+
+def test_fog_bias_rows_cache_is_consistent_under_concurrent_callers(monkeypatch):
+    """get_fog_bias_rows under two threads with different length tuples (the
+    device fill replaced by a CPU stand-in that writes each row's length): every
+    returned view has its own caller's rows, and the cached key and view are
+    replaced together."""
+    import threading
+
+    from kessie_amd import kessie_attention as ka
+    from kessie_amd import ops
+
+    def fake_rows(view, lens, dtype, alpha, start, recall, boost):
+        for r in range(view.shape[0]):
+            view[r].fill_(float(lens[r]))
+
+    monkeypatch.setattr(ops, "fog_bias_rows", fake_rows)
+    cache = ka._FogCache()
+    state = {"generation": 3, "recall_positions": set(), "fog_alpha": 0.5, "fog_start": 0.5, "recall_boost": 0.1}
+    sets = [torch.tensor([5, 7], dtype=torch.int32), torch.tensor([9, 2, 4], dtype=torch.int32)]
+    errors = []
+
+    def worker(k):
+        for i in range(2000):
+            lens = sets[(i + k) % 2]
+            v = cache.get_fog_bias_rows(lens, 16, "cpu", torch.float32, state, seq_lens_host=lens)
+            if v.shape != (lens.numel(), 16):  # a key paired with another call's view
+                errors.append((k, i, tuple(v.shape)))
+                return
+
+    threads = [threading.Thread(target=worker, args=(k,)) for k in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors[:3]
+    # The key and the view are replaced together.
+    key, view = cache._rows_cache
+    assert key[-1] == tuple(int(x) for x in view[:, 0].tolist())
