@@ -150,7 +150,10 @@ int kessie_fog_decode_paged(
  * KESSIE_ERR_WORKSPACE, launching nothing, when the partials of these sizes
  * exceed the array (B * Hq * S * (head_dim + 2) * 4 bytes plus alignment, S =
  * kessie_fog_decode_num_splits(...)).  Calls that overlap on one GPU share
- * the array and race: serialise them (one stream, or events).  No
+ * the array and race: serialise them (one stream, or events).  The first
+ * call on a device looks the array's address up (hipGetSymbolAddress); make
+ * it outside HIP graph capture, after which the call may be captured and
+ * replayed.  No
  * counterpart in the reference: it exists for callers that cannot allocate
  * device memory (code under HIP graph capture, tight serving loops, hosts
  * that forbid allocation). */

@@ -16,7 +16,7 @@ scaled scores (kessie_attention.py:114-139 producer, applied as attn_bias).
 from __future__ import annotations
 
 import math
-from typing import Optional
+from typing import Optional, Sequence
 
 import torch
 
@@ -137,15 +137,23 @@ def paged_prefill_ref(q: torch.Tensor, pool: torch.Tensor, page_table: torch.Ten
 def paged_prefill_blockwise(q: torch.Tensor, pool: torch.Tensor, page_table: torch.Tensor,
                             ctx_lens: torch.Tensor, rows: torch.Tensor,
                             fog_vscale: Optional[torch.Tensor] = None, window: int = 0, causal: bool = True,
-                            sm_scale: Optional[float] = None, block_pages: int = 512) -> torch.Tensor:
+                            sm_scale: Optional[float] = None, block_pages: int = 512,
+                            kv_head: Optional[int] = None, q_heads: Optional[Sequence[int]] = None) -> torch.Tensor:
     """paged_prefill_ref for selected chunk rows, blockwise with an online
     softmax so a million-token context fits in CPU memory.  ``pool`` may live
     on the GPU: each block of pages is gathered there and copied over.
-    q [B, C, Hq, D] (CPU); returns fp32 [B, len(rows), Hq, D]."""
+    q [B, C, Hq, D] (CPU); returns fp32 [B, len(rows), Hq, D].  With
+    ``kv_head`` only that kv head's query heads are computed (or the subset
+    ``q_heads`` of them, heads numbered within the group); the other heads of
+    the result stay zero."""
     b_, c, hq, d = q.shape
     p = pool.shape[1]
-    hkv = pool.shape[3]
-    g = hq // hkv
+    hkv_all = pool.shape[3]
+    g_all = hq // hkv_all
+    kvs = list(range(hkv_all)) if kv_head is None else [int(kv_head)]
+    sub = list(range(g_all)) if q_heads is None else [int(x) for x in q_heads]
+    hkv, g = len(kvs), len(sub)
+    heads = torch.tensor([kh * g_all + x for kh in kvs for x in sub])  # computed q heads, (kv head, sub) order
     if sm_scale is None:
         sm_scale = 1.0 / math.sqrt(d)
     rows = rows.long()
@@ -154,7 +162,7 @@ def paged_prefill_blockwise(q: torch.Tensor, pool: torch.Tensor, page_table: tor
     for b in range(b_):
         ctx = int(ctx_lens[b])
         qpos = ctx - c + rows                                          # [R]
-        qg = q[b, rows].float().view(r, hkv, g, d).permute(1, 2, 0, 3).reshape(hkv, g * r, d)
+        qg = q[b][rows][:, heads].float().view(r, hkv, g, d).permute(1, 2, 0, 3).reshape(hkv, g * r, d)
         pos_col = qpos.repeat(g)                                       # column (g, r) -> qpos[r]
         m = torch.full((hkv, g * r), float("-inf"))
         l = torch.zeros(hkv, g * r)
@@ -164,7 +172,8 @@ def paged_prefill_blockwise(q: torch.Tensor, pool: torch.Tensor, page_table: tor
         n_pages = (hi + p - 1) // p
         for p0 in range(lo // p, n_pages, block_pages):
             p1 = min(n_pages, p0 + block_pages)
-            kv = pool[page_table[b, p0:p1].long().to(pool.device)].cpu().reshape((p1 - p0) * p, 2, hkv, d).float()
+            kv = pool[page_table[b, p0:p1].long().to(pool.device)][:, :, :, kvs].cpu()
+            kv = kv.reshape((p1 - p0) * p, 2, hkv, d).float()
             t0 = p0 * p
             t1 = min(hi, p1 * p)
             kb = kv[: t1 - t0, 0].permute(1, 2, 0)                    # [Hkv, D, n]
@@ -189,7 +198,7 @@ def paged_prefill_blockwise(q: torch.Tensor, pool: torch.Tensor, page_table: tor
             acc = acc * corr[..., None] + torch.bmm(pexp, vb.permute(1, 0, 2).contiguous())
             m = m_new
         o = acc / l[..., None]                                         # [Hkv, G*R, D]
-        out[b] = o.view(hkv, g, r, d).permute(2, 0, 1, 3).reshape(r, hq, d)
+        out[b][:, heads] = o.view(hkv, g, r, d).permute(2, 0, 1, 3).reshape(r, hkv * g, d)
     return out
 
 

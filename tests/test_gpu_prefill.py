@@ -193,7 +193,8 @@ def test_prefill_1m_context_every_query_tile(dev):
     (65,664 pages), 32 q / 8 kv heads, D=128, causal, V-fog over the full
     context.  Full-size GPU run; the first and the last query position of each
     of the kernel's 32 query tiles (64 positions x the 4 heads of a kv head per
-    tile), all 32 heads, checked against the blockwise oracle."""
+    tile), all 32 heads, and all 2,048 positions of one head, checked against
+    the blockwise oracle."""
     from kessie_amd import ops
 
     c, L = 2048, 1 << 20
@@ -210,6 +211,12 @@ def test_prefill_1m_context_every_query_tile(dev):
     rows = torch.tensor(sorted([64 * t for t in range(32)] + [64 * t + 63 for t in range(32)] + [777, 1500]))
     ref = paged_prefill_blockwise(q.cpu(), pool, table.cpu(), lens.cpu(), rows, fog.cpu(), block_pages=4096)
     _check(out[:, rows], ref, torch.bfloat16)
+    # Every one of the 2,048 rows of q head 13 (kv head 3, the second head of
+    # its group), so each row's causal boundary at 1M context is checked.
+    every = torch.arange(c)
+    ref13 = paged_prefill_blockwise(q.cpu(), pool, table.cpu(), lens.cpu(), every, fog.cpu(), block_pages=2048,
+                                    kv_head=3, q_heads=[1])
+    _check(out[:, :, 13:14], ref13[:, :, 13:14], torch.bfloat16)
 
 
 @pytest.mark.parametrize("fog", ["vscale", "bias", "none"])

@@ -142,3 +142,12 @@ def test_blockwise_prefill_equals_direct():
         a = paged_prefill_ref(q, pool, table, torch.tensor([ctx]), w, window=window, rows=rows)
         b = paged_prefill_blockwise(q, pool, table, torch.tensor([ctx]), rows, w, window=window, block_pages=3)
         assert torch.allclose(a, b, atol=1e-5)
+        # One kv head's query heads (all, or a subset): those heads equal the
+        # direct result, every other head stays zero.
+        for kvh, sub in ((1, None), (0, [3, 1])):
+            hs = [kvh * 4 + x for x in (sub if sub is not None else range(4))]
+            c_ = paged_prefill_blockwise(q, pool, table, torch.tensor([ctx]), rows, w, window=window,
+                                         block_pages=3, kv_head=kvh, q_heads=sub)
+            assert torch.allclose(a[:, :, hs], c_[:, :, hs], atol=1e-5)
+            rest = [h for h in range(hq) if h not in hs]
+            assert bool((c_[:, :, rest] == 0).all())

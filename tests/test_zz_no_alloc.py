@@ -3,7 +3,8 @@ device scratch, no workspace argument) against kessie_fog_decode_paged with a
 caller workspace, both called through the C ABI.  Same kernels and split
 count, so the outputs must be identical bit for bit; two calls in a row, the
 second smaller (the scratch keeps the first call's partials, which the
-second must not read), and a shape whose partials exceed the scratch."""
+second must not read), the balanced split layout, a capture in a HIP graph,
+and a shape whose partials exceed the scratch."""
 import ctypes
 
 import pytest
@@ -81,3 +82,60 @@ def test_noalloc_decode_rejects_partials_beyond_the_scratch(dev):
     status, msg = _lib.last_error()
     assert status == _lib.ERR_WORKSPACE and "static scratch" in msg
     assert bool((out == 0).all())  # nothing launched
+
+
+def test_noalloc_decode_balanced_layout_equals_workspace_decode(dev):
+    """A ragged batch whose K/V (1 GiB) takes the balanced split layout (a
+    sequence's partials at h * S * B + unit) through the static scratch: 2
+    sequences of 131,072 and 9,000 tokens, 32 q / 8 kv heads, ~4.3 MB of
+    partials; bit for bit against the workspace call, then a smaller call."""
+    ctx = 131072
+    q, pool, table, lens = decode_case(2, 32, 8, 128, ctx, 16, torch.bfloat16, dev, seed=64, ctx_lens=[ctx, 9000])
+    vs = build_fog_weights(ctx).to(dev)
+    ref, got = _both(dev, q, pool, table, lens, ctx, vs)
+    assert torch.isfinite(ref.float()).all()
+    assert torch.equal(got, ref)
+    del pool
+    q, pool, table, lens = decode_case(1, 32, 8, 128, 2000, 16, torch.bfloat16, dev, seed=65)
+    ref, got = _both(dev, q, pool, table, lens, 2000, None)
+    assert torch.equal(got, ref)
+
+
+def test_noalloc_decode_under_graph_capture(dev):
+    """The no-alloc call captured in a HIP graph (after one eager call on the
+    device, which resolves the scratch address) and replayed with new query
+    values and new lengths between replays: every replay equals the eager call
+    on the same inputs bit for bit."""
+    from kessie_amd import _lib
+
+    lib = _lib.load()
+    ctx = 6000
+    q, pool, table, lens = decode_case(3, 32, 8, 128, ctx, 16, torch.bfloat16, dev, seed=66,
+                                       ctx_lens=[ctx, 4000, 77])
+    vs = build_fog_weights(ctx).to(dev)
+    out = torch.empty_like(q)
+    stream = torch.cuda.Stream()
+
+    def call(o):
+        st = lib.kessie_fog_decode_paged_noalloc(*_args(q, pool, table, lens, ctx, vs, o, _lib.DTYPE_BF16),
+                                                 ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        _lib.check("kessie_fog_decode_paged_noalloc", st)
+
+    call(out)  # eager, outside the capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        call(out)
+    torch.cuda.synchronize()
+    for i, new_lens in enumerate(([ctx, 4000, 77], [100, ctx, 5999], [0, 1, ctx])):
+        q.copy_(torch.randn(q.shape, generator=torch.Generator(device=dev).manual_seed(300 + i), device=dev)
+                .to(torch.bfloat16))
+        lens.copy_(torch.tensor(new_lens, dtype=torch.int32, device=dev))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got = out.clone()
+        want = torch.empty_like(q)
+        call(want)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"replay {i}"
