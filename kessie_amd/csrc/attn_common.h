@@ -50,6 +50,12 @@ struct Params {
   int window, causal;
   float sm_scale;
   int num_splits;
+  // Dense launchers' split (table-less pages, split instance): query tiles
+  // from position split_q0 on (the longest ones) take num_splits workgroups,
+  // the others one; partial rows cover positions split_q0 .. C-1 only.  The
+  // combine writes its row (b, i, h) at position i + q0_off.
+  int split_q0;
+  int q0_off;
   int direct_out;      // 1: the main kernel writes the normalised output
   int launch_combine;  // host side: follow the main kernel with the combine
   int balanced;        // decode split partials: units assigned by pages (decode_seq_of_unit)

@@ -30,7 +30,10 @@
 #include <cstdlib>
 
 #include <atomic>
+#include <map>
 #include <mutex>
+#include <utility>
+#include <vector>
 
 #include "attn_common.h"
 
@@ -363,6 +366,7 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(Params p) {
     first = (int64_t)h * S * p.B + s_first;
     n_s = s_count;
   }
+  i += p.q0_off;  // rows of a dense split start at position q0_off
   const float* m = p.ws_m + first;
   const float* l = p.ws_l + first;
   if (tid < 64) {
@@ -425,6 +429,130 @@ inline int combine_dsplit(int64_t rows, int D) {
   while (y < 8 && rows * y < 256 && D % (4 * y) == 0) y *= 2;  // the chunk D/y stays even
   return y;
 }
+
+// Two consecutive outputs of lane-owned columns: one 8-byte store for
+// fp32, one packed 4-byte store for bf16/fp16 (rows start on even columns).
+template <typename T>
+__device__ __forceinline__ void store2(T* dst, float a, float b);
+template <>
+__device__ __forceinline__ void store2<float>(float* dst, float a, float b) {
+  *reinterpret_cast<float2*>(dst) = make_float2(a, b);
+}
+template <>
+__device__ __forceinline__ void store2<bf16_t>(bf16_t* dst, float a, float b) {
+  typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+  *reinterpret_cast<bf2*>(dst) = bf2{from_f32<bf16_t>(a), from_f32<bf16_t>(b)};
+}
+template <>
+__device__ __forceinline__ void store2<f16_t>(f16_t* dst, float a, float b) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  *reinterpret_cast<h2*>(dst) = h2{from_f32<f16_t>(a), from_f32<f16_t>(b)};
+}
+
+// Combine for many rows (split prefill and the dense launchers: a row per
+// query position and head), S <= 16: each wave merges four rows, lane 16r + s
+// holding (m, l) of split s of row r and every lane D / 64 columns of all
+// four rows, with all of the wave's loads issued before any use.  The
+// per-row workgroups of combine_kernel are dispatch- and latency-bound at
+// these counts (65,536 rows: 97 us).  The same merge, summed in the same
+// order, as combine_kernel (max and sum over the splits by the same butterfly
+// -- its first two steps, across halves and quarters of the wave, only add
+// zeros there -- and the columns in GR groups of every GR-th split, added in
+// group order), so the two kernels give the same bits.
+constexpr int kCombRows = 4;                   // rows per wave
+constexpr int kCombRowsPerWg = 4 * kCombRows;  // four waves
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void combine_rows_kernel(Params p, int64_t rows) {
+  constexpr int NC = D / 64;                       // columns per lane
+  constexpr int GR = kCombineThreads / (D / 2);    // combine_kernel's split groups
+  const int lane = threadIdx.x & 63;
+  const int64_t row0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * kCombRows;
+  if (row0 >= rows) return;  // uniform per wave; no barriers
+  const int S = p.num_splits;
+  // (m, l) of split lane % 16 of row row0 + lane / 16.
+  const int64_t mr = min(row0 + lane / 16, rows - 1);
+  const bool mok = (lane & 15) < S && row0 + lane / 16 < rows;
+  const float m = mok ? p.ws_m[mr * S + (lane & 15)] : kNegInf;
+  const float l = mok ? p.ws_l[mr * S + (lane & 15)] : 0.0f;
+  // Partials: v[r][sp][c] of row row0 + r (clamped into range), split sp < S,
+  // NC columns per load.
+  typedef float fNC __attribute__((ext_vector_type(NC)));
+  fNC v[kCombRows][16];
+#pragma unroll
+  for (int r = 0; r < kCombRows; ++r) {
+    const float* o = p.ws_o + min(row0 + r, rows - 1) * S * D + NC * lane;
+#pragma unroll
+    for (int sp = 0; sp < 16; ++sp)
+      v[r][sp] = sp < S ? *reinterpret_cast<const fNC*>(o + (int64_t)sp * D) : fNC{};
+  }
+  float mx = m;
+#pragma unroll
+  for (int o = 8; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  const float e = m == kNegInf ? 0.0f : expf(m - mx);
+  float sum = e * l;
+#pragma unroll
+  for (int o = 8; o >= 1; o >>= 1) sum += __shfl_xor(sum, o, 64);
+#pragma unroll
+  for (int r = 0; r < kCombRows; ++r) {
+    const int64_t row = row0 + r;
+    if (row >= rows) break;  // uniform
+    float part[GR][NC];
+#pragma unroll
+    for (int g = 0; g < GR; ++g)
+#pragma unroll
+      for (int c = 0; c < NC; ++c) part[g][c] = 0.0f;
+#pragma unroll
+    for (int sp = 0; sp < 16; ++sp) {
+      if (sp < S) {  // uniform
+        const float es = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e), 16 * r + sp));
+#pragma unroll
+        for (int c = 0; c < NC; ++c) part[sp % GR][c] += es * v[r][sp][c];
+      }
+    }
+    const float sr = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sum), 16 * r));
+    const float il = sr > 0.0f ? 1.0f / sr : 0.0f;
+    const int h = (int)(row % p.Hq);
+    const int64_t bi = row / p.Hq;
+    int i = (int)(bi % p.C), b = (int)(bi / p.C);
+    if (p.q_start) {  // varlen prefill: rows past the chunk have no partials
+      if (i >= p.q_start[b + 1] - p.q_start[b]) continue;
+      i += p.q_start[b] - p.q_start[0];
+      b = 0;
+    }
+    i += p.q0_off;  // rows of a dense split start at position q0_off
+    float acc[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      acc[c] = part[0][c];
+#pragma unroll
+      for (int g = 1; g < GR; ++g) acc[c] += part[g][c];
+    }
+    T* dst = static_cast<T*>(p.out) + (int64_t)b * p.o_bs + (int64_t)i * p.o_is + (int64_t)h * p.o_hs + NC * lane;
+    if constexpr (NC == 2)
+      store2<T>(dst, acc[0] * il, acc[1] * il);
+    else
+      dst[0] = from_f32<T>(acc[0] * il);
+  }
+}
+
+// Launches the merge of split partials into the output: combine_rows_kernel
+// for many rows, combine_kernel otherwise.
+template <typename T>
+void launch_combine(const Params& p, int64_t rows, hipStream_t s) {
+  const bool even = ((p.o_bs | p.o_is | p.o_hs) & 1) == 0 && ((uintptr_t)p.out & 3) == 0;  // packed stores
+  if (rows >= 4096 && !p.balanced && p.num_splits <= 16 && (p.D == 128 || p.D == 64) && even) {
+    const dim3 grid((unsigned)div_up(rows, (int64_t)kCombRowsPerWg));
+    if (p.D == 128)
+      hipLaunchKernelGGL((combine_rows_kernel<T, 128>), grid, dim3(256), 0, s, p, rows);
+    else
+      hipLaunchKernelGGL((combine_rows_kernel<T, 64>), grid, dim3(256), 0, s, p, rows);
+    return;
+  }
+  hipLaunchKernelGGL(combine_kernel<T>, dim3((unsigned)rows, combine_dsplit(rows, p.D)), dim3(kCombineThreads), 0,
+                     s, p);
+}
+
 
 // ---------------------------------------------------------------------------
 // MFMA decode (bf16 / f16, head_dim 128, pages of 16 * 2^k tokens)
@@ -1008,9 +1136,7 @@ int launch_generic(Params& p, hipStream_t stream) {
   hipLaunchKernelGGL(attn_generic_kernel<T>, grid, dim3(kGenThreads), lds, stream, p);
   if (check_launch("fog attention (generic)") != KESSIE_OK) return KESSIE_ERR_HIP;
   if (!p.direct_out && p.launch_combine) {
-    const int64_t rows = (int64_t)p.B * p.C * p.Hq;
-    hipLaunchKernelGGL(combine_kernel<T>, dim3((unsigned)rows, combine_dsplit(rows, p.D)), dim3(kCombineThreads),
-                       0, stream, p);
+    launch_combine<T>(p, (int64_t)p.B * p.C * p.Hq, stream);
     return check_launch("fog attention (combine)");
   }
   return KESSIE_OK;
@@ -1419,11 +1545,10 @@ static int run_prefill_mfma(kessie::attn::Params& p, int dtype, void* workspace,
   const hipStream_t s = as_stream(stream);
   const int st = prefill_mfma(p, dtype, s);
   if (st != KESSIE_OK || p.direct_out) return st;
-  const dim3 cgrid((unsigned)rows, combine_dsplit(rows, p.D));
   if (dtype == KESSIE_DTYPE_BF16)
-    hipLaunchKernelGGL(combine_kernel<bf16_t>, cgrid, dim3(kCombineThreads), 0, s, p);
+    launch_combine<bf16_t>(p, rows, s);
   else
-    hipLaunchKernelGGL(combine_kernel<f16_t>, cgrid, dim3(kCombineThreads), 0, s, p);
+    launch_combine<f16_t>(p, rows, s);
   return check_launch("fog prefill (combine)");
 }
 
@@ -1555,6 +1680,89 @@ extern "C" int kessie_fog_prefill_varlen(const void* q, const int32_t* query_sta
 
 // Reference launchers (kessie_kernels_v2.hip:716-751, 788-825): dense fp16
 // [B,H,N,D], no GQA, every position a query.  One split, so no workspace.
+namespace kessie {
+namespace attn {
+namespace {
+// Key splits of the dense launchers' MFMA kernel.  Every position is a query,
+// so with causal masking a query tile's key tiles grow with its position: the
+// longest tile (dispatched first) can take twice the chip's average share,
+// and a small B*H leaves most CUs without a tile at all.  Each query tile's
+// keys are split S ways, from the longest tile's key tiles over the per-CU
+// share of all key tiles, with at least 4 key tiles per split; 1 when the
+// grid alone balances (B=1 H=32 N=8,192 causal: 1,024 workgroups over 256
+// CUs).  Returns S and, in *split_q0, the first position of the split tiles.
+// KESSIE_DENSE_SPLITS > 0 forces the count (tests).
+int dense_splits(int B, int H, int N, int window, int causal, int* split_q0) {
+  *split_q0 = 0;
+  const int kt = div_up(N, 64);  // key tiles of the whole sequence
+  const int nq = div_up(N, 256);
+  std::vector<int> tiles(nq);
+  int64_t total = 0;
+  int longest = 0;
+  for (int t = 0; t < nq; ++t) {
+    const int q0 = 256 * t, q1 = min(N, q0 + 256) - 1;
+    int hi = causal ? q1 + 1 : N;
+    int lo = 0;
+    if (window > 0) {
+      lo = max(0, q0 - window + 1);
+      hi = min(hi, q1 + 1);
+    }
+    tiles[t] = hi > lo ? div_up(hi, 64) - lo / 64 : 0;
+    total += tiles[t];
+    longest = max(longest, tiles[t]);
+  }
+  total *= (int64_t)B * H;
+  const double share = (double)total / device_cus();
+  // Every query tile is split (split_q0 0).  Splitting only the tiles longer
+  // than the share saves their partial rows but dispatches the long tiles'
+  // later splits behind whole short tiles: N=8,192 ran 245-256 us against
+  // 230 us.
+  const int forced = env_int("KESSIE_DENSE_SPLITS", 0);  // testing: > 0 forces the count
+  if (forced > 0) return min(forced, min(kt, kMaxSplits));
+  if (longest <= 0 || share <= 0.0) return 1;
+  // Each split adds a partial row per query of a split tile (written, then
+  // read by the combine), which outweighs the balance gained past a few
+  // splits: on the reference's benchmark (B=1, H=8, causal) the best counts
+  // were 2 at N=4,096-8,192 (longest tile 1.9-3.8 times the share) and 4 at
+  // N=1,024-2,048.
+  const double ratio = longest / share;
+  if (ratio < 1.5) return 1;
+  int s = min(4, max(2, (int)(ratio / 2.0 + 0.5)));
+  s = min(s, max(1, longest / 4));
+  s = min(s, min(kt, kMaxSplits));
+  return max(s, 1);
+}
+
+// Device buffer for the dense launchers' split partials, per device and
+// stream (calls on one stream run in order, so they can share it), allocated
+// on first need and kept until the process ends; an outgrown buffer is kept
+// too (a graph captured with it may replay).  Under stream capture nothing is
+// allocated: nullptr unless the stream's buffer is already large enough.
+std::mutex g_dense_mu;
+std::map<std::pair<int, hipStream_t>, std::pair<void*, size_t>> g_dense_ws;
+std::vector<void*> g_dense_retired;
+
+void* dense_workspace(size_t bytes, hipStream_t s) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  std::lock_guard<std::mutex> lock(g_dense_mu);
+  auto& e = g_dense_ws[{dev, s}];
+  if (e.first != nullptr && e.second >= bytes) return e.first;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
+  void* ptr = nullptr;
+  if (hipMalloc(&ptr, bytes) != hipSuccess || ptr == nullptr) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  if (e.first != nullptr) g_dense_retired.push_back(e.first);
+  e = {ptr, bytes};
+  return ptr;
+}
+}  // namespace
+}  // namespace attn
+}  // namespace kessie
+
 static void dense_fp16(const void* Q, const void* K, const void* V, void* O, const void* fog, float sm_scale,
                        int B, int H, int N, int D, int window, int causal, void* stream) {
   using namespace kessie;
@@ -1611,8 +1819,10 @@ static void dense_fp16(const void* Q, const void* K, const void* V, void* O, con
   // head_dim 128 or 64: the MFMA prefill kernel, reading the dense tensors as
   // table-less 16-token pages (page b*H*N/16 + j = tokens 16j..16j+15 of every
   // head of sequence b, heads N*D apart; H*N a multiple of 16 keeps sequences
-  // on whole pages, and the kernel reads no token past N).  One key split:
-  // these launchers take no workspace.
+  // on whole pages, and the kernel reads no token past N).  Key splits
+  // (partials merged by the combine kernel) when the grid alone would leave
+  // CUs idle, in the library's per-stream buffer (these launchers take no
+  // workspace); without one, a single split.
   const int64_t dense_pages = (int64_t)B * H * N / 16;
   if (((int64_t)H * N) % 16 == 0 && dense_pages <= INT_MAX) {
     Params m = p;
@@ -1621,7 +1831,26 @@ static void dense_fp16(const void* Q, const void* K, const void* V, void* O, con
     m.num_pages = (int)dense_pages;
     m.dense_ppb = (int)(((int64_t)H * N) / 16);
     if (prefill_mfma_ok(m, KESSIE_DTYPE_F16)) {
-      prefill_mfma(m, KESSIE_DTYPE_F16, as_stream(stream));  // records any launch error
+      const hipStream_t s = as_stream(stream);
+      int split_q0 = 0;
+      const int S = dense_splits(B, H, N, window, causal, &split_q0);
+      const int64_t rows = (int64_t)B * (N - split_q0) * H;  // partial rows: the split tiles' queries
+      const size_t need = partial_bytes(rows, S, D);
+      void* ws = S > 1 && need <= ((size_t)1 << 30) ? dense_workspace(need, s) : nullptr;
+      if (ws != nullptr) {
+        m.num_splits = S;
+        m.split_q0 = split_q0;
+        m.direct_out = 0;
+        carve_workspace(m, ws, rows);
+        if (prefill_mfma(m, KESSIE_DTYPE_F16, s) != KESSIE_OK) return;  // error recorded
+        Params c = m;  // the combine's rows: positions split_q0 .. N-1
+        c.C = N - split_q0;
+        c.q0_off = split_q0;
+        launch_combine<f16_t>(c, rows, s);
+        check_launch("dense attention (combine)");
+        return;
+      }
+      prefill_mfma(m, KESSIE_DTYPE_F16, s);  // records any launch error
       return;
     }
   }

@@ -31,14 +31,17 @@
 // sits on one XCD and the query tiles of that head share its keys in L2.
 //
 // Variants (template and Params):
-//   kSplit   grid z splits each query tile's key tiles; every split stores
-//            unnormalised partials (O, max, sum) merged by the combine kernel
-//            -- used when the chunks alone would leave CUs idle;
+//   kSplit   grid z splits each query tile's key tiles (split s takes tiles
+//            s, s + S, ...); every split stores unnormalised partials (O,
+//            max, sum) merged by the combine kernel -- used when the chunks
+//            alone would leave CUs idle;
 //   q_start  varlen batch: x / Hkv numbers the live (sequence, query tile)
 //            pairs, each chunk's queries packed at query_start_loc;
 //   kMode    0 paged; 1 table-less pages (page b * dense_ppb + j) for the
 //            reference's dense [B][H][N][D] launchers, query tiles longest
-//            first; 2 paged with query tiles longest first (a causal chunk
+//            first (split: only the tiles from split_q0 on, S units each,
+//            numbered along x split-major with the unsplit tiles, which
+//            store their output directly); 2 paged with query tiles longest first (a causal chunk
 //            that is most of its context and takes several grid rounds); 3
 //            paged with pages of 32, 64, ... tokens, read as 16-token blocks.
 #include "attn_common.h"
@@ -177,11 +180,43 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
   const int g = blockIdx.x % p.Hkv;
   int qtile = blockIdx.x / p.Hkv;
   int b = blockIdx.y;
-  // Dense causal (every position a query): later query tiles see more keys;
-  // dispatching them first keeps the short ones for the tail of the grid
-  // (+15-19 %).  Not in the paged instances: there the same two lines cost the
-  // long-context shape 1-2 % through code generation.
-  if ((kDense && p.causal) || kMode == 2) qtile = (int)(gridDim.x / p.Hkv) - 1 - qtile;
+  // Split instances: S workgroups per query tile along grid z, each taking
+  // its share of the key tiles.  The dense split instead numbers (tile, split)
+  // units along x, longest tile first: the S splits of each tile from
+  // position split_q0 on, then the shorter tiles, one workgroup each.
+  int S = kSplit ? (int)gridDim.z : 1, split = kSplit ? (int)blockIdx.z : 0;
+  bool part_out = kSplit;  // this workgroup stores split partials
+  if (kDense && kSplit) {
+    // Split-major order, as a grid z of splits would dispatch: pass 0 holds
+    // every query tile, longest first -- split 0 of a split tile, or all of a
+    // tile that is not split (its output stored directly) -- and pass s >= 1
+    // split s of the split tiles, longest first.  The tiles of a head in a
+    // pass stream their keys upward from the same start, sharing them in L2
+    // (units sorted by size instead ran N=8,192 5 % slower).
+    const int nq = div_up(p.C, kPfRows);
+    const int t0 = p.split_q0 / kPfRows;  // first split tile
+    if (qtile < nq) {
+      qtile = nq - 1 - qtile;
+      split = 0;
+      if (qtile >= t0) {
+        S = p.num_splits;
+      } else {
+        S = 1;
+        part_out = false;
+      }
+    } else {
+      const int k = qtile - nq, nl = nq - t0;
+      S = p.num_splits;
+      split = 1 + k / nl;
+      qtile = nq - 1 - k % nl;
+    }
+  } else if ((kDense && p.causal) || kMode == 2) {
+    // Dense causal (every position a query): later query tiles see more keys;
+    // dispatching them first keeps the short ones for the tail of the grid
+    // (+15-19 %).  Not in the paged instances: there the same two lines cost
+    // the long-context shape 1-2 % through code generation.
+    qtile = (int)(gridDim.x / p.Hkv) - 1 - qtile;
+  }
   if (p.q_start) {
     // Varlen: x / Hkv numbers the live (sequence, query tile) pairs in order,
     // so the grid's surplus workgroups all sit at its end and exit at once
@@ -233,16 +268,19 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
   if (qmax >= 0) key_range(p, ctx, qmin, qmax, &lo, &hi);
   const int tile_lo = lo / kPfKT;
   int n_tiles = hi > tile_lo * kPfKT ? div_up(hi - tile_lo * kPfKT, kPfKT) : 0;
-  // Split-K: workgroup z takes its share of the key tiles (possibly none:
-  // it still writes an empty partial for its rows).
-  const int S = kSplit ? (int)gridDim.z : 1, split = kSplit ? (int)blockIdx.z : 0;
-  int first = 0;
-  if (kSplit) {
+  // Split-K: split s takes key tiles s, s + S, s + 2S, ... of the range
+  // (possibly none: it still writes an empty partial for its rows).
+  // Interleaved, the splits that run at one time all stream a head's keys
+  // upward from its first tile, sharing them in L2 (contiguous thirds or
+  // halves started the later splits at staggered keys: dense B=1 H=8 N=8,192
+  // split in two ran each key tile ~30 % slower than unsplit).
+  int first = 0, kstep = kPfKT;  // first tile, key positions between consecutive tiles
+  if (kSplit && S > 1) {
     // (The division runs on the vector unit; readfirstlane returns the
     // uniform bounds to scalar registers.)
-    const int per = __builtin_amdgcn_readfirstlane(div_up(n_tiles, S));
-    first = __builtin_amdgcn_readfirstlane(min(n_tiles, split * per));
-    n_tiles = __builtin_amdgcn_readfirstlane(min(n_tiles, first + per) - first);
+    first = split;
+    n_tiles = __builtin_amdgcn_readfirstlane(n_tiles > split ? (n_tiles - split + S - 1) / S : 0);
+    kstep = S * kPfKT;
   }
   const int t_begin = (tile_lo + first) * kPfKT;
   const int n_tab = div_up(hi, 16);  // table entries that may be read
@@ -301,7 +339,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
   // is clamped into the readable entries and the value replaced afterwards, so
   // the four scalar loads issue back to back with no branch around them.
   auto fetch_ids = [&](int tile) {
-    const int pg0 = (t_begin + tile * kPfKT) >> 4;
+    const int pg0 = (t_begin + tile * kstep) >> 4;
     i32x4 ids;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -368,7 +406,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
   v8 kreg[2][kKL], vreg[2][2];
   float fw0[2] = {1.0f, 1.0f}, fw1[2] = {1.0f, 1.0f}, fb_r[2] = {0.0f, 0.0f};
   auto issue = [&](int tile, i32x4 ids, int set) {
-    const int t0 = t_begin + tile * kPfKT;
+    const int t0 = t_begin + tile * kstep;
     const auto krs = page_rsrc(kpool, slot_id(ids, kslot), t0 + 16 * kslot);
 #pragma unroll
     for (int r = 0; r < kKL; ++r)
@@ -448,9 +486,10 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
   {
     const int klo = p.window > 0 ? max(lo, qmax - p.window + 1) : lo;
     const int khi = min(hi, qmin + 1);
+    // Tile t covers keys [t_begin + t * kstep, + kPfKT).
     const int dlo = klo - t_begin, dhi = khi - t_begin;
-    ti_lo = dlo <= 0 ? 0 : (dlo + kPfKT - 1) / kPfKT;
-    ti_hi = dhi <= 0 ? 0 : dhi / kPfKT;
+    ti_lo = dlo <= 0 ? 0 : (dlo + kstep - 1) / kstep;
+    ti_hi = dhi < kPfKT ? 0 : (dhi - kPfKT) / kstep + 1;
   }
 
   i32x4 ids_a, ids_b;            // page ids of tiles t+3 and t+4
@@ -469,7 +508,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
   // holds tile t+2, stored to its stage in this iteration.
   auto step = [&](int t, f32x16& c0, f32x16& c1, f32x16& x, int set) {
     auto sc = [&](int kb) -> f32x16& { return kb ? c1 : c0; };
-    const int t0 = t_begin + t * kPfKT;
+    const int t0 = t_begin + t * kstep;
     const int st_cur = t & (kPfStages - 1);
     const int st_nxt = (t + 1) & (kPfStages - 1);
     const int st_new = (t + 2) & (kPfStages - 1);
@@ -621,10 +660,11 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
   // Lane (col, half) holds row frow at d = 32*db + 8*(v/4) + 4*half + (v%4).
   const float l = l_half + __shfl_xor(l_half, 32);
   if (!row_ok) return;
-  if (kSplit) {
+  if (kSplit && part_out) {
     // Split partial: unnormalised O, the running max in natural-log units
     // (the softmax here is base 2) and the sum, merged by the combine kernel.
-    const int64_t r = row_id(p, b, qi, head) * S + split;
+    const int64_t r = (kDense ? ((int64_t)b * (p.C - p.split_q0) + (qi - p.split_q0)) * p.Hq + head
+                              : row_id(p, b, qi, head)) * S + split;
     float* dst = p.ws_o + r * kD + 4 * half;
 #pragma unroll
     for (int db = 0; db < kDB; ++db)
@@ -695,7 +735,17 @@ int launch_prefill(Params& p, hipStream_t stream) {
   const int kpos = kPfRows / p.G;
   // Varlen: the live (sequence, query tile) pairs are numbered along x.
   dim3 grid(div_up(p.C, kpos) * p.Hkv * (p.q_start ? p.B : 1), p.q_start ? 1 : p.B, max(p.num_splits, 1));
-  if (p.page_table == nullptr) {  // table-less pages (dense launchers): G 1, no bias, one split
+  // (The dense split instance numbers its (tile, split) units along x.)
+  if (p.page_table == nullptr) {  // table-less pages (dense launchers): G 1, no bias
+    if (p.num_splits > 1) {  // (tile, split) units along x (kernel header)
+      const int nq = div_up(p.C, kPfRows), t0 = p.split_q0 / kPfRows;
+      grid = dim3((unsigned)((t0 + (nq - t0) * p.num_splits) * p.Hkv), p.B, 1);
+      if (p.D == 64)
+        return p.vscale ? launch_one<T, 1, false, true, true, 1, 64>(p, grid, stream)
+                        : launch_one<T, 1, false, false, true, 1, 64>(p, grid, stream);
+      return p.vscale ? launch_one<T, 1, false, true, true, 1>(p, grid, stream)
+                      : launch_one<T, 1, false, false, true, 1>(p, grid, stream);
+    }
     if (p.D == 64)
       return p.vscale ? launch_one<T, 1, false, true, false, 1, 64>(p, grid, stream)
                       : launch_one<T, 1, false, false, false, 1, 64>(p, grid, stream);
@@ -726,7 +776,7 @@ bool prefill_mfma_ok(const Params& p, int dtype) {
     return false;
   if (((int64_t)p.num_pages << (__builtin_ctz((unsigned)p.page_size) - 4)) >= (int64_t)1 << 31) return false;
   // Table-less pages: instantiated for the dense launchers' form only.
-  if (p.page_table == nullptr && (p.dense_ppb <= 0 || p.G != 1 || p.bias || p.num_splits > 1)) return false;
+  if (p.page_table == nullptr && (p.dense_ppb <= 0 || p.G != 1 || p.bias)) return false;
   if (!(p.G == 1 || p.G == 2 || p.G == 4 || p.G == 8 || p.G == 16)) return false;
   if (!(p.sm_scale > 0.0f)) return false;
   if (!aligned16(p.q) || !aligned16(p.k) || !aligned16(p.v) || !aligned16(p.out)) return false;
