@@ -5,9 +5,10 @@ remap Mtok/s, with the kernels' roofline and the CPU oracle timed beside them.
 Primary workload (the JSON ``value``): fog-attention decode, bf16, Llama-3-8B
 attention shape -- batch 16, 32 query / 8 KV heads, head_dim 128, 131,072-token
 context per sequence in 16-token pages (random page tables), V-fog weights
-alpha 0.5 / fog_start 0.5, window 0.  A step is one decode of the batch:
-the streaming partials kernel plus the split-combine kernel.  ``value`` =
-algorithmic bytes of one decode / step time.
+alpha 0.5 / fog_start 0.5, window 0.  A step is one decode of the batch
+through the serving entry point (kessie_fog_decode_paged: the streaming kernel
+plus the split-combine kernel).  ``value`` = algorithmic bytes of one decode /
+step time.
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu] [--no-secondary]
 """
@@ -126,6 +127,17 @@ def setup_decode(dev, b=16, hq=32, hkv=8, d=128, ctx=131072, page_size=16, dtype
 
 
 def run_decode_step(s):
+    """One decode step through the serving entry point (ops.fog_decode ->
+    kessie_fog_decode_paged: the streaming kernel, with the split layout it
+    chooses for the batch, then the split combine)."""
+    from kessie_amd import ops
+
+    ops.fog_decode(s["q"], s["pool"], s["table"], s["lens"], s["ctx"], fog_vscale=s["fog"], out=s["out"], ws=s["ws"])
+
+
+def run_partials_combine(s):
+    """The same decode as the two halves of the C ABI (kessie_fog_decode_partials
+    + kessie_fog_decode_combine: the plain split layout)."""
     from kessie_amd import ops
 
     ops.fog_decode_partials(s["q"], s["pool"], s["table"], s["lens"], s["ctx"], s["ws"], fog_vscale=s["fog"])
@@ -133,12 +145,15 @@ def run_decode_step(s):
 
 
 def time_decode(s, steps, warmup):
+    """(ms per serving step, ms of the streaming kernel alone, ms per
+    partials + combine step)."""
     import torch
 
     from kessie_amd import ops
 
     for _ in range(warmup):
         run_decode_step(s)
+        run_partials_combine(s)
     torch.cuda.synchronize()
     # The steps: K decodes back to back between two events, nothing else in
     # the stream (an event pair around each launch would add its dispatch and
@@ -151,8 +166,8 @@ def time_decode(s, steps, warmup):
     end.record()
     torch.cuda.synchronize()
     total_ms = start.elapsed_time(end)
-    # The streaming kernel alone: the same K steps again, with an event pair
-    # around each partials launch.
+    # The streaming kernel alone: K launches of the partials half, an event
+    # pair around each, on the stream they run on.
     e0, e1 = events(steps), events(steps)
     backlog()
     for i in range(steps):
@@ -162,7 +177,15 @@ def time_decode(s, steps, warmup):
         ops.fog_decode_combine(s["ws"], s["out"], s["hkv"], s["ctx"], s["page_size"])
     torch.cuda.synchronize()
     kern = [a.elapsed_time(b) for a, b in zip(e0, e1)]
-    return total_ms / steps, sum(kern) / len(kern)
+    # The two-call form back to back, for comparison with the serving entry.
+    start, end = events(2)
+    backlog()
+    start.record()
+    for _ in range(steps):
+        run_partials_combine(s)
+    end.record()
+    torch.cuda.synchronize()
+    return total_ms / steps, sum(kern) / len(kern), start.elapsed_time(end) / steps
 
 
 def _cpu_median(fn, reps=3):
@@ -524,16 +547,82 @@ def bench_dense(dev, reps=3, b=1, h=32, n=8192, d=128, cpu=False, cpu_heads=4):
                          "traffic": None, "algorithmic_flops": flops}}
 
 
+def bench_dense_reference_sweep(dev, reps=20, cpu=False):
+    """The reference's own benchmark of its dense launcher
+    (kessie_kernels_v2.hip:961-1004): launch_kessie_windowed_attn, fp16,
+    B=1, H=8, D=128, N = 512 ... 8,192, causal, full and W=1024.  Calls back
+    to back between two events (the reference times 20 calls between host
+    clocks).  FLOPs = 4 * D * H * (query, visible key) pairs."""
+    import ctypes
+
+    import torch
+
+    from kessie_amd import _lib
+
+    lib = _lib.load()
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    g = torch.Generator(device=dev)
+    g.manual_seed(4)
+    rows = []
+    for n in (512, 1024, 2048, 4096, 8192):
+        q, k, v = (torch.randn(1, 8, n, 128, generator=g, device=dev).half() for _ in range(3))
+        o = torch.empty_like(q)
+        ptr = lambda t: ctypes.c_void_p(t.data_ptr())
+        entry = {"N": n}
+        for w in (0, 1024):
+            call = lambda i: lib.launch_kessie_windowed_attn(ptr(q), ptr(k), ptr(v), ptr(o), ctypes.c_float(128 ** -0.5),
+                                                             1, 8, n, 128, w, 1, st)
+            for _ in range(3):
+                call(0)
+            torch.cuda.synchronize()
+            status, msg = _lib.last_error()
+            if status != _lib.OK:
+                raise RuntimeError(msg)
+            ms = time_back_to_back(call, reps)
+            pairs = sum(min(i + 1, w) if w else i + 1 for i in range(n))
+            tf = 4.0 * 128 * 8 * pairs / (ms * 1e-3) / 1e12
+            key = "full" if w == 0 else "w1024"
+            entry[f"{key}_us"] = round(1000 * ms, 1)
+            entry[f"{key}_tflops"] = round(tf, 1)
+        rows.append(entry)
+    big = rows[-1]
+    pairs8k = 8192 * 8193 // 2
+    res_cpu = None
+    if cpu:
+        from oracle.attention import windowed_attention_ref
+
+        cores = _cpu_threads()
+        qc, kc, vc = (torch.randn(1, 8, 2048, 128, generator=torch.Generator().manual_seed(5)) for _ in range(3))
+        sec = _cpu_median(lambda: windowed_attention_ref(qc, kc, vc, 0, True))
+        res_cpu = {"value": round(4.0 * 128 * 8 * (2048 * 2049 // 2) / sec / 1e12, 4), "unit": "TFLOP/s",
+                   "cores": cores, "kind": "port",
+                   "sample": "N=2,048 of the sweep (fp32 dense oracle: scores, causal mask, softmax, @ V), "
+                             "1 warm-up + median of 3", "seconds": round(sec, 3)}
+    return {"workload": "reference dense-launcher benchmark: launch_kessie_windowed_attn fp16, B=1 H=8 D=128, "
+                        "causal, full and W=1024, N=512..8192",
+            "sweep": rows, "cpu_baseline": res_cpu,
+            "roofline": {"bound": "mfma", "kernel": "prefill_mfma_kernel (table-less pages, key splits) + combine",
+                         "shape": "N=8192 full", "achieved": big["full_tflops"], "peak": BF16_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(big["full_tflops"] / BF16_PEAK_TFLOPS, 4), "traffic": None,
+                         "algorithmic_flops": 4 * 128 * 8 * pairs8k}}
+
+
 def bench_decode_fp32(dev, reps=20, cpu=False):
     """Fog decode on the reference CPU path's shape, fp32: B=1, 32q/8kv, D=128,
     4,096-token context in 16-token pages."""
     import torch
+
+    from kessie_amd import ops
 
     s = setup_decode(dev, b=1, ctx=4096, dtype=torch.float32)
     for _ in range(3):
         run_decode_step(s)
     torch.cuda.synchronize()
     ms = time_back_to_back(lambda i: run_decode_step(s), reps)  # steps back to back, as the headline's
+    # The streaming kernel alone (decode_mfma_f32_kernel), K launches back to
+    # back: at ~16 us an event pair around each launch would add its dispatch.
+    ms_kern = time_back_to_back(lambda i: ops.fog_decode_partials(s["q"], s["pool"], s["table"], s["lens"], s["ctx"],
+                                                                   s["ws"], fog_vscale=s["fog"]), reps)
     res_cpu = None
     if cpu:
         from oracle.attention import paged_decode_ref
@@ -545,8 +634,14 @@ def bench_decode_fp32(dev, reps=20, cpu=False):
         res_cpu = {"value": round(s["bytes"] / sec / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
                    "sample": "the full workload (fp32 paged decode oracle), 1 warm-up + median of 3",
                    "ms": round(1000 * sec, 3)}
+    ach = s["bytes"] / (ms_kern * 1e-3) / 1e9
     return {"workload": "fog decode fp32, B=1, 32q/8kv, D=128, 4096-token context",
-            "ms": round(ms, 5), "gbs": round(s["bytes"] / (ms * 1e-3) / 1e9, 1), "cpu_baseline": res_cpu}
+            "ms": round(ms, 5), "gbs": round(s["bytes"] / (ms * 1e-3) / 1e9, 1), "cpu_baseline": res_cpu,
+            "kernel_ms": round(ms_kern, 5),
+            "roofline": {"bound": "hbm", "kernel": "decode_mfma_f32_kernel", "achieved": round(ach, 1),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
+                         "traffic": read_traffic("decode_mfma_f32_kernel"), "algorithmic_bytes": s["bytes"],
+                         "timing": "20 launches of the streaming kernel back to back between two events"}}
 
 
 def bench_decode_ragged(dev, reps=20, cpu=False, lens=None):
@@ -962,7 +1057,8 @@ def bench_hbm_ceilings(dev, reps=10):
 def pmc_run(dev) -> None:
     """A short fixed sequence of launches for hardware-counter passes
     (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE): a 1 GiB device copy of
-    known size (the calibration kernel), then one decode, one remap in
+    known size (the calibration kernel), then one decode (bf16 B=16 128K, then
+    fp32 B=1 4K, each as partials + combine), one remap in
     interleaved pages and one on a dense K tensor, one gather + evict
     pipeline, one recall-inject, one index query, one HF append + fog launch
     and one chunked prefill of the bench workloads."""
@@ -975,7 +1071,12 @@ def pmc_run(dev) -> None:
     torch.cuda.synchronize()
     del src, dst
     s = setup_decode(dev)
-    run_decode_step(s)
+    run_partials_combine(s)
+    torch.cuda.synchronize()
+    del s
+    torch.cuda.empty_cache()
+    s = setup_decode(dev, b=1, ctx=4096, dtype=torch.float32)
+    run_partials_combine(s)
     torch.cuda.synchronize()
     del s
     torch.cuda.empty_cache()
@@ -1012,6 +1113,7 @@ SECONDARY = {
     "prefill": bench_prefill,
     "dense": bench_dense,
     "dense64": lambda dev, cpu=False: bench_dense(dev, d=64, cpu=cpu),
+    "dense_ref": bench_dense_reference_sweep,
     "fog_bias": bench_fog_bias,
     "recall": bench_recall_inject,
     "index": bench_index_query,
@@ -1060,10 +1162,11 @@ def main():
     s = setup_decode(dev)
     torch.cuda.synchronize()
     log(f"timing decode: warmup {args.warmup}, steps {args.steps}")
-    ms_step, ms_kern = time_decode(s, args.steps, args.warmup)
+    ms_step, ms_kern, ms_two = time_decode(s, args.steps, args.warmup)
     value = s["bytes"] / (ms_step * 1e-3) / 1e9
     achieved = s["bytes"] / (ms_kern * 1e-3) / 1e9
-    log(f"decode: {ms_step:.4f} ms/step, partials kernel {ms_kern:.4f} ms, {value:.1f} GB/s")
+    log(f"decode: {ms_step:.4f} ms/step, partials kernel {ms_kern:.4f} ms, partials + combine {ms_two:.4f} ms, "
+        f"{value:.1f} GB/s")
 
     result = {
         "metric": METRIC,
@@ -1081,7 +1184,7 @@ def main():
         "config": {
             "workload": "fog-attention decode, bf16, batch 16, 32 query / 8 KV heads, head_dim 128, "
                         "131072-token context per sequence in 16-token pages, V-fog alpha 0.5 fog_start 0.5, "
-                        "window 0; step = partials kernel + split combine",
+                        "window 0; step = one kessie_fog_decode_paged call (streaming kernel + split combine)",
             "batch": 16, "ctx": 131072, "q_heads": 32, "kv_heads": 8, "head_dim": 128, "page_size": 16,
             "splits": _lib.load().kessie_fog_decode_num_splits(16, 8, 131072, 16),
             "algorithmic_bytes": s["bytes"],
@@ -1091,7 +1194,10 @@ def main():
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic("decode_mfma_kernel"),
             "kernel": "decode_mfma_kernel", "kernel_ms": round(ms_kern, 5),
+            "kernel_timing": "event pair around each of K launches of kessie_fog_decode_partials (the streaming "
+                             "kernel alone, plain split layout), on the stream it runs on",
         },
+        "partials_combine_ms_per_step": round(ms_two, 5),
         "device": {"name": props.name, "cus": props.multi_processor_count},
     }
     if not args.no_cpu:
@@ -1132,6 +1238,9 @@ def main():
         torch.cuda.empty_cache()
         log("secondary: dense fused fog attention, head_dim 64 (reference launcher)")
         sec["dense_fused_fog_8k_d64"] = bench_dense(dev, d=64, cpu=not args.no_cpu)
+        torch.cuda.empty_cache()
+        log("secondary: the reference's dense-launcher benchmark (B=1 H=8 D=128, N=512..8192)")
+        sec["dense_reference_sweep"] = bench_dense_reference_sweep(dev, cpu=not args.no_cpu)
         torch.cuda.empty_cache()
         log("secondary: fog bias producer")
         sec["fog_bias_131k"] = bench_fog_bias(dev)
