@@ -237,6 +237,166 @@ __global__ void topk_unpack_kernel(const uint64_t* __restrict__ keys, int k, int
   if (scores) scores[i] = ok ? unordered(~(uint32_t)(key >> 32)) : -__builtin_huge_valf();
 }
 
+// Fused path (k <= kFusedK): the scan keeps each workgroup's top-k.  A wave
+// scans 8 rows, two per 16-lane group with their loads issued together (short
+// dependency chains and many waves, as the plain scan); the workgroup's 64
+// keys go to LDS, one per row, and its first wave takes the k smallest by k
+// rounds of a wave-wide minimum (the device library's DPP reduction; keys are
+// unique).  One workgroup then selects the first k of all workgroups' lists:
+// every lane keeps its own sorted list of K >= k keys (branchless insertion,
+// its keys loaded first, all at once), each wave takes the k smallest of its
+// lanes' lists by k rounds of the wave minimum, and one wave does the same
+// over the waves' lists and writes the ids and scores.  Two launches instead
+// of the scan and three passes of bitonic merges (a 64-key bitonic merge is a
+// chain of cross-lane shuffles: ~3 us).
+constexpr int kFusedK = 16;
+constexpr int kFusedThreads = 512;                 // scan workgroup: 8 waves
+constexpr int kFusedRowsWg = 8 * kFusedThreads / 64;  // 64 rows per workgroup
+constexpr int kMergeThreads = 1024;                // merge workgroup: 16 waves
+constexpr int kMergeLoads = 8;                     // keys a merge lane loads at once
+
+extern "C" __device__ unsigned long long __ockl_wfred_min_u64(unsigned long long);
+
+template <typename T>
+__global__ __launch_bounds__(kFusedThreads) void scan_topk_kernel(const T* __restrict__ rows, int64_t row_stride,
+                                                                  int n, int d, const float* __restrict__ q,
+                                                                  float* __restrict__ sims, int mode, int k,
+                                                                  uint64_t* __restrict__ keys_out) {
+  typedef typename Row16<T>::type V;
+  constexpr int N = Row16<T>::N;
+  __shared__ float qs[1024];
+  __shared__ float red[kFusedThreads / 64];
+  __shared__ uint64_t wg_keys[kFusedRowsWg];
+  float part = 0.0f;
+  for (int i = threadIdx.x; i < d; i += kFusedThreads) {
+    const float x = q[i];
+    qs[i] = x;
+    part += x * x;
+  }
+  for (int off = 32; off > 0; off >>= 1) part += __shfl_xor(part, off);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = part;
+  __syncthreads();
+  float qq = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kFusedThreads / 64; ++w) qq += red[w];
+  const float q_scale = inv_norm(qq, mode);
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int sub = lane & 15, grp = lane >> 4;
+  // Rows of this wave's groups: r0 + 2 grp + u, u = 0, 1.
+  const int64_t r0 = (int64_t)blockIdx.x * kFusedRowsWg + 8 * wave;
+  const int chunks = d / N;
+  float dot[2] = {0.0f, 0.0f}, ee[2] = {0.0f, 0.0f};
+  int64_t r[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) r[u] = r0 + 2 * grp + u;
+  for (int c = sub; c < chunks; c += 16) {
+    V v[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int64_t rr = r[u] < n ? r[u] : 0;
+      v[u] = __builtin_nontemporal_load(reinterpret_cast<const V*>(rows + rr * row_stride) + c);
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int e = 0; e < N; ++e) {
+        const float x = to_f32(v[u][e]);
+        dot[u] += x * qs[c * N + e];
+        ee[u] += x * x;
+      }
+  }
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const float dd = sum16(dot[u]), nn = sum16(ee[u]);
+    const float sim = dd * q_scale * inv_norm(nn, mode);
+    const bool in = r[u] < n;
+    if (sub == 0) {
+      if (in) sims[r[u]] = sim;
+      wg_keys[8 * wave + 2 * grp + u] = in ? make_key(sim, (uint32_t)r[u]) : ~0ull;
+    }
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  uint64_t key = wg_keys[lane];
+  for (int i = 0; i < k; ++i) {
+    const uint64_t m = __ockl_wfred_min_u64(key);
+    if (key == m) key = ~0ull;  // keys are unique, ~0 aside
+    if (lane == 0) keys_out[(int64_t)blockIdx.x * k + i] = m;
+  }
+}
+
+// Sorted (ascending) list of a lane's K smallest keys so far.
+template <int K>
+struct LaneList {
+  uint64_t v[K];
+  __device__ void clear() {
+#pragma unroll
+    for (int j = 0; j < K; ++j) v[j] = ~0ull;
+  }
+  __device__ void insert(uint64_t x) {  // branchless: each slot takes the new key, its old value or its left neighbour
+#pragma unroll
+    for (int j = K - 1; j > 0; --j) v[j] = x < v[j - 1] ? v[j - 1] : (x < v[j] ? x : v[j]);
+    v[0] = x < v[0] ? x : v[0];
+  }
+  __device__ void pop() {
+#pragma unroll
+    for (int j = 0; j < K - 1; ++j) v[j] = v[j + 1];
+    v[K - 1] = ~0ull;
+  }
+};
+
+// The k smallest keys over the wave's lane lists, in order, to out[0..k).
+template <int K>
+__device__ __forceinline__ void wave_take(LaneList<K>& L, int k, uint64_t* out) {
+  const int lane = threadIdx.x & 63;
+  for (int i = 0; i < k; ++i) {
+    const uint64_t m = __ockl_wfred_min_u64(L.v[0]);
+    if (L.v[0] == m && m != ~0ull) L.pop();
+    if (lane == 0) out[i] = m;
+  }
+}
+
+template <int K>
+__global__ __launch_bounds__(kMergeThreads) void topk_merge_kernel(const uint64_t* __restrict__ keys, int64_t nkeys,
+                                                                   int k, int32_t* __restrict__ ids,
+                                                                   float* __restrict__ scores, int top_k) {
+  constexpr int W = kMergeThreads / 64;
+  __shared__ uint64_t lists[W * K];
+  __shared__ uint64_t best[K];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  LaneList<K> L;
+  L.clear();
+  for (int64_t i0 = threadIdx.x; i0 < nkeys; i0 += (int64_t)kMergeLoads * kMergeThreads) {
+    uint64_t x[kMergeLoads];  // loaded together, then inserted
+#pragma unroll
+    for (int j = 0; j < kMergeLoads; ++j) {
+      const int64_t i = i0 + (int64_t)j * kMergeThreads;
+      x[j] = i < nkeys ? keys[i] : ~0ull;
+    }
+#pragma unroll
+    for (int j = 0; j < kMergeLoads; ++j) L.insert(x[j]);
+  }
+  wave_take(L, k, lists + wave * K);
+  __syncthreads();
+  if (wave != 0) return;
+  L.clear();
+  for (int i = lane; i < W * K; i += 64)
+    if (i % K < k) L.insert(lists[i]);
+  wave_take(L, k, best);
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  for (int i = lane; i < top_k; i += 64) {
+    const uint64_t key = i < k ? best[i] : ~0ull;
+    const bool ok = key != ~0ull;
+    if (ids) ids[i] = ok ? (int32_t)(key & 0xffffffffu) : -1;
+    if (scores) scores[i] = ok ? unordered(~(uint32_t)(key >> 32)) : -__builtin_huge_valf();
+  }
+}
+
+// Workgroups of the fused scan for n rows (each writes k keys).
+inline int64_t fused_wgs(int64_t n) { return div_up(n, (int64_t)kFusedRowsWg); }
+
 // Keys written by pass p, and the number of passes, for n inputs and top k.
 struct Plan {
   int passes;
@@ -280,6 +440,7 @@ using namespace kessie::index;
 extern "C" size_t kessie_index_query_workspace_bytes(int num_chunks, int top_k) {
   if (num_chunks <= 0 || top_k <= 0) return 0;
   const int k = top_k < num_chunks ? top_k : num_chunks;
+  if (k <= kFusedK) return (size_t)((fused_wgs(num_chunks) * k * sizeof(uint64_t) + 255) / 256 * 256);
   const Plan p = plan_for(num_chunks, k);
   // Two ping-pong key arrays.
   return 2 * (size_t)((p.max_keys * sizeof(uint64_t) + 255) / 256 * 256);
@@ -306,6 +467,44 @@ extern "C" int kessie_index_query(const void* index_embeds, int64_t row_stride, 
                  (long long)row_stride, embed_dim);
   KESSIE_REQUIRE(norm_mode >= 0 && norm_mode <= 2, KESSIE_ERR_INVALID, "index query: norm_mode %d", norm_mode);
   const hipStream_t s = as_stream(stream);
+  const int kk = top_k < num_chunks ? top_k : num_chunks;
+  if (kk > 0 && kk <= kFusedK) {
+    // The scan keeps each wave's top-k, one workgroup merges them.
+    const size_t need = kessie_index_query_workspace_bytes(num_chunks, kk);
+    KESSIE_REQUIRE(workspace && workspace_bytes >= need, KESSIE_ERR_WORKSPACE,
+                   "index query: workspace of %zu bytes needed, got %zu", need, workspace_bytes);
+    KESSIE_REQUIRE(aligned16(workspace), KESSIE_ERR_INVALID, "index query: workspace not 16-byte aligned");
+    uint64_t* keys = static_cast<uint64_t*>(workspace);
+    const int64_t wgs = fused_wgs(num_chunks);
+    const dim3 grid((unsigned)wgs);
+    switch (dtype) {
+      case KESSIE_DTYPE_F32:
+        hipLaunchKernelGGL(scan_topk_kernel<float>, grid, dim3(kFusedThreads), 0, s,
+                           static_cast<const float*>(index_embeds), row_stride, num_chunks, embed_dim, query_embed,
+                           similarities, norm_mode, kk, keys);
+        break;
+      case KESSIE_DTYPE_BF16:
+        hipLaunchKernelGGL(scan_topk_kernel<bf16_t>, grid, dim3(kFusedThreads), 0, s,
+                           static_cast<const bf16_t*>(index_embeds), row_stride, num_chunks, embed_dim, query_embed,
+                           similarities, norm_mode, kk, keys);
+        break;
+      default:
+        hipLaunchKernelGGL(scan_topk_kernel<f16_t>, grid, dim3(kFusedThreads), 0, s,
+                           static_cast<const f16_t*>(index_embeds), row_stride, num_chunks, embed_dim, query_embed,
+                           similarities, norm_mode, kk, keys);
+    }
+    if (check_launch("index query scan + top-k") != KESSIE_OK) return last_status();
+    if (kk <= 4)
+      hipLaunchKernelGGL(topk_merge_kernel<4>, dim3(1), dim3(kMergeThreads), 0, s, keys, wgs * kk, kk, top_ids,
+                         top_scores, top_k);
+    else if (kk <= 8)
+      hipLaunchKernelGGL(topk_merge_kernel<8>, dim3(1), dim3(kMergeThreads), 0, s, keys, wgs * kk, kk, top_ids,
+                         top_scores, top_k);
+    else
+      hipLaunchKernelGGL(topk_merge_kernel<16>, dim3(1), dim3(kMergeThreads), 0, s, keys, wgs * kk, kk, top_ids,
+                         top_scores, top_k);
+    return check_launch("index query top-k merge");
+  }
   if (num_chunks > 0) {
     int st = KESSIE_OK;
     switch (dtype) {

@@ -96,3 +96,32 @@ def test_vector_index_class(dev):
     assert idx.search(np.zeros(256, np.float32)) == []
     idx.rebuild([], [])
     assert idx.count == 0 and idx.search(q) == []
+
+
+@pytest.mark.parametrize("n,k,dtype", [(200000, 16, torch.float32), (129, 16, torch.float32), (130, 1, torch.float32),
+                                       (78125, 2, torch.bfloat16), (257, 7, torch.float16)])
+def test_index_fused_scan_topk(dev, n, k, dtype):
+    """k <= 16 runs the scan with each wave's top-k kept in registers and one
+    merge launch: bit-exact against a sort of the kernel's own similarities,
+    with rows spread over many waves (the last one partial) and exact
+    duplicates of the best rows placed in far-apart waves (ties go to the lower
+    row)."""
+    from kessie_amd import ops
+
+    d = 256
+    mat = randn((n, d), torch.float32, dev, 6)
+    q = randn((d,), torch.float32, dev, 7)
+    mat[n // 2] = q * 2.0           # the best row, and copies of it further on
+    mat[n - 1] = q * 0.5
+    if n > 3:
+        mat[1] = q
+    mat = mat.to(dtype)
+    sims, ids, scores = ops.index_query(mat, q, top_k=k)
+    torch.cuda.synchronize()
+    ref = cosine_ref(q.cpu().numpy(), mat.float().cpu().numpy(), 0)
+    tol = 2e-6 if dtype == torch.float32 else 1e-5
+    assert np.abs(sims.cpu().numpy() - ref).max() <= tol
+    _check_topk(sims, ids, scores, ref, k, tol)
+    top = ids.cpu().tolist()
+    best = sorted({n // 2, n - 1} | ({1} if n > 3 else set()))
+    assert top[:len(best)] == best if k >= len(best) else top[:k] == best[:k]
