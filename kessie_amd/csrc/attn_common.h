@@ -144,5 +144,13 @@ inline int env_int(const char* name, int dflt) {
 int prefill_mfma(Params& p, int dtype, hipStream_t stream);
 bool prefill_mfma_ok(const Params& p, int dtype);
 
+// fp32 chunked prefill on MFMA (fog_prefill_f32.hip): p.num_splits from
+// prefill_f32_splits; with more than one the partials go to p.ws_* for the
+// caller's combine.
+bool prefill_f32_ok(const Params& p, int dtype);
+int prefill_f32_splits(int B, int C, int Hkv, int G, int max_ctx);
+int prefill_f32(const Params& p, hipStream_t stream);
+int device_cus();
+
 }  // namespace attn
 }  // namespace kessie

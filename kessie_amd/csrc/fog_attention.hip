@@ -1513,8 +1513,9 @@ extern "C" size_t kessie_fog_prefill_workspace_bytes(int batch, int num_q_tokens
   (void)dtype;
   if (batch <= 0 || num_q_tokens <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0) return 0;
   const int G = num_q_heads / num_kv_heads;
-  const int S = max(kessie::attn::prefill_splits(batch, num_q_tokens, num_kv_heads, G, max_ctx, page_size),
-                    kessie::attn::prefill_mfma_splits(batch, num_q_tokens, num_kv_heads, G, max_ctx));
+  const int S = max(max(kessie::attn::prefill_splits(batch, num_q_tokens, num_kv_heads, G, max_ctx, page_size),
+                        kessie::attn::prefill_mfma_splits(batch, num_q_tokens, num_kv_heads, G, max_ctx)),
+                    kessie::attn::prefill_f32_splits(batch, num_q_tokens, num_kv_heads, G, max_ctx));
   return kessie::attn::partial_bytes((int64_t)batch * num_q_tokens * num_q_heads, S, head_dim);
 }
 
@@ -1606,6 +1607,23 @@ extern "C" int kessie_fog_prefill_paged(const void* q, const void* kv_pool, int 
   KESSIE_REQUIRE(kv_stride >= 0, KESSIE_ERR_INVALID, "fog prefill: kv_stride %lld", (long long)kv_stride);
   if (batch == 0) return KESSIE_OK;
   if (prefill_mfma_ok(p, dtype)) return run_prefill_mfma(p, dtype, workspace, workspace_bytes, stream);
+  if (prefill_f32_ok(p, dtype)) {
+    p.num_splits = prefill_f32_splits(batch, num_q_tokens, num_kv_heads, p.G, max_ctx);
+    p.direct_out = p.num_splits == 1 ? 1 : 0;
+    const int64_t rows = (int64_t)batch * num_q_tokens * num_q_heads;
+    if (!p.direct_out) {
+      const size_t need = partial_bytes(rows, p.num_splits, head_dim);
+      KESSIE_REQUIRE(workspace != nullptr && workspace_bytes >= need, KESSIE_ERR_WORKSPACE,
+                     "fog prefill: workspace of %zu bytes needed, got %zu", need, workspace_bytes);
+      KESSIE_REQUIRE(aligned16(workspace), KESSIE_ERR_INVALID, "fog prefill: workspace not 16-byte aligned");
+      carve_workspace(p, workspace, rows);
+    }
+    const hipStream_t s = as_stream(stream);
+    const int st = prefill_f32(p, s);
+    if (st != KESSIE_OK || p.direct_out) return st;
+    launch_combine<float>(p, rows, s);
+    return check_launch("fog prefill (combine)");
+  }
   p.num_splits = prefill_splits(batch, num_q_tokens, num_kv_heads, p.G, max_ctx, page_size);
   p.direct_out = p.num_splits == 1 ? 1 : 0;
   p.launch_combine = 1;

@@ -1,6 +1,6 @@
 """GPU parity: chunked-prefill fog attention (MFMA kernel and the generic
 kernel) vs the CPU oracle.  bf16/fp16: |gpu - ref| <= 2e-2 + 1e-2*|ref|;
-fp32 (generic kernel): 1e-5."""
+fp32 (fp32 MFMA kernel for head_dim 128, else the generic kernel): 1e-5."""
 import pytest
 import torch
 
@@ -446,3 +446,53 @@ def test_prefill_longest_first_dispatch(dev, monkeypatch):
         ref = paged_prefill_ref(q[i:i + 1].cpu(), pool.cpu(), table[i:i + 1].cpu(), lens[i:i + 1].cpu(),
                                 vs[i].cpu(), None, 0, rows=rows)
         _check(out[i:i + 1, rows], ref, torch.bfloat16)
+
+
+@pytest.mark.parametrize("hq,hkv,c,ctxs,fog,window,page_size,splits", [
+    (32, 8, 100, [1000, 777], "vscale", 0, 16, 0),    # two sequences, one ragged
+    (8, 8, 33, [300], "bias", 0, 16, 0),               # GQA 1
+    (12, 3, 65, [900], "both", 50, 16, 0),             # GQA 4 with three kv heads, window
+    (24, 8, 40, [2000], "none", 0, 32, 0),             # GQA 3 (positions per workgroup not a power of two), 32-token pages
+    (32, 8, 300, [300], "vscale", 0, 16, 0),           # a fresh prompt: the chunk is the whole context
+    (32, 8, 50, [51], "none", 0, 16, 0),               # one cached token before the chunk
+    (16, 4, 20, [5000], "vscale", 0, 64, 5),           # forced key splits (partials + combine), 64-token pages
+    (128, 8, 7, [4000, 7], "bias", 1000, 16, 0),       # GQA 16, window, a context that is only the chunk
+])
+def test_prefill_fp32_mfma_matches_oracle_and_generic(dev, monkeypatch, hq, hkv, c, ctxs, fog, window, page_size,
+                                                      splits):
+    """fp32 chunked prefill on v_mfma_f32_16x16x4_f32 (fp32 throughout):
+    within the fp32 tolerance (1e-5) of the oracle and of the generic kernel,
+    and not the generic kernel's bits (the MFMA route ran)."""
+    from kessie_amd import ops
+
+    if splits:
+        monkeypatch.setenv("KESSIE_PREFILL_SPLITS", str(splits))
+    b = len(ctxs)
+    mx = max(ctxs)
+    q, pool, table, lens = _case(dev, b, c, ctxs, hq, hkv, torch.float32, seed=hq + c, page_size=page_size)
+    vs = torch.rand(b, mx, generator=gen(dev, 41), device=dev) if fog in ("vscale", "both") else None
+    bias = fog_bias(mx, 0.5, 0.5, {3, mx // 2}, 0.1).to(dev) if fog in ("bias", "both") else None
+    out = ops.fog_prefill(q, pool, table, lens, mx, fog_vscale=vs, fog_bias=bias, window=window)
+    monkeypatch.setenv("KESSIE_FORCE_GENERIC", "1")
+    gen_out = ops.fog_prefill(q, pool, table, lens, mx, fog_vscale=vs, fog_bias=bias, window=window)
+    torch.cuda.synchronize()
+    ref = paged_prefill_ref(q.cpu(), pool.cpu(), table.cpu(), lens.cpu(), None if vs is None else vs.cpu(),
+                            None if bias is None else bias.cpu(), window)
+    _check(out, ref, torch.float32)
+    _check(gen_out, ref, torch.float32)
+    assert not torch.equal(out, gen_out)
+
+
+def test_prefill_fp32_mfma_bad_page(dev):
+    """An invalid page id on the fp32 MFMA route masks its 16 tokens:
+    non-causal, so the oracle is the same context without that page."""
+    from kessie_amd import ops
+
+    q, pool, table, lens = _case(dev, 1, 40, [400], 32, 8, torch.float32, seed=9)
+    table[0, 3] = -1
+    out = ops.fog_prefill(q, pool, table, lens, 400, causal=False)
+    torch.cuda.synchronize()
+    keep = [i for i in range(table.shape[1]) if i != 3]
+    ref = paged_prefill_ref(q.cpu(), pool.cpu(), table.cpu()[:, keep].contiguous(), torch.tensor([400 - 16]),
+                            causal=False)
+    _check(out, ref, torch.float32)
