@@ -458,11 +458,14 @@ __device__ __forceinline__ void store2<f16_t>(f16_t* dst, float a, float b) {
 // order, as combine_kernel (max and sum over the splits by the same butterfly
 // -- its first two steps, across halves and quarters of the wave, only add
 // zeros there -- and the columns in GR groups of every GR-th split, added in
-// group order), so the two kernels give the same bits.
+// group order), so the two kernels give the same bits.  SM bounds the split
+// count of an instance (4, 8 or 16): the partial registers are sized by it,
+// so S <= 4 (the dense launchers, most split prefills) runs at 8 waves per
+// SIMD instead of the 3 that room for 16 splits leaves.
 constexpr int kCombRows = 4;                   // rows per wave
 constexpr int kCombRowsPerWg = 4 * kCombRows;  // four waves
 
-template <typename T, int D>
+template <typename T, int D, int SM>
 __global__ __launch_bounds__(256) void combine_rows_kernel(Params p, int64_t rows) {
   constexpr int NC = D / 64;                       // columns per lane
   constexpr int GR = kCombineThreads / (D / 2);    // combine_kernel's split groups
@@ -478,12 +481,12 @@ __global__ __launch_bounds__(256) void combine_rows_kernel(Params p, int64_t row
   // Partials: v[r][sp][c] of row row0 + r (clamped into range), split sp < S,
   // NC columns per load.
   typedef float fNC __attribute__((ext_vector_type(NC)));
-  fNC v[kCombRows][16];
+  fNC v[kCombRows][SM];
 #pragma unroll
   for (int r = 0; r < kCombRows; ++r) {
     const float* o = p.ws_o + min(row0 + r, rows - 1) * S * D + NC * lane;
 #pragma unroll
-    for (int sp = 0; sp < 16; ++sp)
+    for (int sp = 0; sp < SM; ++sp)
       v[r][sp] = sp < S ? *reinterpret_cast<const fNC*>(o + (int64_t)sp * D) : fNC{};
   }
   float mx = m;
@@ -503,7 +506,7 @@ __global__ __launch_bounds__(256) void combine_rows_kernel(Params p, int64_t row
 #pragma unroll
       for (int c = 0; c < NC; ++c) part[g][c] = 0.0f;
 #pragma unroll
-    for (int sp = 0; sp < 16; ++sp) {
+    for (int sp = 0; sp < SM; ++sp) {
       if (sp < S) {  // uniform
         const float es = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e), 16 * r + sp));
 #pragma unroll
@@ -543,10 +546,22 @@ void launch_combine(const Params& p, int64_t rows, hipStream_t s) {
   const bool even = ((p.o_bs | p.o_is | p.o_hs) & 1) == 0 && ((uintptr_t)p.out & 3) == 0;  // packed stores
   if (rows >= 4096 && !p.balanced && p.num_splits <= 16 && (p.D == 128 || p.D == 64) && even) {
     const dim3 grid((unsigned)div_up(rows, (int64_t)kCombRowsPerWg));
-    if (p.D == 128)
-      hipLaunchKernelGGL((combine_rows_kernel<T, 128>), grid, dim3(256), 0, s, p, rows);
-    else
-      hipLaunchKernelGGL((combine_rows_kernel<T, 64>), grid, dim3(256), 0, s, p, rows);
+    const int sm = p.num_splits <= 4 ? 4 : p.num_splits <= 8 ? 8 : 16;
+    if (p.D == 128) {
+      if (sm == 4)
+        hipLaunchKernelGGL((combine_rows_kernel<T, 128, 4>), grid, dim3(256), 0, s, p, rows);
+      else if (sm == 8)
+        hipLaunchKernelGGL((combine_rows_kernel<T, 128, 8>), grid, dim3(256), 0, s, p, rows);
+      else
+        hipLaunchKernelGGL((combine_rows_kernel<T, 128, 16>), grid, dim3(256), 0, s, p, rows);
+    } else {
+      if (sm == 4)
+        hipLaunchKernelGGL((combine_rows_kernel<T, 64, 4>), grid, dim3(256), 0, s, p, rows);
+      else if (sm == 8)
+        hipLaunchKernelGGL((combine_rows_kernel<T, 64, 8>), grid, dim3(256), 0, s, p, rows);
+      else
+        hipLaunchKernelGGL((combine_rows_kernel<T, 64, 16>), grid, dim3(256), 0, s, p, rows);
+    }
     return;
   }
   hipLaunchKernelGGL(combine_kernel<T>, dim3((unsigned)rows, combine_dsplit(rows, p.D)), dim3(kCombineThreads), 0,

@@ -238,24 +238,48 @@ __global__ void topk_unpack_kernel(const uint64_t* __restrict__ keys, int k, int
 }
 
 // Fused path (k <= kFusedK): the scan keeps each workgroup's top-k.  A wave
-// scans 8 rows, two per 16-lane group with their loads issued together (short
-// dependency chains and many waves, as the plain scan); the workgroup's 64
-// keys go to LDS, one per row, and its first wave takes the k smallest by k
-// rounds of a wave-wide minimum (the device library's DPP reduction; keys are
-// unique).  One workgroup then selects the first k of all workgroups' lists:
-// every lane keeps its own sorted list of K >= k keys (branchless insertion,
-// its keys loaded first, all at once), each wave takes the k smallest of its
-// lanes' lists by k rounds of the wave minimum, and one wave does the same
-// over the waves' lists and writes the ids and scores.  Two launches instead
-// of the scan and three passes of bitonic merges (a 64-key bitonic merge is a
-// chain of cross-lane shuffles: ~3 us).
+// scans 16 rows, four per 16-lane group with their loads issued together;
+// the workgroup's 128 keys go to LDS, one per row, and its first wave selects
+// the k smallest.  One workgroup then selects the first k of all workgroups'
+// lists.  Selection is k rounds of: each lane's smallest key, the wave's
+// smallest of those (the device library's DPP reduction), taken out of its
+// lane and kept by lane r of round r -- no sorted lists (inserting each key
+// into a lane's sorted list of 8 took ~600 VALU instructions per wave and left
+// the merge at 7.9 us; now 5.6 us with 16 merge waves, and 8 waves of 6 keys
+// each save another 0.9 us, the per-wave reduction being the fixed cost).
+// 128 rows per workgroup: 611 workgroups for 78,125 rows, one round on the
+// chip, half the keys of 64-row workgroups to merge (64, 256 rows, or 2 or 8
+// rows per 16-lane group: 24.1-26.7 us against 22.5).  The selection at the
+// end of each scan workgroup costs ~1 us of the scan's 17 us.
 constexpr int kFusedK = 16;
-constexpr int kFusedThreads = 512;                 // scan workgroup: 8 waves
-constexpr int kFusedRowsWg = 8 * kFusedThreads / 64;  // 64 rows per workgroup
-constexpr int kMergeThreads = 1024;                // merge workgroup: 16 waves
-constexpr int kMergeLoads = 8;                     // keys a merge lane loads at once
+constexpr int kFusedThreads = 512;                                      // scan workgroup: 8 waves
+constexpr int kFusedRowsGroup = 4;                                      // rows per 16-lane group
+constexpr int kFusedRowsWave = 4 * kFusedRowsGroup;                     // 16 rows per wave
+constexpr int kFusedRowsWg = kFusedRowsWave * kFusedThreads / 64;       // 128 rows per workgroup
+constexpr int kMergeThreads = 512;                                      // merge workgroup: 8 waves
+constexpr int kMergeLoads = 6;                                          // keys a merge lane takes per pass
 
 extern "C" __device__ unsigned long long __ockl_wfred_min_u64(unsigned long long);
+
+// k rounds of selection over the keys the wave's lanes hold (x[0..M) each,
+// unique but for the ~0 padding): round r takes the wave's smallest key out
+// of its lane, and lane r keeps it.  Returns the lane's kept key (~0 for
+// lanes >= k).  Every lane of the wave must take part.
+template <int M>
+__device__ __forceinline__ uint64_t wave_select(uint64_t (&x)[M], int k) {
+  const int lane = threadIdx.x & 63;
+  uint64_t kept = ~0ull;
+  for (int r = 0; r < k; ++r) {
+    uint64_t lm = x[0];
+#pragma unroll
+    for (int j = 1; j < M; ++j) lm = x[j] < lm ? x[j] : lm;
+    const uint64_t m = __ockl_wfred_min_u64(lm);
+    if (lane == r) kept = m;
+#pragma unroll
+    for (int j = 0; j < M; ++j) x[j] = x[j] == m ? ~0ull : x[j];
+  }
+  return kept;
+}
 
 template <typename T>
 __global__ __launch_bounds__(kFusedThreads) void scan_topk_kernel(const T* __restrict__ rows, int64_t row_stride,
@@ -264,6 +288,7 @@ __global__ __launch_bounds__(kFusedThreads) void scan_topk_kernel(const T* __res
                                                                   uint64_t* __restrict__ keys_out) {
   typedef typename Row16<T>::type V;
   constexpr int N = Row16<T>::N;
+  constexpr int R = kFusedRowsGroup;
   __shared__ float qs[1024];
   __shared__ float red[kFusedThreads / 64];
   __shared__ uint64_t wg_keys[kFusedRowsWg];
@@ -283,22 +308,26 @@ __global__ __launch_bounds__(kFusedThreads) void scan_topk_kernel(const T* __res
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int sub = lane & 15, grp = lane >> 4;
-  // Rows of this wave's groups: r0 + 2 grp + u, u = 0, 1.
-  const int64_t r0 = (int64_t)blockIdx.x * kFusedRowsWg + 8 * wave;
+  // Rows of this wave's groups: r0 + R grp + u, u < R.
+  const int64_t r0 = (int64_t)blockIdx.x * kFusedRowsWg + kFusedRowsWave * wave;
   const int chunks = d / N;
-  float dot[2] = {0.0f, 0.0f}, ee[2] = {0.0f, 0.0f};
-  int64_t r[2];
+  float dot[R], ee[R];
+  int64_t r[R];
 #pragma unroll
-  for (int u = 0; u < 2; ++u) r[u] = r0 + 2 * grp + u;
+  for (int u = 0; u < R; ++u) {
+    dot[u] = 0.0f;
+    ee[u] = 0.0f;
+    r[u] = r0 + R * grp + u;
+  }
   for (int c = sub; c < chunks; c += 16) {
-    V v[2];
+    V v[R];
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
+    for (int u = 0; u < R; ++u) {
       const int64_t rr = r[u] < n ? r[u] : 0;
       v[u] = __builtin_nontemporal_load(reinterpret_cast<const V*>(rows + rr * row_stride) + c);
     }
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
+    for (int u = 0; u < R; ++u)
 #pragma unroll
       for (int e = 0; e < N; ++e) {
         const float x = to_f32(v[u][e]);
@@ -307,87 +336,53 @@ __global__ __launch_bounds__(kFusedThreads) void scan_topk_kernel(const T* __res
       }
   }
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
+  for (int u = 0; u < R; ++u) {
     const float dd = sum16(dot[u]), nn = sum16(ee[u]);
     const float sim = dd * q_scale * inv_norm(nn, mode);
     const bool in = r[u] < n;
     if (sub == 0) {
       if (in) sims[r[u]] = sim;
-      wg_keys[8 * wave + 2 * grp + u] = in ? make_key(sim, (uint32_t)r[u]) : ~0ull;
+      wg_keys[kFusedRowsWave * wave + R * grp + u] = in ? make_key(sim, (uint32_t)r[u]) : ~0ull;
     }
   }
   __syncthreads();
   if (wave != 0) return;
-  uint64_t key = wg_keys[lane];
-  for (int i = 0; i < k; ++i) {
-    const uint64_t m = __ockl_wfred_min_u64(key);
-    if (key == m) key = ~0ull;  // keys are unique, ~0 aside
-    if (lane == 0) keys_out[(int64_t)blockIdx.x * k + i] = m;
-  }
+  uint64_t x[(kFusedRowsWg + 63) / 64];
+#pragma unroll
+  for (int j = 0; j < (kFusedRowsWg + 63) / 64; ++j) x[j] = 64 * j + lane < kFusedRowsWg ? wg_keys[64 * j + lane] : ~0ull;
+  const uint64_t kept = wave_select(x, k);
+  if (lane < k) keys_out[(int64_t)blockIdx.x * k + lane] = kept;
 }
 
-// Sorted (ascending) list of a lane's K smallest keys so far.
-template <int K>
-struct LaneList {
-  uint64_t v[K];
-  __device__ void clear() {
-#pragma unroll
-    for (int j = 0; j < K; ++j) v[j] = ~0ull;
-  }
-  __device__ void insert(uint64_t x) {  // branchless: each slot takes the new key, its old value or its left neighbour
-#pragma unroll
-    for (int j = K - 1; j > 0; --j) v[j] = x < v[j - 1] ? v[j - 1] : (x < v[j] ? x : v[j]);
-    v[0] = x < v[0] ? x : v[0];
-  }
-  __device__ void pop() {
-#pragma unroll
-    for (int j = 0; j < K - 1; ++j) v[j] = v[j + 1];
-    v[K - 1] = ~0ull;
-  }
-};
-
-// The k smallest keys over the wave's lane lists, in order, to out[0..k).
-template <int K>
-__device__ __forceinline__ void wave_take(LaneList<K>& L, int k, uint64_t* out) {
-  const int lane = threadIdx.x & 63;
-  for (int i = 0; i < k; ++i) {
-    const uint64_t m = __ockl_wfred_min_u64(L.v[0]);
-    if (L.v[0] == m && m != ~0ull) L.pop();
-    if (lane == 0) out[i] = m;
-  }
-}
-
-template <int K>
+// The first k of nkeys keys: each wave selects the first k of its share,
+// carried from pass to pass (kMergeLoads keys per lane per pass), then the
+// first wave selects over the waves' lists and writes ids and scores.
 __global__ __launch_bounds__(kMergeThreads) void topk_merge_kernel(const uint64_t* __restrict__ keys, int64_t nkeys,
                                                                    int k, int32_t* __restrict__ ids,
                                                                    float* __restrict__ scores, int top_k) {
   constexpr int W = kMergeThreads / 64;
-  __shared__ uint64_t lists[W * K];
-  __shared__ uint64_t best[K];
+  __shared__ uint64_t lists[W * kFusedK];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  LaneList<K> L;
-  L.clear();
-  for (int64_t i0 = threadIdx.x; i0 < nkeys; i0 += (int64_t)kMergeLoads * kMergeThreads) {
-    uint64_t x[kMergeLoads];  // loaded together, then inserted
+  uint64_t kept = ~0ull;  // lane r < k: the wave's r-th key so far
+  for (int64_t base = 0; base < nkeys; base += (int64_t)kMergeLoads * kMergeThreads) {  // uniform trip count
+    uint64_t x[kMergeLoads + 1];
 #pragma unroll
     for (int j = 0; j < kMergeLoads; ++j) {
-      const int64_t i = i0 + (int64_t)j * kMergeThreads;
+      const int64_t i = base + (int64_t)j * kMergeThreads + threadIdx.x;
       x[j] = i < nkeys ? keys[i] : ~0ull;
     }
-#pragma unroll
-    for (int j = 0; j < kMergeLoads; ++j) L.insert(x[j]);
+    x[kMergeLoads] = kept;
+    kept = wave_select(x, k);
   }
-  wave_take(L, k, lists + wave * K);
+  if (lane < kFusedK) lists[wave * kFusedK + lane] = kept;
   __syncthreads();
   if (wave != 0) return;
-  L.clear();
-  for (int i = lane; i < W * K; i += 64)
-    if (i % K < k) L.insert(lists[i]);
-  wave_take(L, k, best);
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  uint64_t y[W * kFusedK / 64];
+#pragma unroll
+  for (int j = 0; j < W * kFusedK / 64; ++j) y[j] = lists[64 * j + lane];
+  const uint64_t best = wave_select(y, k);
   for (int i = lane; i < top_k; i += 64) {
-    const uint64_t key = i < k ? best[i] : ~0ull;
+    const uint64_t key = i == lane && lane < k ? best : ~0ull;
     const bool ok = key != ~0ull;
     if (ids) ids[i] = ok ? (int32_t)(key & 0xffffffffu) : -1;
     if (scores) scores[i] = ok ? unordered(~(uint32_t)(key >> 32)) : -__builtin_huge_valf();
@@ -469,7 +464,7 @@ extern "C" int kessie_index_query(const void* index_embeds, int64_t row_stride, 
   const hipStream_t s = as_stream(stream);
   const int kk = top_k < num_chunks ? top_k : num_chunks;
   if (kk > 0 && kk <= kFusedK) {
-    // The scan keeps each wave's top-k, one workgroup merges them.
+    // The scan keeps each workgroup's top-k, one workgroup merges them.
     const size_t need = kessie_index_query_workspace_bytes(num_chunks, kk);
     KESSIE_REQUIRE(workspace && workspace_bytes >= need, KESSIE_ERR_WORKSPACE,
                    "index query: workspace of %zu bytes needed, got %zu", need, workspace_bytes);
@@ -494,15 +489,8 @@ extern "C" int kessie_index_query(const void* index_embeds, int64_t row_stride, 
                            similarities, norm_mode, kk, keys);
     }
     if (check_launch("index query scan + top-k") != KESSIE_OK) return last_status();
-    if (kk <= 4)
-      hipLaunchKernelGGL(topk_merge_kernel<4>, dim3(1), dim3(kMergeThreads), 0, s, keys, wgs * kk, kk, top_ids,
-                         top_scores, top_k);
-    else if (kk <= 8)
-      hipLaunchKernelGGL(topk_merge_kernel<8>, dim3(1), dim3(kMergeThreads), 0, s, keys, wgs * kk, kk, top_ids,
-                         top_scores, top_k);
-    else
-      hipLaunchKernelGGL(topk_merge_kernel<16>, dim3(1), dim3(kMergeThreads), 0, s, keys, wgs * kk, kk, top_ids,
-                         top_scores, top_k);
+    hipLaunchKernelGGL(topk_merge_kernel, dim3(1), dim3(kMergeThreads), 0, s, keys, wgs * kk, kk, top_ids,
+                       top_scores, top_k);
     return check_launch("index query top-k merge");
   }
   if (num_chunks > 0) {
