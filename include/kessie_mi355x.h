@@ -58,6 +58,13 @@ int kessie_version(void);
 
 /* =========================================================================
  * Legacy entry points -- identical signatures to the reference launchers.
+ *
+ * The two dense launchers take no workspace, so when a key split pays (small
+ * grids with causal imbalance) they keep one partial buffer per (device,
+ * stream), allocated on the first such call on that stream outside graph
+ * capture, grown on a larger request (the old buffer kept), never freed
+ * before process exit.  A call that would need a new buffer while its
+ * stream is capturing, or more than 1 GiB of partials, runs unsplit.
  * ========================================================================= */
 
 /* Dense windowed attention, fp16 [B,H,N,D] Q/K/V/O, D in {64,128}.
@@ -197,10 +204,10 @@ int kessie_fog_decode_combine(const void* workspace, size_t workspace_bytes,
                               int page_size, int dtype, void* stream);
 
 /* Bytes of workspace kessie_fog_prefill_paged may need (host call): room for
- * per-split partials at the larger of the two kernels' split counts.  The
- * MFMA kernel touches it only when a small chunk on a long context splits
- * the key range (S from the CU count, or KESSIE_PREFILL_SPLITS); the generic
- * kernel always uses it. */
+ * per-split partials at the largest of the kernels' split counts.  The MFMA
+ * kernels (bf16/fp16, and fp32 with head_dim 128) touch it only when a small
+ * chunk on a long context splits the key range (S from the CU count, or
+ * KESSIE_PREFILL_SPLITS); the generic kernel always uses it. */
 size_t kessie_fog_prefill_workspace_bytes(int batch, int num_q_tokens,
                                           int num_q_heads, int num_kv_heads,
                                           int head_dim, int max_ctx,
@@ -212,7 +219,9 @@ size_t kessie_fog_prefill_workspace_bytes(int batch, int num_q_tokens,
  * j <= q_pos (causal) with (window == 0 or q_pos - j < window), fog as in
  * decode, fog index = key position.  q/out: [B][C][Hq][D] contiguous.  This
  * equals the last C rows of the reference's dense math over ctx tokens
- * (kessie_hip_kernels.py:577-593). */
+ * (kessie_hip_kernels.py:577-593).  Kernels: bf16/fp16 on MFMA (head_dim 128,
+ * pages of 16 * 2^k tokens, GQA 1/2/4/8/16), fp32 on fp32 MFMA (head_dim 128,
+ * same pages, GQA up to 128), everything else on the generic kernel. */
 int kessie_fog_prefill_paged(
     const void* q, const void* kv_pool, int num_pages, int64_t page_stride,
     int64_t tok_stride,
