@@ -430,6 +430,119 @@ inline int combine_dsplit(int64_t rows, int D) {
   return y;
 }
 
+// combine_kernel with every load issued first (S <= 256 splits, at most
+// kAheadLoads per thread, plain split layout): lane s of wave 0 holds (m, l)
+// of splits s, s + 64, ..., and each thread the float2 column of its split
+// group, all requested before the first use, where combine_kernel waits for
+// the maxima, then for (m, l) again, then for the partials (three round trips
+// instead of one; a 4K-token decode's combine is latency-bound).  The same
+// arithmetic in the same order as combine_kernel's fast path -- max and sum
+// over lanes s, s + 64, ... then the same butterfly, each group's splits
+// summed in increasing order, the groups added in order -- so the two give
+// the same bits.
+constexpr int kAheadLoads = 8;
+
+template <typename T>
+__global__ __launch_bounds__(kCombineThreads) void combine_ahead_kernel(Params p) {
+  __shared__ float e_s[256];
+  __shared__ float2 part[kCombineThreads];
+  __shared__ float inv_l;
+  const int64_t row = blockIdx.x;  // (b*C + i)*Hq + h
+  const int S = p.num_splits;
+  const int D = p.D;
+  const int h = (int)(row % p.Hq);
+  const int64_t bi = row / p.Hq;
+  int i = (int)(bi % p.C);
+  int b = (int)(bi / p.C);
+  if (p.q_start) {  // varlen prefill: rows past the chunk have no partials
+    const int s0 = p.q_start[b] - p.q_start[0];
+    if (i >= p.q_start[b + 1] - p.q_start[b]) return;  // uniform, before any barrier
+    i += s0;
+    b = 0;
+  }
+  i += p.q0_off;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int64_t first = row * S;
+  const int chunk = D / gridDim.y;
+  const int d0 = blockIdx.y * chunk;
+  const int cols = chunk / 2, groups = kCombineThreads / cols;
+  const int col = tid % cols, grp = tid / cols;
+  const float* o = p.ws_o + first * D + d0 + 2 * col;
+  float2 v[kAheadLoads];
+#pragma unroll
+  for (int j = 0; j < kAheadLoads; ++j) {
+    const int sp = grp + j * groups;
+    v[j] = sp < S ? *reinterpret_cast<const float2*>(o + (int64_t)sp * D) : make_float2(0.0f, 0.0f);
+  }
+  float mv[4], lv[4];
+  if (tid < 64) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int sp = lane + 64 * k;
+      mv[k] = sp < S ? p.ws_m[first + sp] : kNegInf;
+      lv[k] = sp < S ? p.ws_l[first + sp] : 0.0f;
+    }
+    float mx = kNegInf;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) mx = fmaxf(mx, mv[k]);
+#pragma unroll
+    for (int w = 32; w >= 1; w >>= 1) mx = fmaxf(mx, __shfl_xor(mx, w, 64));
+    float sum = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int sp = lane + 64 * k;
+      if (sp < S) {
+        const float ms = mv[k];
+        const float e = (ms == kNegInf) ? 0.0f : expf(ms - mx);
+        e_s[sp] = e;
+        sum += e * lv[k];
+      }
+    }
+#pragma unroll
+    for (int w = 32; w >= 1; w >>= 1) sum += __shfl_xor(sum, w, 64);
+    if (lane == 0) inv_l = sum > 0.0f ? 1.0f / sum : 0.0f;
+  }
+  __syncthreads();
+  const float il = inv_l;
+  float ax = 0.0f, ay = 0.0f;
+#pragma unroll
+  for (int j = 0; j < kAheadLoads; ++j) {
+    const int sp = grp + j * groups;
+    if (sp < S) {
+      const float e = e_s[sp];
+      ax += e * v[j].x;
+      ay += e * v[j].y;
+    }
+  }
+  part[tid] = make_float2(ax, ay);
+  __syncthreads();
+  if (tid < cols) {
+    float2 acc = part[tid];
+    for (int g = 1; g < groups; ++g) {
+      acc.x += part[g * cols + tid].x;
+      acc.y += part[g * cols + tid].y;
+    }
+    store_out<T>(p, b, i, h, d0 + 2 * tid, acc.x * il);
+    store_out<T>(p, b, i, h, d0 + 2 * tid + 1, acc.y * il);
+  }
+}
+
+// The per-row merge of split partials: combine_ahead_kernel where its loads
+// fit (plain split layout, S <= 256, an even chunk dividing the workgroup,
+// S <= groups * kAheadLoads), else combine_kernel.  Same bits either way.
+template <typename T>
+void launch_row_combine(const Params& p, int64_t rows, hipStream_t s) {
+  const int y = combine_dsplit(rows, p.D);
+  const int chunk = p.D / y;
+  const int S = p.num_splits;
+  bool ahead = !p.balanced && S <= 256 && (chunk & 1) == 0 && kCombineThreads % (chunk / 2) == 0;
+  if (ahead) ahead = S <= (kCombineThreads / (chunk / 2)) * kAheadLoads;
+  if (ahead)
+    hipLaunchKernelGGL(combine_ahead_kernel<T>, dim3((unsigned)rows, y), dim3(kCombineThreads), 0, s, p);
+  else
+    hipLaunchKernelGGL(combine_kernel<T>, dim3((unsigned)rows, y), dim3(kCombineThreads), 0, s, p);
+}
+
 // Two consecutive outputs of lane-owned columns: one 8-byte store for
 // fp32, one packed 4-byte store for bf16/fp16 (rows start on even columns).
 template <typename T>
@@ -564,8 +677,7 @@ void launch_combine(const Params& p, int64_t rows, hipStream_t s) {
     }
     return;
   }
-  hipLaunchKernelGGL(combine_kernel<T>, dim3((unsigned)rows, combine_dsplit(rows, p.D)), dim3(kCombineThreads), 0,
-                     s, p);
+  launch_row_combine<T>(p, rows, s);
 }
 
 
@@ -1176,8 +1288,7 @@ int launch_decode_mfma(Params& p, hipStream_t stream) {
   if (check_launch("fog decode (mfma)") != KESSIE_OK) return KESSIE_ERR_HIP;
   if (!p.direct_out && p.launch_combine) {
     const int64_t rows = (int64_t)p.B * p.Hq;
-    hipLaunchKernelGGL(combine_kernel<T>, dim3((unsigned)rows, combine_dsplit(rows, p.D)), dim3(kCombineThreads),
-                       0, stream, p);
+    launch_row_combine<T>(p, rows, stream);
     return check_launch("fog decode (combine)");
   }
   return KESSIE_OK;
@@ -1188,23 +1299,40 @@ int launch_decode_mfma_f32(Params& p, hipStream_t stream) {
   dim3 grid(p.num_splits, p.B, div_up(p.Hkv, kDecWaves));
   const int fog = (p.bias ? kFogBias : 0) | (p.vscale ? kFogVs : 0);
   const dim3 block(kDecWaves * 64);
-  switch (fog) {
-    case 0: hipLaunchKernelGGL((decode_mfma_f32_kernel<G, kDecPref, kDecWaves, 0>), grid, block, 0, stream, p); break;
-    case kFogBias:
-      hipLaunchKernelGGL((decode_mfma_f32_kernel<G, kDecPref, kDecWaves, kFogBias>), grid, block, 0, stream, p);
-      break;
-    case kFogVs:
-      hipLaunchKernelGGL((decode_mfma_f32_kernel<G, kDecPref, kDecWaves, kFogVs>), grid, block, 0, stream, p);
-      break;
-    default:
-      hipLaunchKernelGGL((decode_mfma_f32_kernel<G, kDecPref, kDecWaves, kFogBias | kFogVs>), grid, block, 0, stream,
-                         p);
+  // Splits of at most two 16-token blocks (short contexts) take the
+  // one-block-in-flight instance: half the code to fetch, and a 4K-token
+  // step 1 us faster although its two blocks then load one after the other.
+  const int per = div_up(div_up(max(p.max_ctx, 1), 16), max(p.num_splits, 1));
+  if (!p.balanced && per <= 2) {
+    switch (fog) {
+      case 0: hipLaunchKernelGGL((decode_mfma_f32_kernel<G, 1, kDecWaves, 0>), grid, block, 0, stream, p); break;
+      case kFogBias:
+        hipLaunchKernelGGL((decode_mfma_f32_kernel<G, 1, kDecWaves, kFogBias>), grid, block, 0, stream, p);
+        break;
+      case kFogVs:
+        hipLaunchKernelGGL((decode_mfma_f32_kernel<G, 1, kDecWaves, kFogVs>), grid, block, 0, stream, p);
+        break;
+      default:
+        hipLaunchKernelGGL((decode_mfma_f32_kernel<G, 1, kDecWaves, kFogBias | kFogVs>), grid, block, 0, stream, p);
+    }
+  } else {
+    switch (fog) {
+      case 0: hipLaunchKernelGGL((decode_mfma_f32_kernel<G, kDecPref, kDecWaves, 0>), grid, block, 0, stream, p); break;
+      case kFogBias:
+        hipLaunchKernelGGL((decode_mfma_f32_kernel<G, kDecPref, kDecWaves, kFogBias>), grid, block, 0, stream, p);
+        break;
+      case kFogVs:
+        hipLaunchKernelGGL((decode_mfma_f32_kernel<G, kDecPref, kDecWaves, kFogVs>), grid, block, 0, stream, p);
+        break;
+      default:
+        hipLaunchKernelGGL((decode_mfma_f32_kernel<G, kDecPref, kDecWaves, kFogBias | kFogVs>), grid, block, 0, stream,
+                           p);
+    }
   }
   if (check_launch("fog decode (mfma fp32)") != KESSIE_OK) return KESSIE_ERR_HIP;
   if (!p.direct_out && p.launch_combine) {
     const int64_t rows = (int64_t)p.B * p.Hq;
-    hipLaunchKernelGGL(combine_kernel<float>, dim3((unsigned)rows, combine_dsplit(rows, p.D)), dim3(kCombineThreads),
-                       0, stream, p);
+    launch_row_combine<float>(p, rows, stream);
     return check_launch("fog decode (combine)");
   }
   return KESSIE_OK;
@@ -1507,18 +1635,9 @@ extern "C" int kessie_fog_decode_combine(const void* workspace, size_t workspace
   carve_workspace(p, const_cast<void*>(workspace), rows);
   hipStream_t s = as_stream(stream);
   switch (dtype) {
-    case KESSIE_DTYPE_F32:
-      hipLaunchKernelGGL(combine_kernel<float>, dim3((unsigned)rows, combine_dsplit(rows, p.D)),
-                         dim3(kCombineThreads), 0, s, p);
-      break;
-    case KESSIE_DTYPE_BF16:
-      hipLaunchKernelGGL(combine_kernel<bf16_t>, dim3((unsigned)rows, combine_dsplit(rows, p.D)),
-                         dim3(kCombineThreads), 0, s, p);
-      break;
-    default:
-      hipLaunchKernelGGL(combine_kernel<f16_t>, dim3((unsigned)rows, combine_dsplit(rows, p.D)),
-                         dim3(kCombineThreads), 0, s, p);
-      break;
+    case KESSIE_DTYPE_F32: launch_row_combine<float>(p, rows, s); break;
+    case KESSIE_DTYPE_BF16: launch_row_combine<bf16_t>(p, rows, s); break;
+    default: launch_row_combine<f16_t>(p, rows, s); break;
   }
   return check_launch("fog decode combine");
 }
