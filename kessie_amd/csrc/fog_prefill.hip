@@ -356,6 +356,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
     }
     return ids;
   };
+
   auto valid_mask = [&](i32x4 ids) {
     int m = 0;
 #pragma unroll
@@ -364,6 +365,29 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
   };
   auto slot_id = [&](i32x4 ids, int slot) {
     return uniform(slot & 2 ? (slot & 1 ? ids[3] : ids[2]) : (slot & 1 ? ids[1] : ids[0]));
+  };
+  // A tile's page ids and this wave's own (page slot kslot).  Every tile
+  // but the last has its four entries in range: one base, four consecutive
+  // words (one scalar load of 16 bytes) and the wave's own word, instead of
+  // four clamped addresses and a select chain over the slot.
+  struct TileIds {
+    i32x4 ids;
+    int own;
+  };
+  auto fetch_tile = [&](int tile) {
+    TileIds r;
+    if constexpr (!kDense && !kBig) {
+      const int pg0 = (t_begin + tile * kstep) >> 4;
+      if (tile < n_tiles && pg0 + 3 < n_tab) {
+        const int32_t* e = table + pg0;
+        r.ids = i32x4{e[0], e[1], e[2], e[3]};
+        r.own = e[kslot];
+        return r;
+      }
+    }
+    r.ids = fetch_ids(tile);
+    r.own = slot_id(r.ids, kslot);
+    return r;
   };
 
   // Global loads go through buffer resources whose record count covers only
@@ -381,14 +405,25 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
 #pragma unroll
   for (int r = 0; r < kKL; ++r) koff[r] = (uint32_t)((krow(r) & 15) * ts_b + 16 * kc);
   const uint32_t voff0 = (uint32_t)((vkey_off & 15) * ts_b + 16 * kc), voff1 = voff0 + (uint32_t)ts_b;
-  auto page_rsrc = [&](const char* pool, int pid, int first_tok) {
+  // A page's place in its pool (bytes) and the bytes of its rows inside the
+  // key range: 0 and 0 for an invalid page id or no rows in range, so its
+  // loads read zeros.  With head_dim 128 a wave's K and V share the page, and
+  // the span is computed once for both.
+  // (A page's stride in bytes is below 2^32, checked on the host, so its
+  // offset is one 32 x 32 -> 64-bit product.)
+  const uint32_t pstride_b = (uint32_t)(p.page_stride * (int64_t)sizeof(T));
+  auto page_span = [&](int pid, int first_tok, int64_t& off, int& bytes) {
     const int nrows = min(max(hi - first_tok, 0), 16);
     const bool ok = (uint32_t)pid < n_ids && nrows > 0;
-    int64_t at = (int64_t)pid * p.page_stride;
-    if constexpr (kBig) at = (int64_t)(pid >> psh) * p.page_stride + (int64_t)((pid & pmask) << 4) * p.tok_stride;
-    const char* base = ok ? pool + at * (int64_t)sizeof(T) : pool;
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), (short)0, ok ? (nrows - 1) * ts_b + kRowB : 0,
-                                             kRsrcWord3);
+    const uint32_t upid = ok ? (uint32_t)pid : 0u;
+    uint64_t at = (uint64_t)upid * pstride_b;
+    if constexpr (kBig)
+      at = (uint64_t)(upid >> psh) * pstride_b + (uint64_t)(((upid & (uint32_t)pmask) << 4) * (uint32_t)ts_b);
+    off = (int64_t)at;
+    bytes = ok ? (nrows - 1) * ts_b + kRowB : 0;
+  };
+  auto span_rsrc = [&](const char* pool, int64_t off, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(pool + off), (short)0, bytes, kRsrcWord3);
   };
   // Rows of V weights and of the bias: keys past the range read as zero.
   // (The second weight goes through a resource starting one key later, so the
@@ -405,14 +440,20 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
   // iteration before their stage store, and land behind a whole iteration.
   v8 kreg[2][kKL], vreg[2][2];
   float fw0[2] = {1.0f, 1.0f}, fw1[2] = {1.0f, 1.0f}, fb_r[2] = {0.0f, 0.0f};
-  auto issue = [&](int tile, i32x4 ids, int set) {
+  auto issue = [&](int tile, const TileIds& tid_s, int set) {
     const int t0 = t_begin + tile * kstep;
-    const auto krs = page_rsrc(kpool, slot_id(ids, kslot), t0 + 16 * kslot);
+    int64_t k_at;
+    int k_bytes;
+    page_span(tid_s.own, t0 + 16 * kslot, k_at, k_bytes);
+    const auto krs = span_rsrc(kpool, k_at, k_bytes);
 #pragma unroll
     for (int r = 0; r < kKL; ++r)
       kreg[set][r] = __builtin_bit_cast(v8, __builtin_amdgcn_raw_buffer_load_b128(krs, (int)koff[r], 0, 0));
     if (vload) {
-      const auto vrs = page_rsrc(vpool, slot_id(ids, vslot), t0 + 16 * vslot);
+      int64_t v_at = k_at;
+      int v_bytes = k_bytes;
+      if constexpr (kD != 128) page_span(slot_id(tid_s.ids, vslot), t0 + 16 * vslot, v_at, v_bytes);
+      const auto vrs = span_rsrc(vpool, v_at, v_bytes);
       vreg[set][0] = __builtin_bit_cast(v8, __builtin_amdgcn_raw_buffer_load_b128(vrs, (int)voff0, 0, 0));
       vreg[set][1] = __builtin_bit_cast(v8, __builtin_amdgcn_raw_buffer_load_b128(vrs, (int)voff1, 0, 0));
       if (kVs) {
@@ -492,7 +533,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
     ti_hi = dhi < kPfKT ? 0 : (dhi - kPfKT) / kstep + 1;
   }
 
-  i32x4 ids_a, ids_b;            // page ids of tiles t+3 and t+4
+  TileIds ids_a, ids_b;          // page ids of tiles t+3 and t+4
   int pm0 = 0, pm1 = 0, pm2 = 0;  // valid-page masks of tiles t, t+1 and t+2
   // Scores in three 16-register buffers: a tile's two 32-key blocks in two of
   // them, the next tile's second block built in the third while the first
@@ -513,10 +554,10 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
     const int st_nxt = (t + 1) & (kPfStages - 1);
     const int st_new = (t + 2) & (kPfStages - 1);
     // Tile t+3's global loads (none past the last tile: its ids are -1).
-    const int pm3 = valid_mask(ids_a);
+    const int pm3 = valid_mask(ids_a.ids);
     issue(t + 3, ids_a, set);
     ids_a = ids_b;
-    ids_b = fetch_ids(t + 5);
+    ids_b = fetch_tile(t + 5);
 
     const bool interior = pm0 == 0xF && t >= ti_lo && t < ti_hi;
     const float* fbt = fbs + st_cur * kPfKT + 8 * half;
@@ -629,17 +670,17 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
     __syncthreads();
   };
   if (n_tiles > 0) {
-    const i32x4 ids0 = fetch_ids(0), ids1 = fetch_ids(1), ids2 = fetch_ids(2);
-    pm0 = valid_mask(ids0);
-    pm1 = valid_mask(ids1);
-    pm2 = valid_mask(ids2);
+    const TileIds ids0 = fetch_tile(0), ids1 = fetch_tile(1), ids2 = fetch_tile(2);
+    pm0 = valid_mask(ids0.ids);
+    pm1 = valid_mask(ids1.ids);
+    pm2 = valid_mask(ids2.ids);
     issue(0, ids0, 0);
     store(0, 0);
     issue(1, ids1, 1);
     store(1, 1);
     issue(2, ids2, 0);
-    ids_a = fetch_ids(3);
-    ids_b = fetch_ids(4);
+    ids_a = fetch_tile(3);
+    ids_b = fetch_tile(4);
     __syncthreads();
     {
       f32x16 s0[2];
@@ -781,6 +822,8 @@ bool prefill_mfma_ok(const Params& p, int dtype) {
   if (!(p.sm_scale > 0.0f)) return false;
   if (!aligned16(p.q) || !aligned16(p.k) || !aligned16(p.v) || !aligned16(p.out)) return false;
   if (p.page_stride % 8 || p.tok_stride % 8 || p.head_stride % 8) return false;
+  // A page's stride in bytes below 2^32 (the kernel forms page offsets as 32 x 32-bit products).
+  if (p.page_stride < 0 || p.page_stride * 2 >= ((int64_t)1 << 32)) return false;
   if (p.q_bs % 8 || p.q_is % 8 || p.q_hs % 8 || p.o_bs % 4 || p.o_is % 4 || p.o_hs % 4) return false;
   return true;
 }
