@@ -376,8 +376,8 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
   };
   auto fetch_tile = [&](int tile) {
     TileIds r;
+    const int pg0 = (t_begin + tile * kstep) >> 4;
     if constexpr (!kDense && !kBig) {
-      const int pg0 = (t_begin + tile * kstep) >> 4;
       if (tile < n_tiles && pg0 + 3 < n_tab) {
         const int32_t* e = table + pg0;
         r.ids = i32x4{e[0], e[1], e[2], e[3]};
@@ -386,7 +386,15 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
       }
     }
     r.ids = fetch_ids(tile);
-    r.own = slot_id(r.ids, kslot);
+    if constexpr (kDense) {
+      r.own = tile < n_tiles && pg0 + kslot < n_tab ? dense0 + pg0 + kslot : -1;
+    } else if constexpr (kBig) {
+      const int j = pg0 + kslot;
+      const int e = table[min(j, n_tab - 1) >> psh];
+      r.own = tile < n_tiles && j < n_tab && (uint32_t)e < (uint32_t)p.num_pages ? (e << psh) | (j & pmask) : -1;
+    } else {
+      r.own = slot_id(r.ids, kslot);
+    }
     return r;
   };
 
