@@ -51,24 +51,28 @@ def backlog(ms: float = 5.0) -> None:
 
 
 def preheat(fn, ms: float = 150.0) -> int:
-    """Untimed calls of ``fn`` for ~ms of GPU time before a timed loop.  The
-    device raises its clocks over the first tens of milliseconds of load: the
-    first timed pass of the headline decode after 3 warm-up steps ran 1.7 %
-    slower than the passes after it (1,279 against 1,257 us per step), so
-    every timed loop of a heavy kernel starts from steady clocks.  Returns the
-    number of calls made (they are not steps of the measurement)."""
+    """Untimed calls of ``fn`` until ~ms of GPU time has passed, before a
+    timed loop.  The device raises its clocks over the first tens of
+    milliseconds of load: the first timed pass of the headline decode after 3
+    warm-up steps ran 1.7 % slower than the passes after it (1,279 against
+    1,257 us per step), so every timed loop of a heavy kernel starts from
+    steady clocks.  Calls go in doubling batches, each timed with an event
+    pair.  Returns the number of calls made (they are not steps of the
+    measurement)."""
     import torch
 
     e0, e1 = events(2)
-    e0.record()
-    fn()
-    e1.record()
-    torch.cuda.synchronize()
-    n = max(1, int(ms / max(e0.elapsed_time(e1), 1e-3)))
-    for _ in range(n):
-        fn()
-    torch.cuda.synchronize()
-    return n + 1
+    total, n, calls = 0.0, 1, 0
+    while total < ms and calls < 4096:
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        total += e0.elapsed_time(e1)
+        calls += n
+        n = min(2 * n, 256)
+    return calls
 
 
 def time_back_to_back(fn, reps):
