@@ -496,3 +496,20 @@ def test_prefill_fp32_mfma_bad_page(dev):
     ref = paged_prefill_ref(q.cpu(), pool.cpu(), table.cpu()[:, keep].contiguous(), torch.tensor([400 - 16]),
                             causal=False)
     _check(out, ref, torch.float32)
+
+
+@pytest.mark.parametrize("splits,window", [(300, 0), (7, 100)])
+def test_prefill_fp32_mfma_many_splits(dev, monkeypatch, splits, window):
+    """fp32 MFMA prefill with more key splits than the load-ahead combine
+    takes (300: the per-row combine merges them) and a windowed split: both
+    at 1e-5 of the oracle; most of the 300 splits hold no key block and store
+    empty partials."""
+    from kessie_amd import ops
+
+    monkeypatch.setenv("KESSIE_PREFILL_SPLITS", str(splits))
+    q, pool, table, lens = _case(dev, 2, 24, [3000, 1200], 32, 8, torch.float32, seed=77)
+    vs = torch.rand(2, 3000, generator=gen(dev, 78), device=dev)
+    out = ops.fog_prefill(q, pool, table, lens, 3000, fog_vscale=vs, window=window)
+    torch.cuda.synchronize()
+    ref = paged_prefill_ref(q.cpu(), pool.cpu(), table.cpu(), lens.cpu(), vs.cpu(), None, window)
+    _check(out, ref, torch.float32)
