@@ -50,23 +50,27 @@ def backlog(ms: float = 5.0) -> None:
     torch.cuda._sleep(int(ms * 1e-3 * 2.4e9))
 
 
-def preheat(fn, ms: float = 150.0) -> int:
+def preheat(fn, ms: float = 150.0, cycle: int = 0) -> int:
     """Untimed calls of ``fn`` until ~ms of GPU time has passed, before a
     timed loop.  The device raises its clocks over the first tens of
     milliseconds of load: the first timed pass of the headline decode after 3
     warm-up steps ran 1.7 % slower than the passes after it (1,279 against
-    1,257 us per step), so every timed loop of a heavy kernel starts from
-    steady clocks.  Calls go in doubling batches, each timed with an event
-    pair.  Returns the number of calls made (they are not steps of the
-    measurement)."""
+    1,257 us per step), so every timed loop starts from steady clocks.  Calls
+    go in doubling batches, each timed with an event pair.  With cycle > 0,
+    ``fn(j)`` is called with j = 0, 1, ... modulo cycle (the input sets the
+    timed loop rotates through), else ``fn()``.  Returns the number of calls
+    made (they are not steps of the measurement)."""
     import torch
 
     e0, e1 = events(2)
     total, n, calls = 0.0, 1, 0
     while total < ms and calls < 4096:
         e0.record()
-        for _ in range(n):
-            fn()
+        for j in range(calls, calls + n):
+            if cycle > 0:
+                fn(j % cycle)
+            else:
+                fn()
         e1.record()
         torch.cuda.synchronize()
         total += e0.elapsed_time(e1)
@@ -80,7 +84,9 @@ def time_back_to_back(fn, reps):
     (behind a backlog, so the queue never drains).  For kernels of tens of
     microseconds an event pair around every launch adds the dispatch and
     completion of that launch (~2-3 us on MI355X); back to back, the time per
-    call matches rocprofv3's kernel duration to ~1 %.  ``fn(i)`` makes call i."""
+    call matches rocprofv3's kernel duration to ~1 %.  ``fn(i)`` makes call i.
+    A pre-heat of the same calls (rotating i) brings the clocks up first."""
+    preheat(fn, 100.0, cycle=reps)
     start, end = events(2)
     backlog()
     start.record()
@@ -404,6 +410,12 @@ def bench_gather_evict(dev, reps=5, cpu=False):
         valid.fill_(1)
         pipeline()
     torch.cuda.synchronize()
+
+    def heat():
+        valid.fill_(1)
+        pipeline()
+
+    preheat(heat)
     e0, e1, e2 = events(reps), events(reps), events(reps)
     backlog()
     for i in range(reps):
@@ -543,6 +555,7 @@ def bench_dense(dev, reps=3, b=1, h=32, n=8192, d=128, cpu=False, cpu_heads=4):
     s = torch.cuda.current_stream()
     kk.fused_fog_attention(q, k, v, w, stream=s)
     torch.cuda.synchronize()
+    preheat(lambda: kk.fused_fog_attention(q, k, v, w, stream=s))
     e0, e1 = events(reps), events(reps)
     backlog()
     for i in range(reps):
