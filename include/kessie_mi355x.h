@@ -243,8 +243,9 @@ int kessie_fog_prefill_paged(
  * query_start_loc[b] <= max_query_len, query i of it at ctx_lens[b] - C_b + i
  * (a longer chunk is read as its first max_query_len queries at positions
  * ctx_lens[b] - max_query_len + i; its other rows are not written).
- * MFMA shapes only (bf16/fp16, head_dim 128, pages of 16 * 2^k tokens, GQA 1/2/4/8/16,
- * 16-byte aligned rows); other shapes return KESSIE_ERR_UNSUPPORTED without
+ * MFMA shapes only (head_dim 128, pages of 16 * 2^k tokens, 16-byte aligned
+ * rows; bf16/fp16 with GQA 1/2/4/8/16, or fp32 on the fp32 MFMA kernel with
+ * any GQA ratio up to 128); other shapes return KESSIE_ERR_UNSUPPORTED without
  * launching (call kessie_fog_prefill_paged per sequence instead).  The
  * workspace is sized by kessie_fog_prefill_workspace_bytes(batch,
  * max_query_len, ...) and used only when the chunks are too few to fill the

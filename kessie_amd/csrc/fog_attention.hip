@@ -1657,6 +1657,29 @@ extern "C" size_t kessie_fog_prefill_workspace_bytes(int batch, int num_q_tokens
 // split-K (partials + combine) when the chunks alone would leave CUs idle.
 // Partial rows are (b*C + i)*Hq + h; with q_start the combine skips rows past a
 // sequence's chunk and writes the rest at its packed offset.
+// fp32 chunked prefill on the fp32 MFMA kernel (per-sequence or varlen
+// batches alike): key splits when the chunks alone leave CUs idle, their
+// partials merged by the combine.
+static int run_prefill_f32(kessie::attn::Params& p, void* workspace, size_t workspace_bytes, void* stream) {
+  using namespace kessie;
+  using namespace kessie::attn;
+  p.num_splits = prefill_f32_splits(p.B, p.C, p.Hkv, p.G, p.max_ctx);
+  p.direct_out = p.num_splits == 1 ? 1 : 0;
+  const int64_t rows = (int64_t)p.B * p.C * p.Hq;
+  if (!p.direct_out) {
+    const size_t need = partial_bytes(rows, p.num_splits, p.D);
+    KESSIE_REQUIRE(workspace != nullptr && workspace_bytes >= need, KESSIE_ERR_WORKSPACE,
+                   "fog prefill: workspace of %zu bytes needed, got %zu", need, workspace_bytes);
+    KESSIE_REQUIRE(aligned16(workspace), KESSIE_ERR_INVALID, "fog prefill: workspace not 16-byte aligned");
+    carve_workspace(p, workspace, rows);
+  }
+  const hipStream_t s = as_stream(stream);
+  const int st = prefill_f32(p, s);
+  if (st != KESSIE_OK || p.direct_out) return st;
+  launch_combine<float>(p, rows, s);
+  return check_launch("fog prefill (combine)");
+}
+
 static int run_prefill_mfma(kessie::attn::Params& p, int dtype, void* workspace, size_t workspace_bytes,
                             void* stream) {
   using namespace kessie;
@@ -1741,23 +1764,7 @@ extern "C" int kessie_fog_prefill_paged(const void* q, const void* kv_pool, int 
   KESSIE_REQUIRE(kv_stride >= 0, KESSIE_ERR_INVALID, "fog prefill: kv_stride %lld", (long long)kv_stride);
   if (batch == 0) return KESSIE_OK;
   if (prefill_mfma_ok(p, dtype)) return run_prefill_mfma(p, dtype, workspace, workspace_bytes, stream);
-  if (prefill_f32_ok(p, dtype)) {
-    p.num_splits = prefill_f32_splits(batch, num_q_tokens, num_kv_heads, p.G, max_ctx);
-    p.direct_out = p.num_splits == 1 ? 1 : 0;
-    const int64_t rows = (int64_t)batch * num_q_tokens * num_q_heads;
-    if (!p.direct_out) {
-      const size_t need = partial_bytes(rows, p.num_splits, head_dim);
-      KESSIE_REQUIRE(workspace != nullptr && workspace_bytes >= need, KESSIE_ERR_WORKSPACE,
-                     "fog prefill: workspace of %zu bytes needed, got %zu", need, workspace_bytes);
-      KESSIE_REQUIRE(aligned16(workspace), KESSIE_ERR_INVALID, "fog prefill: workspace not 16-byte aligned");
-      carve_workspace(p, workspace, rows);
-    }
-    const hipStream_t s = as_stream(stream);
-    const int st = prefill_f32(p, s);
-    if (st != KESSIE_OK || p.direct_out) return st;
-    launch_combine<float>(p, rows, s);
-    return check_launch("fog prefill (combine)");
-  }
+  if (prefill_f32_ok(p, dtype)) return run_prefill_f32(p, workspace, workspace_bytes, stream);
   p.num_splits = prefill_splits(batch, num_q_tokens, num_kv_heads, p.G, max_ctx, page_size);
   p.direct_out = p.num_splits == 1 ? 1 : 0;
   p.launch_combine = 1;
@@ -1824,9 +1831,11 @@ extern "C" int kessie_fog_prefill_varlen(const void* q, const int32_t* query_sta
                  "fog prefill varlen: page_table, ctx_lens and query_start_loc are required");
   KESSIE_REQUIRE(kv_stride >= 0, KESSIE_ERR_INVALID, "fog prefill varlen: kv_stride %lld", (long long)kv_stride);
   if (batch == 0 || max_query_len == 0) return KESSIE_OK;
+  if (prefill_f32_ok(p, dtype)) return run_prefill_f32(p, workspace, workspace_bytes, stream);
   KESSIE_REQUIRE(prefill_mfma_ok(p, dtype), KESSIE_ERR_UNSUPPORTED,
-                 "fog prefill varlen: shape not taken by the MFMA kernel (bf16/fp16, head_dim 128, 16-token pages, "
-                 "GQA 1/2/4/8/16, 16-byte aligned rows)");
+                 "fog prefill varlen: shape not taken by the MFMA kernels (bf16/fp16: head_dim 128, pages of 16*2^k "
+                 "tokens, GQA 1/2/4/8/16; fp32: head_dim 128, pages of 16*2^k tokens, GQA up to 128; 16-byte aligned "
+                 "rows)");
   return run_prefill_mfma(p, dtype, workspace, workspace_bytes, stream);
 }
 

@@ -9,7 +9,8 @@
 // or a logit bias), fp32 throughout, online softmax in natural units.
 //
 // Work decomposition: one workgroup = 128 query rows (128/G positions x the
-// G heads of one kv head) of one sequence; 8 waves x 16 rows.  The workgroup
+// G heads of one kv head) of one sequence; 8 waves x 16 rows.  Varlen batches
+// (query_start_loc) number the live (sequence, query tile) pairs along x.  The workgroup
 // streams its kv head's 16-token blocks through a two-stage LDS ring (K and V
 // rows, and the block's fog values): every thread loads 16 bytes of K and of
 // V of the next block while the waves compute the current one, then stores
@@ -49,13 +50,46 @@ __global__ __launch_bounds__(kF32Threads) void prefill_f32_kernel(Params p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, grp = lane >> 4;
   const int g = blockIdx.x % p.Hkv;
-  const int qtile = blockIdx.x / p.Hkv;
-  const int b = blockIdx.y;
+  int qtile = blockIdx.x / p.Hkv;
+  int b = blockIdx.y;
   const int S = kSplit ? (int)gridDim.z : 1, split = kSplit ? (int)blockIdx.z : 0;
   const int G = p.G;
   const int kpos = kF32Rows / G;  // query positions per workgroup
+  if (p.q_start) {
+    // Varlen: x / Hkv numbers the live (sequence, query tile) pairs in order
+    // (the grid's surplus workgroups at its end exit at once); each wave
+    // scans query_start_loc 64 sequences at a time (prefix sum by shuffles).
+    int found = -1, before = 0;
+    for (int b0 = 0; b0 < p.B; b0 += 64) {
+      const int bb = b0 + lane;
+      const int nt = bb < p.B ? div_up(min(max(p.q_start[bb + 1] - p.q_start[bb], 0), p.C), kpos) : 0;
+      int inc = nt;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(inc, o, 64);
+        if (lane >= o) inc += y;
+      }
+      const int total = __builtin_amdgcn_readlane(inc, 63);
+      if (qtile < before + total) {
+        const int l = __ffsll((unsigned long long)__ballot(before + inc > qtile)) - 1;
+        found = b0 + l;
+        qtile -= before + __builtin_amdgcn_readlane(inc - nt, l);
+        break;
+      }
+      before += total;
+    }
+    if (found < 0) return;  // uniform, before any barrier
+    b = found;
+  }
   const int ctx = seq_ctx(p, b);
-  const int C = p.C;
+  int C = p.C;  // this sequence's queries, and where its rows start
+  int64_t q_off = (int64_t)b * p.q_bs, o_off = (int64_t)b * p.o_bs;
+  if (p.q_start) {
+    const int s0 = p.q_start[b] - p.q_start[0];
+    C = min(max(p.q_start[b + 1] - p.q_start[b], 0), p.C);  // partial rows are indexed by max_query_len
+    q_off = (int64_t)s0 * p.q_is;
+    o_off = (int64_t)s0 * p.o_is;
+  }
 
   const int qi_first = qtile * kpos;
   const int qi_last = min(C, qi_first + kpos) - 1;
@@ -84,8 +118,8 @@ __global__ __launch_bounds__(kF32Threads) void prefill_f32_kernel(Params p) {
   // B operand of S^T: query row d = 32 grp + 4 j + e (zero for an invalid row).
   f32x4v qreg[8];
   {
-    const float* qr = static_cast<const float*>(p.q) + (int64_t)b * p.q_bs +
-                      (int64_t)min(max(qi, 0), qi_last) * p.q_is + (int64_t)head * p.q_hs;
+    const float* qr = static_cast<const float*>(p.q) + q_off + (int64_t)min(max(qi, 0), qi_last) * p.q_is +
+                      (int64_t)head * p.q_hs;
 #pragma unroll
     for (int j = 0; j < 8; ++j)
       qreg[j] = row_ok ? *reinterpret_cast<const f32x4v*>(qr + 32 * grp + 4 * j) : f32x4v{0.0f, 0.0f, 0.0f, 0.0f};
@@ -219,7 +253,7 @@ __global__ __launch_bounds__(kF32Threads) void prefill_f32_kernel(Params p) {
     return;
   }
   const float il = l_run > 0.0f ? 1.0f / l_run : 0.0f;
-  float* dst = static_cast<float*>(p.out) + (int64_t)b * p.o_bs + (int64_t)qi * p.o_is + (int64_t)head * p.o_hs + 4 * grp;
+  float* dst = static_cast<float*>(p.out) + o_off + (int64_t)qi * p.o_is + (int64_t)head * p.o_hs + 4 * grp;
 #pragma unroll
   for (int blk = 0; blk < 8; ++blk) *reinterpret_cast<f32x4v*>(dst + 16 * blk) = oacc[blk] * il;
 }
@@ -253,7 +287,7 @@ int prefill_f32_splits(int B, int C, int Hkv, int G, int max_ctx) {
 
 bool prefill_f32_ok(const Params& p, int dtype) {
   if (env_int("KESSIE_FORCE_GENERIC", 0)) return false;
-  if (dtype != KESSIE_DTYPE_F32 || p.D != 128 || p.page_table == nullptr || p.q_start != nullptr) return false;
+  if (dtype != KESSIE_DTYPE_F32 || p.D != 128 || p.page_table == nullptr) return false;
   if (p.page_size < 16 || (p.page_size & (p.page_size - 1)) != 0) return false;
   if (p.G < 1 || p.G > kF32Rows) return false;
   if (!aligned16(p.q) || !aligned16(p.k) || !aligned16(p.v) || !aligned16(p.out)) return false;
@@ -266,7 +300,7 @@ bool prefill_f32_ok(const Params& p, int dtype) {
 // p.num_splits (> 1: partials in p.ws_*, merged by the caller) set by the caller.
 int prefill_f32(const Params& p, hipStream_t s) {
   const int kpos = max(1, kF32Rows / p.G);
-  const dim3 grid(div_up(p.C, kpos) * p.Hkv, p.B, max(p.num_splits, 1));
+  const dim3 grid(div_up(p.C, kpos) * p.Hkv * (p.q_start ? p.B : 1), p.q_start ? 1 : p.B, max(p.num_splits, 1));
   if (p.num_splits > 1)
     launch_f32<true>(p, grid, s);
   else

@@ -306,7 +306,7 @@ def fog_prefill_varlen(q: torch.Tensor, query_start_loc: torch.Tensor, max_query
     launch: q/out [T, Hq, D] packed, sequence b's queries at rows
     query_start_loc[b] - query_start_loc[0] .. (int32 [B+1] on the device, e.g.
     a slice of vLLM's query_start_loc), query i of it at ctx_lens[b] - C_b + i.
-    Returns False, having launched nothing, for shapes the MFMA kernel does not
+    Returns False, having launched nothing, for shapes the MFMA kernels do not
     take (the caller then runs fog_prefill per sequence).  ws: split-K
     workspace (a cached one when None), used when the chunks are too few to
     fill the device."""

@@ -265,9 +265,11 @@ def test_prefill_varlen_matches_per_sequence(dev, fog, window, monkeypatch):
 
 
 def test_prefill_varlen_unsupported_shape_launches_nothing(dev):
+    """8-token pages: neither MFMA kernel takes them, so the varlen entry
+    returns False and leaves the output as it was."""
     from kessie_amd import ops
 
-    _, pool, table, lens = _case(dev, 2, 1, [40, 40], 32, 8, torch.float32, seed=14)
+    _, pool, table, lens = _case(dev, 2, 1, [40, 40], 32, 8, torch.float32, seed=14, page_size=8)
     qsl = torch.tensor([0, 3, 8], dtype=torch.int32, device=dev)
     q = torch.randn(8, 32, 128, device=dev)
     out = torch.full_like(q, 7.0)
@@ -513,3 +515,99 @@ def test_prefill_fp32_mfma_many_splits(dev, monkeypatch, splits, window):
     torch.cuda.synchronize()
     ref = paged_prefill_ref(q.cpu(), pool.cpu(), table.cpu(), lens.cpu(), vs.cpu(), None, window)
     _check(out, ref, torch.float32)
+
+
+def _varlen_q(dev, chunks, hq, dtype, seed, lead=0):
+    starts = [lead]
+    for c in chunks:
+        starts.append(starts[-1] + c)
+    qsl = torch.tensor(starts, dtype=torch.int32, device=dev)
+    q_all = torch.randn(starts[-1], hq, 128, generator=gen(dev, seed), device=dev).to(dtype)
+    return qsl, q_all[lead:], [x - lead for x in starts]
+
+
+@pytest.mark.parametrize("hq,hkv,page_size,fog,window,splits", [
+    (32, 8, 16, "vscale", 0, 1),     # one key split: every row written by the attention kernel
+    (32, 8, 16, "bias", 50, 5),      # five forced splits (partials + combine), window
+    (24, 8, 32, "none", 0, 3),       # GQA 3, 32-token pages
+    (128, 8, 16, "both", 300, 2),    # GQA 16
+])
+def test_prefill_fp32_varlen_matches_per_sequence(dev, monkeypatch, hq, hkv, page_size, fog, window, splits):
+    """fp32 varlen prefill (one launch of the fp32 MFMA kernel over ragged
+    chunks incl. a one-token chunk and an empty one, query_start_loc starting
+    at 5) equals the per-sequence fp32 launches bit for bit at an equal key
+    split count, and the oracle within 1e-5."""
+    from kessie_amd import ops
+
+    monkeypatch.setenv("KESSIE_PREFILL_SPLITS", str(splits))
+    chunks, ctxs = [37, 1, 300, 0, 129], [900, 64, 300, 50, 4000]
+    b, mx = len(chunks), max(ctxs)
+    _, pool, table, lens = _case(dev, b, 1, ctxs, hq, hkv, torch.float32, seed=61, page_size=page_size)
+    qsl, q, starts = _varlen_q(dev, chunks, hq, torch.float32, 62, lead=5)
+    vs = torch.rand(b, mx, generator=gen(dev, 63), device=dev) if fog in ("vscale", "both") else None
+    bias = fog_bias(mx, 0.5, 0.5, {3, 17, 200}, 0.1).to(dev) if fog in ("bias", "both") else None
+    out = torch.full_like(q, float("nan"))
+    assert ops.fog_prefill_varlen(q, qsl, max(chunks), pool, table, lens, mx, fog_vscale=vs, fog_bias=bias,
+                                  window=window, out=out)
+    torch.cuda.synchronize()
+    assert not torch.isnan(out).any()
+    for i, c in enumerate(chunks):
+        if c == 0:
+            continue
+        s = starts[i]
+        one = ops.fog_prefill(q[s:s + c].unsqueeze(0).contiguous(), pool, table[i:i + 1], lens[i:i + 1], mx,
+                              fog_vscale=None if vs is None else vs[i:i + 1], fog_bias=bias, window=window)
+        torch.cuda.synchronize()
+        assert torch.equal(out[s:s + c], one[0]), f"sequence {i}"
+        ref = paged_prefill_ref(q[s:s + c].unsqueeze(0).cpu(), pool.cpu(), table[i:i + 1].cpu(),
+                                lens[i:i + 1].cpu(), None if vs is None else vs[i].cpu(),
+                                None if bias is None else bias.cpu(), window)
+        _check(out[s:s + c].unsqueeze(0), ref, torch.float32)
+
+
+def test_prefill_fp32_varlen_many_sequences_sized_splits(dev):
+    """70 ragged fp32 sequences (the tile numbering scans query_start_loc 64
+    at a time; empty chunks at 3 and 64) at the sized split count, every row
+    against the oracle within 1e-5."""
+    from kessie_amd import ops
+
+    g = torch.Generator().manual_seed(71)
+    b, hq, hkv = 70, 16, 8
+    chunks = torch.randint(0, 81, (b,), generator=g).tolist()
+    chunks[3] = chunks[64] = 0
+    ctxs = [c + int(x) for c, x in zip(chunks, torch.randint(1, 400, (b,), generator=g))]
+    _, pool, table, lens = _case(dev, b, 1, ctxs, hq, hkv, torch.float32, seed=72)
+    qsl, q, starts = _varlen_q(dev, chunks, hq, torch.float32, 73)
+    out = torch.full_like(q, float("nan"))
+    assert ops.fog_prefill_varlen(q, qsl, max(chunks), pool, table, lens, max(ctxs), out=out)
+    torch.cuda.synchronize()
+    assert not torch.isnan(out).any()
+    pool_c, table_c, lens_c, out_c, q_c = pool.cpu(), table.cpu(), lens.cpu(), out.cpu(), q.cpu()
+    for i, c in enumerate(chunks):
+        if c == 0:
+            continue
+        s = starts[i]
+        ref = paged_prefill_ref(q_c[s:s + c].unsqueeze(0), pool_c, table_c[i:i + 1], lens_c[i:i + 1])
+        _check(out_c[s:s + c].unsqueeze(0), ref, torch.float32)
+
+
+@pytest.mark.parametrize("splits", [1, 4])
+def test_prefill_fp32_varlen_chunk_longer_than_max_query_len(dev, monkeypatch, splits):
+    """fp32 varlen: a chunk longer than max_query_len is read as its first
+    max_query_len queries at the last max_query_len positions of its context,
+    its other rows untouched, the next sequence unaffected, with and without
+    key splits (partial rows indexed by max_query_len)."""
+    from kessie_amd import ops
+
+    monkeypatch.setenv("KESSIE_PREFILL_SPLITS", str(splits))
+    mq = 200
+    _, pool, table, lens = _case(dev, 2, 1, [3000, 2000], 32, 8, torch.float32, seed=81)
+    qsl, q, _ = _varlen_q(dev, [300, 50], 32, torch.float32, 82)
+    out = torch.full_like(q, float("nan"))
+    assert ops.fog_prefill_varlen(q, qsl, mq, pool, table, lens, 3000, out=out)
+    torch.cuda.synchronize()
+    assert torch.isnan(out[mq:300]).all()
+    ref0 = paged_prefill_ref(q[:mq].unsqueeze(0).cpu(), pool.cpu(), table[:1].cpu(), lens[:1].cpu())
+    _check(out[:mq].unsqueeze(0), ref0, torch.float32)
+    ref1 = paged_prefill_ref(q[300:].unsqueeze(0).cpu(), pool.cpu(), table[1:].cpu(), lens[1:].cpu())
+    _check(out[300:].unsqueeze(0), ref1, torch.float32)
