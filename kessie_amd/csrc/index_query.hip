@@ -22,6 +22,12 @@
 #include "common.h"
 
 namespace kessie {
+namespace attn {
+int device_cus();  // compute units of the current device (fog_attention.hip)
+}  // namespace attn
+}  // namespace kessie
+
+namespace kessie {
 namespace index {
 namespace {
 
@@ -239,59 +245,106 @@ __global__ void topk_unpack_kernel(const uint64_t* __restrict__ keys, int k, int
 
 // Fused path (k <= kFusedK): the scan keeps each workgroup's top-k.  A wave
 // scans 16 rows, four per 16-lane group with their loads issued together;
-// the workgroup's 128 keys go to LDS, one per row, and its first wave selects
-// the k smallest.  One workgroup then selects the first k of all workgroups'
-// lists.  Selection is k rounds of: each lane's smallest key, the wave's
-// smallest of those (the device library's DPP reduction), taken out of its
-// lane and kept by lane r of round r -- no sorted lists (inserting each key
-// into a lane's sorted list of 8 took ~600 VALU instructions per wave and left
-// the merge at 7.9 us; now 5.6 us with 16 merge waves, and 8 waves of 6 keys
-// each save another 0.9 us, the per-wave reduction being the fixed cost).
-// 128 rows per workgroup: 611 workgroups for 78,125 rows, one round on the
-// chip, half the keys of 64-row workgroups to merge (64, 256 rows, or 2 or 8
-// rows per 16-lane group: 24.1-26.7 us against 22.5).  The selection at the
-// end of each scan workgroup costs ~1 us of the scan's 17 us.
+// the workgroup's keys go to LDS, one per row, and every thread counts the
+// keys below one of them over a segment of the others (LDS adds sum the
+// counts), so each key's rank comes out with no selection rounds; the first
+// k are written in order.  One workgroup then takes the first k of all
+// workgroups' lists (the threshold pass of topk_merge_kernel, or selection
+// rounds).  Per query at 78,125 x 256 fp32, back to back: 21.9 us with
+// 64-bit selection rounds in both kernels, 21.2 with 32-bit rounds, 20.4 with
+// the threshold merge, 20.2 with the scan's rank count, 19.9 with 10-wave
+// workgroups (the scan alone, a plain grid-stride kernel: 14.9).  More rows
+// per 16-lane group (8) or 64- and 256-row workgroups measured slower.
 constexpr int kFusedK = 16;
-constexpr int kFusedThreads = 512;                                      // scan workgroup: 8 waves
 constexpr int kFusedRowsGroup = 4;                                      // rows per 16-lane group
 constexpr int kFusedRowsWave = 4 * kFusedRowsGroup;                     // 16 rows per wave
-constexpr int kFusedRowsWg = kFusedRowsWave * kFusedThreads / 64;       // 128 rows per workgroup
+constexpr int kFusedWavesMin = 8;                                       // scan workgroups: 8 or 10 waves
+constexpr int kFusedWavesMax = 10;
 constexpr int kMergeThreads = 512;                                      // merge workgroup: 8 waves
 constexpr int kMergeLoads = 6;                                          // keys a merge lane takes per pass
 
-extern "C" __device__ unsigned long long __ockl_wfred_min_u64(unsigned long long);
+extern "C" __device__ unsigned int __ockl_wfred_min_u32(unsigned int);
 
 // k rounds of selection over the keys the wave's lanes hold (x[0..M) each,
 // unique but for the ~0 padding): round r takes the wave's smallest key out
 // of its lane, and lane r keeps it.  Returns the lane's kept key (~0 for
-// lanes >= k).  Every lane of the wave must take part.
+// lanes >= k).  Every lane of the wave must take part.  A round reduces the
+// keys' high words (the score) over the wave; when one slot of one lane holds
+// that word, its low word (the chunk index) is read from there, and only on a
+// tie (or when nothing but padding is left) do the low words of the tied
+// slots take a second reduction -- two 32-bit reductions at most, against a
+// 64-bit one whose compares and selects each take two instructions.
 template <int M>
-__device__ __forceinline__ uint64_t wave_select(uint64_t (&x)[M], int k) {
+__device__ __forceinline__ uint64_t wave_select(const uint64_t (&x)[M], int k) {
   const int lane = threadIdx.x & 63;
+  uint32_t hi[M], lo[M];
+#pragma unroll
+  for (int j = 0; j < M; ++j) {
+    hi[j] = (uint32_t)(x[j] >> 32);
+    lo[j] = (uint32_t)x[j];
+  }
   uint64_t kept = ~0ull;
   for (int r = 0; r < k; ++r) {
-    uint64_t lm = x[0];
+    uint32_t lm = hi[0];
 #pragma unroll
-    for (int j = 1; j < M; ++j) lm = x[j] < lm ? x[j] : lm;
-    const uint64_t m = __ockl_wfred_min_u64(lm);
-    if (lane == r) kept = m;
+    for (int j = 1; j < M; ++j) lm = hi[j] < lm ? hi[j] : lm;
+    const uint32_t mh = __ockl_wfred_min_u32(lm);
+    uint64_t bal[M];
+    int count = 0;
 #pragma unroll
-    for (int j = 0; j < M; ++j) x[j] = x[j] == m ? ~0ull : x[j];
+    for (int j = 0; j < M; ++j) {
+      bal[j] = __builtin_amdgcn_ballot_w64(hi[j] == mh);
+      count += __builtin_popcountll(bal[j]);
+    }
+    uint32_t ml;
+    if (count == 1) {  // the one slot whose high word is mh: read its low word, take it out
+      uint32_t t = 0;
+      uint64_t any = 0;
+#pragma unroll
+      for (int j = 0; j < M; ++j) {
+        t = hi[j] == mh ? lo[j] : t;
+        any |= bal[j];
+      }
+      ml = (uint32_t)__builtin_amdgcn_readlane((int)t, __builtin_ctzll(any));
+#pragma unroll
+      for (int j = 0; j < M; ++j)
+        if (hi[j] == mh) {
+          hi[j] = ~0u;
+          lo[j] = ~0u;
+        }
+    } else {
+      uint32_t c = ~0u;
+#pragma unroll
+      for (int j = 0; j < M; ++j) c = hi[j] == mh && lo[j] < c ? lo[j] : c;
+      ml = __ockl_wfred_min_u32(c);
+#pragma unroll
+      for (int j = 0; j < M; ++j)
+        if (hi[j] == mh && lo[j] == ml) {
+          hi[j] = ~0u;
+          lo[j] = ~0u;
+        }
+    }
+    if (lane == r) kept = ((uint64_t)mh << 32) | ml;
   }
   return kept;
 }
 
-template <typename T>
-__global__ __launch_bounds__(kFusedThreads) void scan_topk_kernel(const T* __restrict__ rows, int64_t row_stride,
+template <typename T, int W>
+__global__ __launch_bounds__(64 * W) void scan_topk_kernel(const T* __restrict__ rows, int64_t row_stride,
                                                                   int n, int d, const float* __restrict__ q,
                                                                   float* __restrict__ sims, int mode, int k,
                                                                   uint64_t* __restrict__ keys_out) {
   typedef typename Row16<T>::type V;
   constexpr int N = Row16<T>::N;
   constexpr int R = kFusedRowsGroup;
+  constexpr int kFusedThreads = 64 * W, kFusedRowsWg = kFusedRowsWave * W;
   __shared__ float qs[1024];
   __shared__ float red[kFusedThreads / 64];
   __shared__ uint64_t wg_keys[kFusedRowsWg];
+  __shared__ int wg_rank[kFusedRowsWg];
+  static_assert(kFusedThreads % kFusedRowsWg == 0 && kFusedRowsWg % (kFusedThreads / kFusedRowsWg) == 0,
+                "scan_topk_kernel: rank segments");
+  if (threadIdx.x < kFusedRowsWg) wg_rank[threadIdx.x] = 0;
   float part = 0.0f;
   for (int i = threadIdx.x; i < d; i += kFusedThreads) {
     const float x = q[i];
@@ -342,17 +395,52 @@ __global__ __launch_bounds__(kFusedThreads) void scan_topk_kernel(const T* __res
     const bool in = r[u] < n;
     if (sub == 0) {
       if (in) sims[r[u]] = sim;
-      wg_keys[kFusedRowsWave * wave + R * grp + u] = in ? make_key(sim, (uint32_t)r[u]) : ~0ull;
+      // Rows past n: distinct keys above every row's (row indices stay below 2^31).
+      const int at = kFusedRowsWave * wave + R * grp + u;
+      wg_keys[at] = in ? make_key(sim, (uint32_t)r[u]) : ~0ull - (uint64_t)(kFusedRowsWg - 1 - at);
     }
   }
   __syncthreads();
-  if (wave != 0) return;
-  uint64_t x[(kFusedRowsWg + 63) / 64];
+  // Rank of each of the workgroup's (distinct) keys: thread t counts the keys
+  // below key t % kFusedRowsWg in segment t / kFusedRowsWg (broadcast LDS reads).
+  constexpr int kSeg = kFusedRowsWg * kFusedRowsWg / kFusedThreads;
+  const int mine_at = threadIdx.x % kFusedRowsWg, seg = threadIdx.x / kFusedRowsWg;
+  const uint64_t mine = wg_keys[mine_at];
+  int below = 0;
 #pragma unroll
-  for (int j = 0; j < (kFusedRowsWg + 63) / 64; ++j) x[j] = 64 * j + lane < kFusedRowsWg ? wg_keys[64 * j + lane] : ~0ull;
-  const uint64_t kept = wave_select(x, k);
-  if (lane < k) keys_out[(int64_t)blockIdx.x * k + lane] = kept;
+  for (int j = 0; j < kSeg; ++j) below += wg_keys[seg * kSeg + j] < mine ? 1 : 0;
+  atomicAdd(&wg_rank[mine_at], below);
+  __syncthreads();
+  if (threadIdx.x < kFusedRowsWg) {
+    const int rank = wg_rank[threadIdx.x];
+    if (rank < k) keys_out[(int64_t)blockIdx.x * k + rank] = mine;
+  }
 }
+
+// The wave's smallest key (every lane takes part): the smallest high word,
+// then the smallest low word among the lanes holding it.
+__device__ __forceinline__ uint64_t wave_min_key(uint64_t x) {
+  const uint32_t hi = (uint32_t)(x >> 32);
+  const uint32_t mh = __ockl_wfred_min_u32(hi);
+  const uint32_t ml = __ockl_wfred_min_u32(hi == mh ? (uint32_t)x : ~0u);
+  return ((uint64_t)mh << 32) | ml;
+}
+
+// Writes ids / scores [0, top_k): rank r < k from key, the rest -1 / -inf.
+__device__ __forceinline__ void store_result(int32_t* ids, float* scores, int i, uint64_t key) {
+  const bool ok = key != ~0ull;
+  if (ids) ids[i] = ok ? (int32_t)(key & 0xffffffffu) : -1;
+  if (scores) scores[i] = ok ? unordered(~(uint32_t)(key >> 32)) : -__builtin_huge_valf();
+}
+
+// Threshold merge (k <= kThreshK, nkeys <= kMergeLoads * kMergeThreads): T =
+// the largest of the W waves' smallest keys bounds the k-th smallest key from
+// above (W >= k distinct keys are <= T), so the answer is the first k of the
+// keys <= T -- typically a few dozen -- ranked by counting; more than
+// kThreshCand of them (keys clustered in one wave's share) falls back to the
+// selection rounds.
+constexpr int kThreshK = kMergeThreads / 64;
+constexpr int kThreshCand = 64;  // one per lane of the ranking wave
 
 // The first k of nkeys keys: each wave selects the first k of its share,
 // carried from pass to pass (kMergeLoads keys per lane per pass), then the
@@ -362,7 +450,53 @@ __global__ __launch_bounds__(kMergeThreads) void topk_merge_kernel(const uint64_
                                                                    float* __restrict__ scores, int top_k) {
   constexpr int W = kMergeThreads / 64;
   __shared__ uint64_t lists[W * kFusedK];
+  __shared__ uint64_t cand[kThreshCand];
+  __shared__ uint64_t wmin[W];
+  __shared__ int ncand;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (k <= kThreshK && nkeys <= (int64_t)kMergeLoads * kMergeThreads) {  // uniform
+    uint64_t x[kMergeLoads];
+#pragma unroll
+    for (int j = 0; j < kMergeLoads; ++j) {
+      const int64_t i = (int64_t)j * kMergeThreads + threadIdx.x;
+      x[j] = i < nkeys ? keys[i] : ~0ull;
+    }
+    if (threadIdx.x == 0) ncand = 0;
+    if (wave == 0) cand[lane] = ~0ull;  // the rank count reads whole groups of 8
+    uint64_t lm = x[0];
+#pragma unroll
+    for (int j = 1; j < kMergeLoads; ++j) lm = x[j] < lm ? x[j] : lm;
+    const uint64_t wm = wave_min_key(lm);
+    if (lane == 0) wmin[wave] = wm;
+    __syncthreads();
+    uint64_t t = wmin[0];
+#pragma unroll
+    for (int w = 1; w < W; ++w) t = wmin[w] > t ? wmin[w] : t;
+    int cnt = 0;
+#pragma unroll
+    for (int j = 0; j < kMergeLoads; ++j) cnt += x[j] <= t ? 1 : 0;
+    if (cnt > 0) {
+      int at = atomicAdd(&ncand, cnt);
+#pragma unroll
+      for (int j = 0; j < kMergeLoads; ++j)
+        if (x[j] <= t) {
+          if (at < kThreshCand) cand[at] = x[j];
+          ++at;
+        }
+    }
+    __syncthreads();
+    const int c = ncand;
+    if (c <= kThreshCand) {  // uniform
+      if (wave != 0) return;
+      const uint64_t mine = lane < c ? cand[lane] : ~0ull;
+      int rank = 0;
+      const int c8 = (c + 7) & ~7;
+      for (int j = 0; j < c8; ++j) rank += cand[j] < mine ? 1 : 0;
+      if (lane < c && rank < k) store_result(ids, scores, rank, mine);
+      for (int i = k + lane; i < top_k; i += 64) store_result(ids, scores, i, ~0ull);
+      return;
+    }
+  }
   uint64_t kept = ~0ull;  // lane r < k: the wave's r-th key so far
   for (int64_t base = 0; base < nkeys; base += (int64_t)kMergeLoads * kMergeThreads) {  // uniform trip count
     uint64_t x[kMergeLoads + 1];
@@ -381,16 +515,41 @@ __global__ __launch_bounds__(kMergeThreads) void topk_merge_kernel(const uint64_
 #pragma unroll
   for (int j = 0; j < W * kFusedK / 64; ++j) y[j] = lists[64 * j + lane];
   const uint64_t best = wave_select(y, k);
-  for (int i = lane; i < top_k; i += 64) {
-    const uint64_t key = i == lane && lane < k ? best : ~0ull;
-    const bool ok = key != ~0ull;
-    if (ids) ids[i] = ok ? (int32_t)(key & 0xffffffffu) : -1;
-    if (scores) scores[i] = ok ? unordered(~(uint32_t)(key >> 32)) : -__builtin_huge_valf();
-  }
+  for (int i = lane; i < top_k; i += 64) store_result(ids, scores, i, i == lane && lane < k ? best : ~0ull);
 }
 
 // Workgroups of the fused scan for n rows (each writes k keys).
-inline int64_t fused_wgs(int64_t n) { return div_up(n, (int64_t)kFusedRowsWg); }
+inline int64_t fused_wgs(int64_t n, int waves) { return div_up(n, (int64_t)kFusedRowsWave * waves); }
+
+// Scan workgroup size for n rows: 8 or 10 waves (128 or 160 rows), whichever
+// leaves the fewest rows on the busiest CU of a one-round grid (78,125 rows
+// on 256 CUs: 611 workgroups put three, 384 rows, on 99 CUs; 489 of 160 rows
+// at most two, 320 rows -- 19.9 against 20.2 us per query); ties keep 8.
+int fused_waves(int64_t n) {
+  const int64_t cus = attn::device_cus();
+  int best = kFusedWavesMin;
+  int64_t best_rows = 0;
+  for (int w : {kFusedWavesMin, kFusedWavesMax}) {
+    const int64_t rows = div_up(fused_wgs(n, w), cus) * kFusedRowsWave * w;
+    if (w == kFusedWavesMin || rows < best_rows) {
+      best = w;
+      best_rows = rows;
+    }
+  }
+  return best;
+}
+
+template <typename T>
+void launch_scan_topk(int waves, dim3 grid, hipStream_t s, const void* rows, int64_t stride, int n, int d,
+                      const float* q, float* sims, int mode, int k, uint64_t* keys) {
+  const T* r = static_cast<const T*>(rows);
+  if (waves == kFusedWavesMax)
+    hipLaunchKernelGGL((scan_topk_kernel<T, kFusedWavesMax>), grid, dim3(64 * kFusedWavesMax), 0, s, r, stride, n, d,
+                       q, sims, mode, k, keys);
+  else
+    hipLaunchKernelGGL((scan_topk_kernel<T, kFusedWavesMin>), grid, dim3(64 * kFusedWavesMin), 0, s, r, stride, n, d,
+                       q, sims, mode, k, keys);
+}
 
 // Keys written by pass p, and the number of passes, for n inputs and top k.
 struct Plan {
@@ -435,7 +594,8 @@ using namespace kessie::index;
 extern "C" size_t kessie_index_query_workspace_bytes(int num_chunks, int top_k) {
   if (num_chunks <= 0 || top_k <= 0) return 0;
   const int k = top_k < num_chunks ? top_k : num_chunks;
-  if (k <= kFusedK) return (size_t)((fused_wgs(num_chunks) * k * sizeof(uint64_t) + 255) / 256 * 256);
+  if (k <= kFusedK)  // sized for the smaller workgroups (the most lists)
+    return (size_t)((fused_wgs(num_chunks, kFusedWavesMin) * k * sizeof(uint64_t) + 255) / 256 * 256);
   const Plan p = plan_for(num_chunks, k);
   // Two ping-pong key arrays.
   return 2 * (size_t)((p.max_keys * sizeof(uint64_t) + 255) / 256 * 256);
@@ -470,23 +630,21 @@ extern "C" int kessie_index_query(const void* index_embeds, int64_t row_stride, 
                    "index query: workspace of %zu bytes needed, got %zu", need, workspace_bytes);
     KESSIE_REQUIRE(aligned16(workspace), KESSIE_ERR_INVALID, "index query: workspace not 16-byte aligned");
     uint64_t* keys = static_cast<uint64_t*>(workspace);
-    const int64_t wgs = fused_wgs(num_chunks);
+    const int waves = fused_waves(num_chunks);
+    const int64_t wgs = fused_wgs(num_chunks, waves);
     const dim3 grid((unsigned)wgs);
     switch (dtype) {
       case KESSIE_DTYPE_F32:
-        hipLaunchKernelGGL(scan_topk_kernel<float>, grid, dim3(kFusedThreads), 0, s,
-                           static_cast<const float*>(index_embeds), row_stride, num_chunks, embed_dim, query_embed,
-                           similarities, norm_mode, kk, keys);
+        launch_scan_topk<float>(waves, grid, s, index_embeds, row_stride, num_chunks, embed_dim, query_embed,
+                                similarities, norm_mode, kk, keys);
         break;
       case KESSIE_DTYPE_BF16:
-        hipLaunchKernelGGL(scan_topk_kernel<bf16_t>, grid, dim3(kFusedThreads), 0, s,
-                           static_cast<const bf16_t*>(index_embeds), row_stride, num_chunks, embed_dim, query_embed,
-                           similarities, norm_mode, kk, keys);
+        launch_scan_topk<bf16_t>(waves, grid, s, index_embeds, row_stride, num_chunks, embed_dim, query_embed,
+                                 similarities, norm_mode, kk, keys);
         break;
       default:
-        hipLaunchKernelGGL(scan_topk_kernel<f16_t>, grid, dim3(kFusedThreads), 0, s,
-                           static_cast<const f16_t*>(index_embeds), row_stride, num_chunks, embed_dim, query_embed,
-                           similarities, norm_mode, kk, keys);
+        launch_scan_topk<f16_t>(waves, grid, s, index_embeds, row_stride, num_chunks, embed_dim, query_embed,
+                                similarities, norm_mode, kk, keys);
     }
     if (check_launch("index query scan + top-k") != KESSIE_OK) return last_status();
     hipLaunchKernelGGL(topk_merge_kernel, dim3(1), dim3(kMergeThreads), 0, s, keys, wgs * kk, kk, top_ids,

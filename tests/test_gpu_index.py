@@ -125,3 +125,28 @@ def test_index_fused_scan_topk(dev, n, k, dtype):
     top = ids.cpu().tolist()
     best = sorted({n // 2, n - 1} | ({1} if n > 3 else set()))
     assert top[:len(best)] == best if k >= len(best) else top[:k] == best[:k]
+
+
+@pytest.mark.parametrize("k", [5, 8, 9])
+@pytest.mark.parametrize("clustered", [False, True])
+def test_index_merge_threshold_and_fallback(dev, k, clustered):
+    """78,125 rows, one merge workgroup over the scan workgroups' lists: k <= 8
+    ranks the keys at or below the largest of its waves' smallest keys; k = 9
+    and lists whose best keys all sit in one merge wave's share (rows 0..2047
+    close to the query: more candidates than the threshold pass holds) take
+    the selection rounds.  Bit-exact against a sort of the kernel's own
+    similarities either way."""
+    from kessie_amd import ops
+
+    n, d = 78125, 256
+    mat = randn((n, d), torch.float32, dev, 8)
+    q = randn((d,), torch.float32, dev, 9)
+    if clustered:
+        mat[:2048] = q + 0.05 * randn((2048, d), torch.float32, dev, 10)
+    sims, ids, scores = ops.index_query(mat, q, top_k=k)
+    torch.cuda.synchronize()
+    ref = cosine_ref(q.cpu().numpy(), mat.cpu().numpy(), 0)
+    assert np.abs(sims.cpu().numpy() - ref).max() <= 2e-6
+    _check_topk(sims, ids, scores, ref, k, 2e-6)
+    if clustered:
+        assert ids.cpu().max().item() < 2048
