@@ -127,18 +127,20 @@ def test_index_fused_scan_topk(dev, n, k, dtype):
     assert top[:len(best)] == best if k >= len(best) else top[:k] == best[:k]
 
 
-@pytest.mark.parametrize("k", [5, 8, 9])
+@pytest.mark.parametrize("n,k", [(78125, 5), (78125, 6), (78125, 8), (78125, 9), (40000, 8)])
 @pytest.mark.parametrize("clustered", [False, True])
-def test_index_merge_threshold_and_fallback(dev, k, clustered):
-    """78,125 rows, one merge workgroup over the scan workgroups' lists: k <= 8
-    ranks the keys at or below the largest of its waves' smallest keys; k = 9
-    and lists whose best keys all sit in one merge wave's share (rows 0..2047
+def test_index_merge_threshold_and_fallback(dev, n, k, clustered):
+    """One merge workgroup over the scan workgroups' lists (489 of them for
+    78,125 rows, 250 for 40,000): with k <= 8 and at most 3,072 keys (78,125
+    rows with k = 5, 6; 40,000 rows with k = 8) it ranks the keys at or below
+    the largest of its waves' smallest keys; more keys (78,125 with k = 8),
+    k = 9, or the best rows clustered in one merge wave's share (rows 0..2047
     close to the query: more candidates than the threshold pass holds) take
     the selection rounds.  Bit-exact against a sort of the kernel's own
     similarities either way."""
     from kessie_amd import ops
 
-    n, d = 78125, 256
+    d = 256
     mat = randn((n, d), torch.float32, dev, 8)
     q = randn((d,), torch.float32, dev, 9)
     if clustered:
