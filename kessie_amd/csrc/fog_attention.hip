@@ -971,7 +971,8 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) 
 }
 
 // ---------------------------------------------------------------------------
-// fp32 decode on MFMA (head_dim 128, pages of 16 * 2^k tokens): the bf16 kernel's
+// fp32 decode on MFMA (head_dim 128, pages of 16 * 2^k tokens) for GQA ratios
+// 8 and 16 (up to 4: decode_f32_4x4_kernel below): the bf16 kernel's
 // decomposition with v_mfma_f32_16x16x4_f32 and the probabilities kept in
 // fp32 (no rounding of p, so fp32 inputs meet a 1e-5 tolerance).
 //   * K: lane (grp, row) loads token `row`'s d = 32*grp .. 32*grp+31 (128
@@ -1294,39 +1295,259 @@ int launch_decode_mfma(Params& p, hipStream_t stream) {
   return KESSIE_OK;
 }
 
+// ---------------------------------------------------------------------------
+// fp32 decode for GQA ratios up to 4 on v_mfma_f32_4x4x1_16b_f32: 16
+// independent 4x4x1 products per instruction, block b = lane / 4; lane 4b + j
+// receives column j of block b's result (register r: row r), A comes from
+// lane 4b + r and B from lane 4b + j.  The 16x16x4 instance fills 16 head
+// columns of which G are live; here every column is:
+//   * S: block b = (d-quarter b / 4, token group b % 4), A = K (row r: token
+//     4 (b % 4) + r -- the token lane l & 15 loads, d = 32 (l >> 4) + step:
+//     the 16x16x4 instance's K loads unchanged), B = Q (column j: head j, zero
+//     from G on); 32 steps run through a d-quarter and two shuffles add the
+//     quarters, leaving lane l with head l & 3's scores of tokens
+//     4 ((l >> 2) & 3) + r in its registers r;
+//   * PV: A = p (row r: head r; each lane reads its head's 16 probabilities
+//     from a 64-float LDS slot of its wave), B = V (column: d = l in the first
+//     product, 64 + l in the second), read from global memory one dword per
+//     lane and token, so V needs no transpose; lane l ends with O[head r][l]
+//     and O[head r][64 + l] in its registers r.
+// ---------------------------------------------------------------------------
+template <int G, int PREF, int W, int FOG>
+__global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_f32_4x4_kernel(
+    Params p) {
+  static_assert(G >= 1 && G <= 4, "decode_f32_4x4_kernel: GQA ratio up to 4");
+  __shared__ __align__(16) float pslot_all[W][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int g = blockIdx.z * W + wave;
+  if (g >= p.Hkv) return;  // no workgroup barriers below
+  float* pslot = pslot_all[wave];
+  const int S = p.num_splits;
+  const int unit = blockIdx.y * S + blockIdx.x;  // balanced splits: this workgroup's unit
+  int b = blockIdx.y, split = blockIdx.x, per = 0;
+  int ctx;
+  if (p.balanced) {
+    const BatchPages bp = batch_pages(p);
+    per = decode_unit_pages(bp, S, p.B);
+    if (!decode_seq_of_unit(bp, per, unit, &b, &split)) return;  // past the batch's units: no partial to write
+    per = __builtin_amdgcn_readfirstlane(per);
+    b = __builtin_amdgcn_readfirstlane(b);
+    split = __builtin_amdgcn_readfirstlane(split);
+    ctx = bp.seq_len(b);
+  } else {
+    ctx = seq_ctx(p, b);
+  }
+  const int x = lane & 3;          // head of this lane's scores and probabilities
+  const int tg = (lane >> 2) & 3;  // its token group: tokens 4 tg + r
+  const int row = lane & 15;       // K: the token it loads
+  const int grp = lane >> 4;       // K and Q: its d-quarter
+
+  const int lo = p.window > 0 ? max(0, ctx - p.window) : 0;
+  const int pg_lo = lo >> 4;
+  const int pg_hi = (ctx + 15) >> 4;
+  if (!p.balanced) per = (pg_hi - pg_lo + S - 1) / S;
+  const int p0 = pg_lo + split * per;
+  const int p1 = min(pg_hi, p0 + per);
+
+  const float* kbase = static_cast<const float*>(p.k) + (int64_t)g * p.head_stride;
+  const float* vbase = static_cast<const float*>(p.v) + (int64_t)g * p.head_stride;
+  const int32_t* table = p.page_table + (int64_t)b * p.table_stride;
+  const int64_t ts = p.tok_stride;
+  const int psh = __builtin_ctz((unsigned)p.page_size) - 4;
+  const int pmask = (1 << psh) - 1;
+  const int64_t koff = (int64_t)row * ts + 32 * grp;
+
+  // B operand of S: Q[head x][d = 32 grp + 4 j + e] (zero from G on).
+  f32x4 qreg[8];
+  {
+    const float* qrow =
+        static_cast<const float*>(p.q) + (int64_t)b * p.q_bs + (int64_t)(g * G + min(x, G - 1)) * p.q_hs;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      qreg[j] = x < G ? *reinterpret_cast<const f32x4*>(qrow + 32 * grp + 4 * j) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+
+  f32x4 oacc[2];  // O[head r][d = l + 64 h]
+  oacc[0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  oacc[1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  float m_run = kNegInf, l_run = 0.0f;  // head x's
+
+  f32x4 kreg[PREF][8];
+  float vreg[PREF][32];  // V[token t][d = lane] at t, V[t][64 + lane] at 16 + t
+  int pid_s[PREF];
+  float fb_cur = 0.0f, fv_cur = 0.0f;
+  const float* fog_b = (FOG & kFogBias) ? p.bias + (int64_t)b * p.bias_bs : nullptr;
+  const float* fog_v = (FOG & kFogVs) ? p.vscale + (int64_t)b * p.vs_bs : nullptr;
+  auto load_fog = [&](int lp) {
+    const int tl = 16 * lp + lane;
+    const bool in = lane < 16 && tl >= lo && tl < ctx;
+    if (FOG & kFogBias) fb_cur = in ? fog_b[tl] : 0.0f;
+    if (FOG & kFogVs) fv_cur = in ? fog_v[tl] : 0.0f;
+  };
+  auto issue = [&](int st, int lp) {
+    const int pid = table[lp >> psh];
+    pid_s[st] = pid;
+    if (pid >= 0 && pid < p.num_pages) {
+      const int64_t at = (int64_t)pid * p.page_stride + (int64_t)((lp & pmask) << 4) * ts;
+      const float* kp = kbase + at;
+      const float* vp = vbase + at + lane;
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        kreg[st][j] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(kp + koff + 4 * j));
+#pragma unroll
+      for (int t = 0; t < 16; ++t) {
+        vreg[st][t] = __builtin_nontemporal_load(vp + t * ts);
+        vreg[st][16 + t] = __builtin_nontemporal_load(vp + t * ts + 64);
+      }
+    }
+  };
+
+#pragma unroll
+  for (int st = 0; st < PREF; ++st)
+    if (p0 + st < p1) issue(st, p0 + st);
+  if (FOG && p0 < p1) load_fog(p0);
+
+  for (int base = p0; base < p1; base += PREF) {
+#pragma unroll
+    for (int st = 0; st < PREF; ++st) {
+      const int lp = base + st;
+      if (lp >= p1) break;
+      const int pid = pid_s[st];
+      if (pid < 0 || pid >= p.num_pages) {
+        if (FOG && lp + 1 < p1) load_fog(lp + 1);
+        if (lp + PREF < p1) issue(st, lp + PREF);
+        continue;
+      }
+      const int t_page = lp << 4;
+      const bool full = t_page >= lo && t_page + 16 <= ctx;
+      f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          acc = __builtin_amdgcn_mfma_f32_4x4x1f32(kreg[st][j][e], qreg[j][e], acc, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {  // the four d-quarters
+        acc[r] += __shfl_xor(acc[r], 16);
+        acc[r] += __shfl_xor(acc[r], 32);
+      }
+      float sc[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int t = t_page + 4 * tg + r;
+        const bool ok = full || (t >= lo && t < ctx);
+        float s = acc[r] * p.sm_scale;
+        if (FOG & kFogBias) s += __shfl(fb_cur, 4 * tg + r);
+        sc[r] = ok ? s : kNegInf;
+      }
+      float mloc = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+      mloc = fmaxf(mloc, __shfl_xor(mloc, 4));
+      mloc = fmaxf(mloc, __shfl_xor(mloc, 8));
+      const float mnew = fmaxf(m_run, mloc);
+      const float alpha = (m_run == kNegInf) ? 0.0f : __expf(m_run - mnew);
+      float pr[4];
+      float psum = 0.0f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        pr[r] = (sc[r] == kNegInf) ? 0.0f : __expf(sc[r] - mnew);
+        psum += pr[r];
+      }
+      psum += __shfl_xor(psum, 4);
+      psum += __shfl_xor(psum, 8);
+      l_run = l_run * alpha + psum;
+      m_run = mnew;
+      if (FOG & kFogVs) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pr[r] *= __shfl(fv_cur, 4 * tg + r);
+      }
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {  // head r's factor, from lane r
+          const float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha), r));
+          oacc[0][r] *= a;
+          oacc[1][r] *= a;
+        }
+      }
+      if (!full) {  // tokens outside [lo, ctx) may hold anything: zero their V
+#pragma unroll
+        for (int t = 0; t < 16; ++t)
+          if (!(t_page + t >= lo && t_page + t < ctx)) {
+            vreg[st][t] = 0.0f;
+            vreg[st][16 + t] = 0.0f;
+          }
+      }
+      // p to the wave's LDS slot ([head][token]); each lane reads its head's 16.
+      wave_lds_sync();  // the previous block's reads are done
+      if (grp == 0) *reinterpret_cast<f32x4*>(pslot + 16 * x + 4 * tg) = f32x4{pr[0], pr[1], pr[2], pr[3]};
+      wave_lds_sync();
+      f32x4 pt[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) pt[k] = *reinterpret_cast<const f32x4*>(pslot + 16 * x + 4 * k);
+#pragma unroll
+      for (int t = 0; t < 16; ++t) {
+        oacc[0] = __builtin_amdgcn_mfma_f32_4x4x1f32(pt[t >> 2][t & 3], vreg[st][t], oacc[0], 0, 0, 0);
+        oacc[1] = __builtin_amdgcn_mfma_f32_4x4x1f32(pt[t >> 2][t & 3], vreg[st][16 + t], oacc[1], 0, 0, 0);
+      }
+      if (FOG && lp + 1 < p1) load_fog(lp + 1);
+      if (lp + PREF < p1) issue(st, lp + PREF);
+    }
+  }
+
+  // Lane l holds O[head r][l] and O[head r][64 + l] (r < G live); lane r holds
+  // head r's running max and sum.
+#pragma unroll
+  for (int r = 0; r < G; ++r) {
+    const int head = g * G + r;
+    if (p.direct_out) {
+      const float lr = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, l_run), r));
+      const float il = lr > 0.0f ? 1.0f / lr : 0.0f;
+      float* dst = static_cast<float*>(p.out) + (int64_t)b * p.o_bs + (int64_t)head * p.o_hs;
+      dst[lane] = oacc[0][r] * il;
+      dst[64 + lane] = oacc[1][r] * il;
+    } else {
+      const int64_t slot = p.balanced ? (int64_t)head * S * p.B + unit : row_id(p, b, 0, head) * S + split;
+      float* dst = p.ws_o + slot * 128;
+      dst[lane] = oacc[0][r];
+      dst[64 + lane] = oacc[1][r];
+      if (lane == r) {
+        p.ws_m[slot] = m_run;
+        p.ws_l[slot] = l_run;
+      }
+    }
+  }
+}
+
+template <int G, int PREF, int FOG>
+void launch_f32_instance(const Params& p, dim3 grid, dim3 block, hipStream_t stream) {
+  if constexpr (G <= 4)
+    hipLaunchKernelGGL((decode_f32_4x4_kernel<G, PREF, kDecWaves, FOG>), grid, block, 0, stream, p);
+  else
+    hipLaunchKernelGGL((decode_mfma_f32_kernel<G, PREF, kDecWaves, FOG>), grid, block, 0, stream, p);
+}
+
 template <int G>
 int launch_decode_mfma_f32(Params& p, hipStream_t stream) {
   dim3 grid(p.num_splits, p.B, div_up(p.Hkv, kDecWaves));
   const int fog = (p.bias ? kFogBias : 0) | (p.vscale ? kFogVs : 0);
   const dim3 block(kDecWaves * 64);
   // Splits of at most two 16-token blocks (short contexts) take the
-  // one-block-in-flight instance: half the code to fetch, and a 4K-token
-  // step 1 us faster although its two blocks then load one after the other.
+  // one-block-in-flight instance: less code to fetch, and a 4K-token step
+  // 1 us faster although its two blocks then load one after the other.
   const int per = div_up(div_up(max(p.max_ctx, 1), 16), max(p.num_splits, 1));
   if (!p.balanced && per <= 2) {
     switch (fog) {
-      case 0: hipLaunchKernelGGL((decode_mfma_f32_kernel<G, 1, kDecWaves, 0>), grid, block, 0, stream, p); break;
-      case kFogBias:
-        hipLaunchKernelGGL((decode_mfma_f32_kernel<G, 1, kDecWaves, kFogBias>), grid, block, 0, stream, p);
-        break;
-      case kFogVs:
-        hipLaunchKernelGGL((decode_mfma_f32_kernel<G, 1, kDecWaves, kFogVs>), grid, block, 0, stream, p);
-        break;
-      default:
-        hipLaunchKernelGGL((decode_mfma_f32_kernel<G, 1, kDecWaves, kFogBias | kFogVs>), grid, block, 0, stream, p);
+      case 0: launch_f32_instance<G, 1, 0>(p, grid, block, stream); break;
+      case kFogBias: launch_f32_instance<G, 1, kFogBias>(p, grid, block, stream); break;
+      case kFogVs: launch_f32_instance<G, 1, kFogVs>(p, grid, block, stream); break;
+      default: launch_f32_instance<G, 1, kFogBias | kFogVs>(p, grid, block, stream);
     }
   } else {
     switch (fog) {
-      case 0: hipLaunchKernelGGL((decode_mfma_f32_kernel<G, kDecPref, kDecWaves, 0>), grid, block, 0, stream, p); break;
-      case kFogBias:
-        hipLaunchKernelGGL((decode_mfma_f32_kernel<G, kDecPref, kDecWaves, kFogBias>), grid, block, 0, stream, p);
-        break;
-      case kFogVs:
-        hipLaunchKernelGGL((decode_mfma_f32_kernel<G, kDecPref, kDecWaves, kFogVs>), grid, block, 0, stream, p);
-        break;
-      default:
-        hipLaunchKernelGGL((decode_mfma_f32_kernel<G, kDecPref, kDecWaves, kFogBias | kFogVs>), grid, block, 0, stream,
-                           p);
+      case 0: launch_f32_instance<G, kDecPref, 0>(p, grid, block, stream); break;
+      case kFogBias: launch_f32_instance<G, kDecPref, kFogBias>(p, grid, block, stream); break;
+      case kFogVs: launch_f32_instance<G, kDecPref, kFogVs>(p, grid, block, stream); break;
+      default: launch_f32_instance<G, kDecPref, kFogBias | kFogVs>(p, grid, block, stream);
     }
   }
   if (check_launch("fog decode (mfma fp32)") != KESSIE_OK) return KESSIE_ERR_HIP;

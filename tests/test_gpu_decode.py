@@ -314,14 +314,17 @@ def test_decode_ragged_batch_at_the_balanced_limit(dev, b):
     (32, 8, "vscale", 0, None),
     (32, 8, "both", 100, [4096, 1000, 17]),
     (16, 16, "bias", 0, [333, 0, 4096]),
+    (16, 8, "vscale", 0, [4096, 2500]),
+    (64, 8, "both", 0, None),
     (64, 4, "none", 5000, None),
 ])
 def test_decode_fp32_mfma_matches_oracle_and_generic(dev, monkeypatch, hq, hkv, fog, window, ctx_lens):
-    """fp32 decode on the MFMA kernel (v_mfma_f32_16x16x4_f32, probabilities in
-    fp32): within the fp32 tolerance of the oracle and of the VALU kernel."""
+    """fp32 decode on the MFMA kernels (v_mfma_f32_4x4x1_16b_f32 for GQA ratios
+    up to 4, v_mfma_f32_16x16x4_f32 for 8 and 16; probabilities in fp32):
+    within the fp32 tolerance of the oracle and of the VALU kernel."""
     from kessie_amd import ops
 
-    b = 3 if ctx_lens else 2
+    b = len(ctx_lens) if ctx_lens else 2
     ctx = 4096
     q, pool, table, lens = decode_case(b, hq, hkv, 128, ctx, 16, torch.float32, dev, seed=71, ctx_lens=ctx_lens)
     vs = build_fog_weights(ctx).to(dev) if fog in ("vscale", "both") else None
@@ -334,3 +337,28 @@ def test_decode_fp32_mfma_matches_oracle_and_generic(dev, monkeypatch, hq, hkv, 
                            None if bias is None else bias.cpu(), window=window)
     _check(a, ref, torch.float32)
     _check(g, ref, torch.float32)
+
+
+@pytest.mark.parametrize("hq,hkv,ctx_lens", [(16, 8, [20000, 3000]), (32, 8, [30000]), (8, 8, [12345, 1, 9000])])
+def test_decode_fp32_long_contexts(dev, hq, hkv, ctx_lens):
+    """fp32 decode with more than two 16-token blocks per split (the
+    two-blocks-in-flight instance of the 4x4x1 kernel), GQA 2, 4 and 1,
+    ragged lengths incl. a one-token sequence, V-fog: against the oracle at
+    1e-5."""
+    out, ref = _run(dev, len(ctx_lens), hq, hkv, max(ctx_lens), torch.float32, ctx_lens=ctx_lens)
+    _check(out, ref, torch.float32)
+
+
+def test_decode_fp32_invalid_page_ids_are_masked(dev):
+    """An invalid page id (negative, or past the pool) on the fp32 4x4x1
+    kernel: its 16 tokens are left out, as the bf16 kernel does."""
+    from kessie_amd import ops
+
+    q, pool, table, lens = decode_case(1, 32, 8, 128, 256, 16, torch.float32, dev, seed=4)
+    table[0, 2] = -1
+    table[0, 11] = 1 << 20
+    out = ops.fog_decode(q, pool, table, lens, max_ctx=256)
+    torch.cuda.synchronize()
+    keep = [i for i in range(16) if i not in (2, 11)]
+    ref = paged_decode_ref(q.cpu(), pool.cpu(), table.cpu()[:, keep].contiguous(), torch.tensor([len(keep) * 16]))
+    _check(out, ref, torch.float32)
