@@ -664,7 +664,7 @@ def bench_decode_fp32(dev, reps=20, cpu=False):
         run_decode_step(s)
     torch.cuda.synchronize()
     ms = time_back_to_back(lambda i: run_decode_step(s), reps)  # steps back to back, as the headline's
-    # The streaming kernel alone (decode_mfma_f32_kernel), K launches back to
+    # The streaming kernel alone (decode_f32_4x4_kernel), K launches back to
     # back: at ~16 us an event pair around each launch would add its dispatch.
     ms_kern = time_back_to_back(lambda i: ops.fog_decode_partials(s["q"], s["pool"], s["table"], s["lens"], s["ctx"],
                                                                    s["ws"], fog_vscale=s["fog"]), reps)
@@ -683,9 +683,9 @@ def bench_decode_fp32(dev, reps=20, cpu=False):
     return {"workload": "fog decode fp32, B=1, 32q/8kv, D=128, 4096-token context",
             "ms": round(ms, 5), "gbs": round(s["bytes"] / (ms * 1e-3) / 1e9, 1), "cpu_baseline": res_cpu,
             "kernel_ms": round(ms_kern, 5),
-            "roofline": {"bound": "hbm", "kernel": "decode_mfma_f32_kernel", "achieved": round(ach, 1),
+            "roofline": {"bound": "hbm", "kernel": "decode_f32_4x4_kernel", "achieved": round(ach, 1),
                          "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
-                         "traffic": read_traffic("decode_mfma_f32_kernel"), "algorithmic_bytes": s["bytes"],
+                         "traffic": read_traffic("decode_f32_4x4_kernel"), "algorithmic_bytes": s["bytes"],
                          "timing": "20 launches of the streaming kernel back to back between two events"}}
 
 
