@@ -156,6 +156,9 @@ __device__ __forceinline__ float sum2<f16_t>(uint32_t w, float acc) {
 }
 
 
+// Headroom of the lazy rescale, in log2 units: probabilities up to 2^8.
+constexpr float kRescaleSlack = 8.0f;
+
 template <typename T, int G, bool kBias, bool kVs, bool kSplit, int kMode, int kD>
 __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
   static_assert(kD == 128 || kD == 64, "head_dim 128, or 64 on table-less pages");
@@ -606,9 +609,12 @@ __global__ __launch_bounds__(kPfThreads) void prefill_mfma_kernel(Params p) {
       }
     float mloc = max_xor32(fmaxf(ma, mb));
     if (!kBias) mloc *= c2;  // without a bias, y = x * c2 and c2 > 0
-    const float mnew = fmaxf(m_run, mloc);
+    // The reference max moves only when a row's max rises by more than
+    // kRescaleSlack (log2 units); until then p = 2^(y - m_run) <= 2^kRescaleSlack,
+    // as exact in T as any p <= 1, and the O accumulators are left alone.
+    const float mnew = mloc > m_run + kRescaleSlack ? mloc : m_run;
     const float muse = mnew == kNegInf ? 0.0f : mnew;
-    const float alpha = mnew == kNegInf ? 1.0f : __builtin_amdgcn_exp2f(m_run - mnew);
+    const float alpha = mnew == m_run ? 1.0f : __builtin_amdgcn_exp2f(m_run - mnew);
     // (Rescaled before the exponentials, so that they, the next scores and PV
     // form one branch-free region.)
     if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {

@@ -39,6 +39,8 @@ constexpr int kF32Row = 128 + 4;          // LDS row stride of the K and V tiles
 
 typedef float f32x4v __attribute__((ext_vector_type(4)));
 
+constexpr float kF32RescaleSlack = 5.545177444479562f;  // 8 ln 2
+
 template <int FOG, bool kSplit>
 __global__ __launch_bounds__(kF32Threads) void prefill_f32_kernel(Params p) {
   constexpr bool kBias = (FOG & 1) != 0, kVs = (FOG & 2) != 0;
@@ -206,8 +208,11 @@ __global__ __launch_bounds__(kF32Threads) void prefill_f32_kernel(Params p) {
     float mloc = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
     mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
     mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
-    const float mnew = fmaxf(m_run, mloc);
-    const float alpha = m_run == kNegInf ? (mnew == kNegInf ? 1.0f : 0.0f) : __expf(m_run - mnew);
+    // The reference max moves only when a row's max rises by more than
+    // kF32RescaleSlack (natural units, 8 ln 2): until then p <= 2^8 and the O
+    // accumulators are left alone.
+    const float mnew = mloc > m_run + kF32RescaleSlack ? mloc : m_run;
+    const float alpha = mnew == m_run ? 1.0f : (m_run == kNegInf ? 0.0f : __expf(m_run - mnew));
     float pr[4];
     float psum = 0.0f;
 #pragma unroll
