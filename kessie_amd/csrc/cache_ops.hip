@@ -36,12 +36,30 @@ __device__ __forceinline__ float round_to<float>(float x) {
 
 template <typename T>
 __global__ __launch_bounds__(kThreads) void fog_bias_kernel(T* buf, int kv_len, int boundary, float inv_b,
-                                                            float neg_alpha) {
+                                                            float neg_alpha, const int32_t* recall, int n_recall,
+                                                            float boost) {
 #pragma clang fp contract(off)
-  const int i = blockIdx.x * kThreads + threadIdx.x;
+  // Recalled positions take the boost: the workgroup marks those inside its
+  // own kThreads positions (a scan of the recall list into LDS flags), so
+  // every position is written once, by one launch.
+  __shared__ int marked[kThreads];
+  const int lo = blockIdx.x * kThreads;
+  const int i = lo + threadIdx.x;
+  marked[threadIdx.x] = 0;
+  if (n_recall > 0) {  // uniform
+    __syncthreads();
+    const int hi = min(lo + kThreads, kv_len);
+    for (int r = threadIdx.x; r < n_recall; r += kThreads) {
+      const int p = recall[r];
+      if (p >= lo && p < hi) marked[p - lo] = 1;
+    }
+    __syncthreads();
+  }
   if (i >= kv_len) return;
   T v = round_to<T>(0.0f);
-  if (i < boundary) {
+  if (marked[threadIdx.x]) {
+    v = round_to<T>(boost);
+  } else if (i < boundary) {
     const T pos = round_to<T>((float)i);
     const T x = round_to<T>(to_f32(pos) * inv_b);
     const T d = round_to<T>(1.0f - to_f32(x));
@@ -51,15 +69,6 @@ __global__ __launch_bounds__(kThreads) void fog_bias_kernel(T* buf, int kv_len, 
   buf[i] = v;
 }
 
-template <typename T>
-__global__ __launch_bounds__(kThreads) void recall_scatter_kernel(T* buf, int kv_len, const int32_t* pos, int n,
-                                                                  float boost) {
-  const int r = blockIdx.x * kThreads + threadIdx.x;
-  if (r >= n) return;
-  const int p = pos[r];
-  if (p >= 0 && p < kv_len) buf[p] = round_to<T>(boost);
-}
-
 // One row per sequence: row b is the vector above for kv_len = seq_lens[b]
 // (its own fog boundary B_b = int(len * (1 - fog_start)), computed in double
 // as in Python), every value rounded as in `T` and stored as fp32 -- the form
@@ -67,17 +76,32 @@ __global__ __launch_bounds__(kThreads) void recall_scatter_kernel(T* buf, int kv
 template <typename T>
 __global__ __launch_bounds__(kThreads) void fog_bias_rows_kernel(float* out, int64_t row_stride,
                                                                  const int32_t* seq_lens, int max_len,
-                                                                 double one_minus_fs, float neg_alpha) {
+                                                                 double one_minus_fs, float neg_alpha,
+                                                                 const int32_t* recall, int n_recall, float boost) {
 #pragma clang fp contract(off)
+  __shared__ int marked[kThreads];  // recalled positions of this workgroup's range, as in fog_bias_kernel
   const int b = blockIdx.y;
-  const int i = blockIdx.x * kThreads + threadIdx.x;
-  if (i >= max_len) return;
+  const int lo = blockIdx.x * kThreads;
+  const int i = lo + threadIdx.x;
   const int len = min(max(seq_lens[b], 0), max_len);
+  marked[threadIdx.x] = 0;
+  if (n_recall > 0) {  // uniform
+    __syncthreads();
+    const int hi = min(lo + kThreads, len);
+    for (int r = threadIdx.x; r < n_recall; r += kThreads) {
+      const int p = recall[r];
+      if (p >= lo && p < hi) marked[p - lo] = 1;
+    }
+    __syncthreads();
+  }
+  if (i >= max_len) return;
   const double bd = (double)len * one_minus_fs;
   const int64_t big_b = bd <= 0.0 ? 0 : (int64_t)bd;
   const int boundary = (int)(big_b < len ? big_b : len);
   float v = 0.0f;
-  if (i < boundary) {
+  if (marked[threadIdx.x]) {
+    v = to_f32(round_to<T>(boost));
+  } else if (i < boundary) {
     const float inv_b = __frcp_rn((float)big_b);  // fp32 1/B, rounded to nearest as on the host
     const T pos = round_to<T>((float)i);
     const T x = round_to<T>(to_f32(pos) * inv_b);
@@ -89,26 +113,12 @@ __global__ __launch_bounds__(kThreads) void fog_bias_rows_kernel(float* out, int
 }
 
 template <typename T>
-__global__ __launch_bounds__(kThreads) void recall_rows_kernel(float* out, int64_t row_stride,
-                                                               const int32_t* seq_lens, int max_len,
-                                                               const int32_t* pos, int n, float boost) {
-  const int b = blockIdx.y;
-  const int r = blockIdx.x * kThreads + threadIdx.x;
-  if (r >= n) return;
-  const int len = min(max(seq_lens[b], 0), max_len);
-  const int p = pos[r];
-  if (p >= 0 && p < len) out[(int64_t)b * row_stride + p] = to_f32(round_to<T>(boost));
-}
-
-template <typename T>
 int fog_bias_rows_launch(float* out, int64_t row_stride, const int32_t* seq_lens, int rows, int max_len,
                          double one_minus_fs, float neg_alpha, const int32_t* recall, int n_recall, float boost,
                          hipStream_t s) {
   hipLaunchKernelGGL(fog_bias_rows_kernel<T>, dim3(div_up(max_len, kThreads), rows), dim3(kThreads), 0, s, out,
-                     row_stride, seq_lens, max_len, one_minus_fs, neg_alpha);
-  if (n_recall > 0)
-    hipLaunchKernelGGL(recall_rows_kernel<T>, dim3(div_up(n_recall, kThreads), rows), dim3(kThreads), 0, s, out,
-                       row_stride, seq_lens, max_len, recall, n_recall, boost);
+                     row_stride, seq_lens, max_len, one_minus_fs, neg_alpha, recall, n_recall > 0 ? n_recall : 0,
+                     boost);
   return check_launch("fog bias rows");
 }
 
@@ -140,10 +150,7 @@ int fog_bias_launch(void* buf, int kv_len, int boundary, float inv_b, float neg_
                     int n_recall, float boost, hipStream_t s) {
   T* b = static_cast<T*>(buf);
   hipLaunchKernelGGL(fog_bias_kernel<T>, dim3(div_up(kv_len, kThreads)), dim3(kThreads), 0, s, b, kv_len, boundary,
-                     inv_b, neg_alpha);
-  if (n_recall > 0)
-    hipLaunchKernelGGL(recall_scatter_kernel<T>, dim3(div_up(n_recall, kThreads)), dim3(kThreads), 0, s, b, kv_len,
-                       recall, n_recall, boost);
+                     inv_b, neg_alpha, recall, n_recall > 0 ? n_recall : 0, boost);
   return check_launch("fog bias");
 }
 
