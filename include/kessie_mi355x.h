@@ -416,8 +416,9 @@ int kessie_page_gather(const void* src_pool, int64_t page_bytes,
  * buf[p] = -fog_alpha * (1 - p/B)^2 for p < B, 0 otherwise, every op rounded
  * to `dtype` as torch's device kernels round it (p/B as p * fp32(1/B)); then
  * buf[r] = dtype(recall_boost) for each recall_positions[r] in [0, kv_len)
- * (num_recall int32 device values; duplicates allowed).  One launch for the
- * vector plus one for the recall scatter; no host synchronisation. */
+ * (num_recall int32 device values; duplicates allowed).  One launch (each
+ * workgroup sets the recalled positions of its own range); no host
+ * synchronisation. */
 int kessie_fog_bias_fill(void* buf, int dtype, int kv_len, double fog_alpha,
                          double fog_start, const int32_t* recall_positions,
                          int num_recall, double recall_boost, void* stream);
@@ -429,7 +430,7 @@ int kessie_fog_bias_fill(void* buf, int dtype, int kv_len, double fog_alpha,
  * seq_lens[b] (each sequence its own fog boundary
  * B_b = int(seq_lens[b] * (1.0 - fog_start))), widened to fp32; positions
  * from seq_lens[b] to max_len - 1 get 0.  Recalled positions below a row's
- * length get dtype(recall_boost).  Two launches, no host synchronisation.
+ * length get dtype(recall_boost).  One launch, no host synchronisation.
  * (kessie_attention.py:114-139 builds one vector per call, for one kv_len;
  * this is that vector for every sequence of a mixed batch.) */
 int kessie_fog_bias_fill_rows(float* out, int64_t row_stride,
