@@ -327,7 +327,55 @@ __device__ void decode_units_of_seq(const BatchPages& bp, int P, int b, int* u0,
 // column, and the groups meet in LDS.  (One thread per d looping over every
 // split was latency-bound: 25 us for one 128K sequence's 32 rows x 256 splits,
 // against 89 us for the whole partials kernel.)
-template <typename T>
+// Sum over the split groups of column col of a combine workgroup (thread
+// tid = group * cols + col, cols a power of two).  TREE: the groups inside a
+// wave by shuffles (lane bits from cols up), then the waves' sums in order
+// through LDS -- a few steps where adding the groups one by one took a chain
+// of dependent LDS reads (one combine of the fp32 4K decode: 32 groups).  Not
+// TREE: the groups added one by one in increasing order, which with at most
+// one split per group is the splits in increasing order whatever cols is --
+// so a varlen prefill and its per-sequence launches (different row counts,
+// hence different head_dim splits) give the same bits.  Both combine kernels
+// sum this way for a given TREE, so their results are the same bits.  The
+// result is valid in threads tid < cols.
+template <bool TREE>
+__device__ __forceinline__ float2 sum_groups(float ax, float ay, int tid, int cols, int groups, float2* part) {
+  if (!TREE) {
+    part[tid] = make_float2(ax, ay);
+    __syncthreads();
+    float2 acc = make_float2(0.0f, 0.0f);
+    if (tid < cols) {
+      acc = part[tid];
+      for (int g = 1; g < groups; ++g) {
+        acc.x += part[g * cols + tid].x;
+        acc.y += part[g * cols + tid].y;
+      }
+    }
+    return acc;
+  }
+  for (int off = cols; off < 64; off <<= 1) {
+    ax += __shfl_xor(ax, off, 64);
+    ay += __shfl_xor(ay, off, 64);
+  }
+  const int lane = tid & 63;
+  const int q_n = cols < 64 ? kCombineThreads / 64 : groups;  // partial sums per column
+  if (cols >= 64)
+    part[tid] = make_float2(ax, ay);
+  else if (lane < cols)
+    part[(tid >> 6) * cols + lane] = make_float2(ax, ay);
+  __syncthreads();
+  float2 acc = make_float2(0.0f, 0.0f);
+  if (tid < cols) {
+    acc = part[tid];
+    for (int q = 1; q < q_n; ++q) {
+      acc.x += part[q * cols + tid].x;
+      acc.y += part[q * cols + tid].y;
+    }
+  }
+  return acc;
+}
+
+template <typename T, bool TREE>
 __global__ __launch_bounds__(kCombineThreads) void combine_kernel(Params p) {
   __shared__ float e_s[kMaxSplits];
   __shared__ float2 part[kCombineThreads];
@@ -402,14 +450,8 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(Params p) {
       ax += e * v.x;
       ay += e * v.y;
     }
-    part[tid] = make_float2(ax, ay);
-    __syncthreads();
+    const float2 acc = sum_groups<TREE>(ax, ay, tid, cols, groups, part);
     if (tid < cols) {
-      float2 acc = part[tid];
-      for (int g = 1; g < groups; ++g) {
-        acc.x += part[g * cols + tid].x;
-        acc.y += part[g * cols + tid].y;
-      }
       store_out<T>(p, b, i, h, d0 + 2 * tid, acc.x * il);
       store_out<T>(p, b, i, h, d0 + 2 * tid + 1, acc.y * il);
     }
@@ -438,11 +480,11 @@ inline int combine_dsplit(int64_t rows, int D) {
 // instead of one; a 4K-token decode's combine is latency-bound).  The same
 // arithmetic in the same order as combine_kernel's fast path -- max and sum
 // over lanes s, s + 64, ... then the same butterfly, each group's splits
-// summed in increasing order, the groups added in order -- so the two give
-// the same bits.
+// summed in increasing order, the groups met by the same sum_groups -- so the
+// two give the same bits.
 constexpr int kAheadLoads = 8;
 
-template <typename T>
+template <typename T, bool TREE>
 __global__ __launch_bounds__(kCombineThreads) void combine_ahead_kernel(Params p) {
   __shared__ float e_s[256];
   __shared__ float2 part[kCombineThreads];
@@ -514,14 +556,8 @@ __global__ __launch_bounds__(kCombineThreads) void combine_ahead_kernel(Params p
       ay += e * v[j].y;
     }
   }
-  part[tid] = make_float2(ax, ay);
-  __syncthreads();
+  const float2 acc = sum_groups<TREE>(ax, ay, tid, cols, groups, part);
   if (tid < cols) {
-    float2 acc = part[tid];
-    for (int g = 1; g < groups; ++g) {
-      acc.x += part[g * cols + tid].x;
-      acc.y += part[g * cols + tid].y;
-    }
     store_out<T>(p, b, i, h, d0 + 2 * tid, acc.x * il);
     store_out<T>(p, b, i, h, d0 + 2 * tid + 1, acc.y * il);
   }
@@ -530,7 +566,9 @@ __global__ __launch_bounds__(kCombineThreads) void combine_ahead_kernel(Params p
 // The per-row merge of split partials: combine_ahead_kernel where its loads
 // fit (plain split layout, S <= 256, an even chunk dividing the workgroup,
 // S <= groups * kAheadLoads), else combine_kernel.  Same bits either way.
-template <typename T>
+// Decode sums the split groups as a tree; the prefill combines (TREE false)
+// in split order, which keeps varlen and per-sequence launches bit-equal.
+template <typename T, bool TREE = true>
 void launch_row_combine(const Params& p, int64_t rows, hipStream_t s) {
   const int y = combine_dsplit(rows, p.D);
   const int chunk = p.D / y;
@@ -538,9 +576,9 @@ void launch_row_combine(const Params& p, int64_t rows, hipStream_t s) {
   bool ahead = !p.balanced && S <= 256 && (chunk & 1) == 0 && kCombineThreads % (chunk / 2) == 0;
   if (ahead) ahead = S <= (kCombineThreads / (chunk / 2)) * kAheadLoads;
   if (ahead)
-    hipLaunchKernelGGL(combine_ahead_kernel<T>, dim3((unsigned)rows, y), dim3(kCombineThreads), 0, s, p);
+    hipLaunchKernelGGL((combine_ahead_kernel<T, TREE>), dim3((unsigned)rows, y), dim3(kCombineThreads), 0, s, p);
   else
-    hipLaunchKernelGGL(combine_kernel<T>, dim3((unsigned)rows, y), dim3(kCombineThreads), 0, s, p);
+    hipLaunchKernelGGL((combine_kernel<T, TREE>), dim3((unsigned)rows, y), dim3(kCombineThreads), 0, s, p);
 }
 
 // Two consecutive outputs of lane-owned columns: one 8-byte store for
@@ -677,7 +715,7 @@ void launch_combine(const Params& p, int64_t rows, hipStream_t s) {
     }
     return;
   }
-  launch_row_combine<T>(p, rows, s);
+  launch_row_combine<T, false>(p, rows, s);
 }
 
 
