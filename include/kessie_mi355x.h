@@ -417,8 +417,9 @@ int kessie_page_gather(const void* src_pool, int64_t page_bytes,
  * to `dtype` as torch's device kernels round it (p/B as p * fp32(1/B)); then
  * buf[r] = dtype(recall_boost) for each recall_positions[r] in [0, kv_len)
  * (num_recall int32 device values; duplicates allowed).  One launch (each
- * workgroup sets the recalled positions of its own range); no host
- * synchronisation. */
+ * workgroup sets the recalled positions of its own range, reading the whole
+ * recall list: ~kv_len / 256 * num_recall reads, cheap for recall lists of a
+ * few thousand positions); no host synchronisation. */
 int kessie_fog_bias_fill(void* buf, int dtype, int kv_len, double fog_alpha,
                          double fog_start, const int32_t* recall_positions,
                          int num_recall, double recall_boost, void* stream);
