@@ -40,6 +40,9 @@ def _close_attn(got, ref):
     (torch.bfloat16, 1000, 0.0, 0.5, []),
     (torch.float32, 3, 0.5, 1.5, [1]),               # negative boundary: no fog
     (torch.float32, 0, 0.5, 0.5, []),
+    # thousands of recalled positions (every workgroup scans the whole list):
+    # workgroup edges, duplicates, out-of-range values
+    (torch.bfloat16, 131072, 0.5, 0.5, list(range(0, 131072, 37)) + [255, 256, 511, 512, 512, 131071, 131072, -1]),
 ])
 def test_fog_bias_fill(dev, dtype, kv_len, alpha, start, recall):
     from kessie_amd import ops
@@ -409,8 +412,10 @@ def test_connector_save_blocks_modes(dev, monkeypatch, mode):
         assert torch.equal(blk.kv_data, cache[:, bid, :tok].cpu())
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
-def test_fog_bias_rows_match_the_reference_vector_per_sequence(dev, dtype):
+@pytest.mark.parametrize("dtype,rec", [(torch.bfloat16, [5, 250, 4000, 131071]), (torch.float16, [5, 250, 4000, 131071]),
+                                       (torch.float32, [5, 250, 4000, 131071]),
+                                       (torch.bfloat16, list(range(3, 131072, 41)) + [255, 256, 298, 299, 300, 300, -7])])
+def test_fog_bias_rows_match_the_reference_vector_per_sequence(dev, dtype, rec):
     """Row b of the batched producer equals, bit for bit, the reference's op
     sequence run by torch on the same device for kv_len = seq_lens[b] (widened
     to fp32), zero past the row's length; recalled positions past a row's
@@ -419,7 +424,6 @@ def test_fog_bias_rows_match_the_reference_vector_per_sequence(dev, dtype):
 
     lens = [0, 1, 7, 300, 4096, 131072, 999, 2]
     n = max(lens)
-    rec = [5, 250, 4000, 131071]
     out = torch.full((len(lens), n), float("nan"), dtype=torch.float32, device=dev)
     ops.fog_bias_rows(out, torch.tensor(lens, dtype=torch.int32, device=dev), dtype, 0.5, 0.5,
                       torch.tensor(rec, dtype=torch.int32, device=dev), 0.1)
