@@ -2108,7 +2108,7 @@ namespace {
 // longest tile (dispatched first) can take twice the chip's average share,
 // and a small B*H leaves most CUs without a tile at all.  Each query tile's
 // keys are split S ways, from the longest tile's key tiles over the per-CU
-// share of all key tiles, with at least 4 key tiles per split; 1 when the
+// share of all key tiles, with at least 2 key tiles per split; 1 when the
 // grid alone balances (B=1 H=32 N=8,192 causal: 1,024 workgroups over 256
 // CUs).  Returns S and, in *split_q0, the first position of the split tiles.
 // KESSIE_DENSE_SPLITS > 0 forces the count (tests).
@@ -2142,13 +2142,15 @@ int dense_splits(int B, int H, int N, int window, int causal, int* split_q0) {
   if (longest <= 0 || share <= 0.0) return 1;
   // Each split adds a partial row per query of a split tile (written, then
   // read by the combine), which outweighs the balance gained past a few
-  // splits: on the reference's benchmark (B=1, H=8, causal) the best counts
-  // were 2 at N=4,096-8,192 (longest tile 1.9-3.8 times the share) and 4 at
-  // N=1,024-2,048.
+  // splits: on the reference's benchmark (B=1, H=8, causal; forced counts 1,
+  // 2, 4, 8) the best were 2 where the longest tile is 1.9-3.8 times the
+  // share (N=4,096-8,192 full, N=4,096 W=1,024) and 4 from 5.3 times on
+  // (N=512-2,048, full and W=1,024), down to 2 key tiles per split (N=512:
+  // 22.4 us against 24.1 with 4 tiles per split).
   const double ratio = longest / share;
   if (ratio < 1.5) return 1;
-  int s = min(4, max(2, (int)(ratio / 2.0 + 0.5)));
-  s = min(s, max(1, longest / 4));
+  int s = ratio >= 5.0 ? 4 : 2;
+  s = min(s, max(1, longest / 2));
   s = min(s, min(kt, kMaxSplits));
   return max(s, 1);
 }
