@@ -56,6 +56,24 @@ def test_prefill_chunk_shapes(dev, c, ctx):
     _check(out, ref, torch.bfloat16)
 
 
+@pytest.mark.parametrize("dtype,c", [(torch.bfloat16, 1024), (torch.bfloat16, 1536), (torch.float32, 128),
+                                     (torch.float32, 256)])
+def test_prefill_fresh_prompts_at_the_split_rule_edges(dev, dtype, c):
+    """Fresh prompts (chunk = context, causal, V-fog) where the automatic key
+    split count turns on what is counted: bf16 prompts of 1,024 and 1,536
+    tokens stay unsplit because a causal query tile sees half the context on
+    average, fp32 prompts of 128 and 256 tokens split 2 and 4 ways at four key
+    blocks per split; each against the oracle."""
+    from kessie_amd import ops
+
+    q, pool, table, lens = _case(dev, 1, c, [c], 32, 8, dtype, seed=c + 7)
+    fog = build_fog_weights(c).to(dev)
+    out = ops.fog_prefill(q, pool, table, lens, c, fog_vscale=fog)
+    torch.cuda.synchronize()
+    ref = paged_prefill_ref(q.cpu(), pool.cpu(), table.cpu(), lens.cpu(), fog.cpu())
+    _check(out, ref, dtype)
+
+
 @pytest.mark.parametrize("window", [1, 16, 37, 100, 10000])
 def test_prefill_window(dev, window):
     from kessie_amd import ops
